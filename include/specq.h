@@ -1,0 +1,170 @@
+/*
+ * specq.h -- C ABI of libspecq.so, the gfx950 (MI355X) quantized speculative-decoding
+ * verification kernels.
+ *
+ * Each entry point replaces one launcher of the reference's kernels.py and takes plain
+ * device pointers, element strides and sizes (no framework types).  All launches are
+ * asynchronous on the caller's HIP stream (`stream` is a hipStream_t, NULL = the null
+ * stream); no entry point allocates, frees or synchronizes, so every one of them may be
+ * recorded into a hipGraph.  Strides are in elements of the tensor's own dtype; the
+ * innermost dimension of every tensor must be contiguous (stride 1).
+ *
+ * Plan mode (the reference's USE_PLAN, kernels.py:14-17): when `plan` is non-NULL the
+ * active problem size is read on the device from that int32 buffer at kernel run time and
+ * the grid is sized from the host-side maxima, so one captured graph serves every shape.
+ * Plan values are clamped to the maxima the grid was sized for.  Inactive rows/sequences/
+ * query slots are never written.
+ *
+ * Workspaces: kernels that split a reduction across workgroups need device scratch of at
+ * least the size returned by the matching *_workspace_size() call.  Every workspace starts
+ * with a fixed 256 KiB counter region (SPECQ_WORKSPACE_COUNTER_BYTES) followed by scratch.
+ * The counter region must be zero-filled once when the workspace is created; every kernel
+ * returns the counters it used to zero, so one workspace can serve any sequence of calls,
+ * of any kernel and size, issued in stream order.  Calls that may run concurrently
+ * (different streams) must not share a workspace.
+ *
+ * Return codes: 0 on success, otherwise a negative errno-style code; the message is
+ * available from specq_last_error() (per calling thread).  Arguments are validated before
+ * any HIP call is made.
+ */
+#ifndef SPECQ_H
+#define SPECQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPECQ_OK 0
+#define SPECQ_EIO (-5)       /* HIP launch/runtime error */
+#define SPECQ_EINVAL (-22)   /* invalid argument (null pointer, bad size or stride) */
+#define SPECQ_ENOSPC (-28)   /* workspace missing or too small */
+#define SPECQ_ENOTSUP (-95)  /* valid but unsupported configuration (tile, head_dim, ...) */
+
+#define SPECQ_WORKSPACE_COUNTER_BYTES (256 * 1024)
+
+/* Library ABI version (major * 100 + minor). */
+int specq_version(void);
+
+/* Message describing the last error raised on this thread ("" if none). */
+const char* specq_last_error(void);
+
+/* ---------------------------------------------------------------------------------------
+ * W8A8 GEMM: C[m, n] = fp16( (float(sum_k A[m,k] * W[n,k]) * sa[m]) * sw[n] ),  m < M, n < N
+ * Replaces w8a8_matmul (kernels.py:71-86) and _w8a8_kernel (kernels.py:27-55).
+ *   a        int8 [M, K], row stride lda          (a_q)
+ *   w        int8 [N, K], row stride ldw          (w_q, "W^T" addressing, kernels.py:43)
+ *   sa       fp32 [M] per-token scale;  sw  fp32 [N] per-channel scale
+ *   c        fp16 [M, N], row stride ldc
+ *   grid_m_max  rows the grid is sized for (>= M); 0 means M.  The reference's grid_m_max.
+ *   plan     NULL, or device int32*: plan[0] = active M (kernels.py:35-38)
+ *   block_m  token rows per workgroup: a multiple of 16, at most 320 (the reference's
+ *            BLOCK_M; 16/32/64/128 are its values); 0 = choose from the M staircase.
+ *   block_n  output channels per workgroup: 16, 32 or 64; 0 = auto.  (BLOCK_N)
+ *   num_warps  64-wide waves per workgroup splitting K: 1, 2 or 4 (8 is taken as 4); 0 = 4.
+ *   split_k  workgroups splitting K; 0 = auto.  The INT32 result does not depend on it.
+ * ------------------------------------------------------------------------------------- */
+size_t specq_w8a8_workspace_size(int m_grid, int N, int K, int block_m, int block_n,
+                                 int num_warps, int split_k);
+int specq_w8a8(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
+               const float* sa, const float* sw, void* c, int64_t ldc,
+               int M, int N, int K, int grid_m_max, const int32_t* plan,
+               int block_m, int block_n, int num_warps, int split_k,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * W4A16 GEMM: C[m, n] = fp16( sum_k a[m,k] * fp16(fp16(q[n,k]) * sc[n, k/group]) )
+ * with q the signed int4 weight in [-8, 7] stored as an unsigned nibble with offset 8.
+ * Replaces w4a16_matmul (kernels.py:150-166) and _w4a16_kernel (kernels.py:94-135).
+ *   a        fp16 [M, K], row stride lda
+ *   wq       packed weights, row stride ldq in elements of the layout's storage type:
+ *            layout 0 (reference, kernels.py:89-92, 143-145): uint8 [N, K/2]; byte j of a row
+ *              holds k = j in its low nibble and k = j + K/2 in its high nibble.
+ *            layout 1: int32 [N, K/8]; nibble i (bits 4i..4i+3) of word j holds k = 8j + i.
+ *   sc       fp16 [N, K/group] group scales, row stride ld_sc
+ *   group    K group size: a multiple of 32 (layout 1) or 16 (layout 0) dividing K.
+ *   Other arguments as specq_w8a8.  The fp32 accumulation order depends only on (N, K),
+ *   block_n, num_warps and split_k, never on M, block_m or the plan, so plan-mode and
+ *   eager results are bit-identical for equal tile arguments.
+ * ------------------------------------------------------------------------------------- */
+size_t specq_w4a16_workspace_size(int m_grid, int N, int K, int block_m, int block_n,
+                                  int num_warps, int split_k);
+int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t ldq, int wq_layout,
+                const void* sc, int64_t ld_sc, void* c, int64_t ldc,
+                int M, int N, int K, int group, int grid_m_max, const int32_t* plan,
+                int block_m, int block_n, int num_warps, int split_k,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * INT8 paged-KV verification attention.
+ * Replaces paged_attention (kernels.py:239-262) and _paged_attn_kernel (kernels.py:178-236).
+ *   q        fp16 [B_grid, ql_grid, H, D]   strides s_qb, s_qt, s_qh (d contiguous)
+ *   kc, vc   int8 [pages, PAGE, H_KV, D]    strides s_kp, s_ko, s_kh (shared by kc and vc)
+ *   ks, vs   fp16 or fp32 (scale_fp32 = 0/1) [pages, PAGE, H_KV], strides s_sp, s_so, s_sh
+ *   block_tbl int32 [B_grid, max_pages], row stride s_bt
+ *   ctx_len  int32 [B_grid]; includes the q_len query tokens, which are the last q_len
+ *            positions of each sequence (kernels.py:173, 204)
+ *   out      fp16 like q, strides s_ob, s_ot, s_oh
+ *   n_seqs, q_len  active sequences and query tokens (eager mode)
+ *   QPP      query tokens per program: 1 = decode style, q_len = fused verification
+ *            (rows packed per program = QPP * H/H_KV, at most 64)
+ *   plan     NULL, or device int32*: plan[0] = n_seqs, plan[1] = q_len (the reference passes
+ *            plan[1:] of its [M, B, q_len] buffer, bench_graphs.py:58)
+ *   D must be 64 or 128; PAGE a multiple of 16.  sm_scale is the softmax scale (1/sqrt(D)).
+ *   The KV split across workgroups is a fixed function of token position (512 tokens per
+ *   split), so results do not depend on B, QPP or the plan.
+ * ------------------------------------------------------------------------------------- */
+size_t specq_paged_attn_workspace_size(int B_grid, int H, int H_KV, int ql_grid, int QPP,
+                                       int max_pages, int PAGE);
+int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64_t s_qh,
+                     const int8_t* kc, const int8_t* vc, int64_t s_kp, int64_t s_ko, int64_t s_kh,
+                     const void* ks, const void* vs, int64_t s_sp, int64_t s_so, int64_t s_sh,
+                     int scale_fp32, const int32_t* block_tbl, int64_t s_bt, int max_pages,
+                     const int32_t* ctx_len, void* out, int64_t s_ob, int64_t s_ot, int64_t s_oh,
+                     int B_grid, int n_seqs, int q_len, int ql_grid, int H, int H_KV, int D,
+                     int PAGE, int QPP, float sm_scale, const int32_t* plan,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Elementwise steps around the GEMMs of a verification layer.
+ * specq_silu_mul: h[m, n] = fp16( silu(float(gate[m,n])) * float(up[m,n]) ), m < M.
+ *   No reference counterpart (the reference's graph stack has no MLP activation,
+ *   bench_graphs.py:62); it is the SiLU*mul step of the gate/up -> down chain.
+ * specq_quantize_act_int8: per-token symmetric INT8 quantisation of fp16 rows,
+ *   s[m] = max(amax_k |x[m,k]|, 1e-8) / 127,  q[m,k] = clamp(rne(x[m,k] / s[m]), -127, 127).
+ *   Replaces quantize_act_int8 (kernels.py:58-62) on the device.
+ * specq_silu_mul_quant_int8: the two above fused; feeds the next W8A8 GEMM directly.
+ * In plan mode plan[0] is the active M.
+ * ------------------------------------------------------------------------------------- */
+int specq_silu_mul(const void* gate, int64_t ld_gate, const void* up, int64_t ld_up,
+                   void* h, int64_t ld_h, int M, int N, int grid_m_max, const int32_t* plan,
+                   void* stream);
+int specq_quantize_act_int8(const void* x, int64_t ldx, int8_t* q, int64_t ldq, float* s,
+                            int M, int K, int grid_m_max, const int32_t* plan, void* stream);
+int specq_silu_mul_quant_int8(const void* gate, int64_t ld_gate, const void* up, int64_t ld_up,
+                              int8_t* q, int64_t ldq, float* s, int M, int N, int grid_m_max,
+                              const int32_t* plan, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Resource usage of the kernel a call with these arguments would launch (the reference's
+ * compiled-kernel metadata ck.n_regs / ck.n_spills / ck.metadata.shared, regs.py:29-32).
+ * kind: 0 = W8A8, 1 = W4A16 (layout in `variant`), 2 = paged attention (D in `variant`).
+ * ------------------------------------------------------------------------------------- */
+typedef struct specq_kernel_attrs {
+  char name[160];          /* kernel symbol */
+  int num_regs;            /* VGPRs (architected + accumulation) per lane */
+  int lds_bytes;           /* LDS per workgroup (static + dynamic at these arguments) */
+  int scratch_bytes;       /* private scratch per lane (register spills) */
+  int threads;             /* workgroup size at these arguments */
+  int grid;                /* workgroups launched at these arguments */
+  int block_m, block_n, num_warps, split_k;  /* resolved tile configuration */
+} specq_kernel_attrs;
+int specq_kernel_attrs_query(int kind, int variant, int m_grid, int N, int K, int block_m,
+                             int block_n, int num_warps, int split_k, specq_kernel_attrs* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SPECQ_H */

@@ -1,0 +1,50 @@
+// Host-side helpers shared by the C-ABI translation units: error reporting, argument checks.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/specq.h"
+
+namespace specq {
+
+void set_error(const char* fmt, ...);
+void clear_error();
+
+inline int fail(int code, const char* what) {
+  set_error("%s", what);
+  return code;
+}
+
+#define SPECQ_REQUIRE(cond, code, ...) \
+  do {                                 \
+    if (!(cond)) {                     \
+      ::specq::set_error(__VA_ARGS__); \
+      return code;                     \
+    }                                  \
+  } while (0)
+
+// Every workspace starts with a fixed counter region (zero between calls), then scratch.
+constexpr size_t kCounterBytes = 256 * 1024;
+constexpr int64_t kMaxCounters = kCounterBytes / 4;
+
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+inline int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Largest power of two <= 16 dividing every value (pointer addresses and element counts).
+inline int common_vec(std::initializer_list<uint64_t> vals) {
+  int v = 16;
+  for (uint64_t x : vals)
+    while (v > 1 && (x % (uint64_t)v) != 0) v >>= 1;
+  return v;
+}
+
+int launch(const void* fn, int grid, int threads, size_t lds, hipStream_t stream, void* params);
+
+// Number of CUs of the current device (cached per device).
+int device_cus();
+
+}  // namespace specq

@@ -1,0 +1,115 @@
+// Elementwise steps that sit between the GEMMs of a verification layer, plus their C ABI:
+//   silu_mul            h = fp16(silu(gate) * up)                        (fp32 math)
+//   quantize_act_int8   per-token symmetric INT8 (kernels.py:58-62 on the device)
+//   silu_mul_quant_int8 the two fused: the fp16 h is formed in registers and quantised
+//                       without a round trip through HBM.
+// One workgroup per token row; rows at or beyond the active M (plan[0] in plan mode) exit.
+// The quantiser reproduces the reference formula bit for bit: amax in fp32,
+// s = max(amax, 1e-8) / 127 (IEEE division), q = clamp(rne(x / s), -127, 127).
+#include "api_common.hpp"
+#include "common.hpp"
+
+namespace specq {
+
+struct EltParams {
+  const _Float16* x; int64_t ldx;    // quantize input, or gate
+  const _Float16* up; int64_t ld_up; // silu_mul only
+  _Float16* h; int64_t ldh;          // silu_mul output
+  int8_t* q; int64_t ldq; float* s;  // quantize outputs
+  const int32_t* plan;
+  int M, N, m_grid;
+};
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+template <int MODE>  // 0 = silu_mul, 1 = quantize, 2 = silu_mul + quantize
+__global__ __launch_bounds__(256) void elt_kernel(EltParams p) {
+  int M = p.M;
+  if (p.plan != nullptr) M = min(max(p.plan[0], 0), p.m_grid);
+  const int m = blockIdx.x;
+  if (m >= uniform(M)) return;
+  const _Float16* xr = p.x + (int64_t)m * p.ldx;
+  const _Float16* ur = (MODE != 1) ? p.up + (int64_t)m * p.ld_up : nullptr;
+  const int N = p.N;
+
+  auto value = [&](int k) -> _Float16 {
+    if constexpr (MODE == 1) return xr[k];
+    else return (_Float16)(silu_f((float)xr[k]) * (float)ur[k]);
+  };
+
+  if constexpr (MODE == 0) {
+    _Float16* hr = p.h + (int64_t)m * p.ldh;
+    for (int k = threadIdx.x; k < N; k += blockDim.x) hr[k] = value(k);
+    return;
+  } else {
+    __shared__ float red[256 / kWave];
+    float amax = 0.f;
+    for (int k = threadIdx.x; k < N; k += blockDim.x) amax = fmaxf(amax, fabsf((float)value(k)));
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    if (lane_id() == 0) red[wave_id()] = amax;
+    __syncthreads();
+    amax = red[0];
+    for (int i = 1; i < (int)(blockDim.x / kWave); ++i) amax = fmaxf(amax, red[i]);
+    const float s = fmaxf(amax, 1e-8f) / 127.0f;
+    int8_t* qr = p.q + (int64_t)m * p.ldq;
+    for (int k = threadIdx.x; k < N; k += blockDim.x) {
+      float v = rintf((float)value(k) / s);
+      v = fminf(fmaxf(v, -127.f), 127.f);
+      qr[k] = (int8_t)v;
+    }
+    if (threadIdx.x == 0) p.s[m] = s;
+  }
+}
+
+static int launch_elt(int mode, EltParams& p, hipStream_t stream) {
+  const int m_grid = p.m_grid;
+  if (m_grid == 0) return SPECQ_OK;
+  const void* fn = mode == 0 ? reinterpret_cast<const void*>(&elt_kernel<0>)
+                 : mode == 1 ? reinterpret_cast<const void*>(&elt_kernel<1>)
+                             : reinterpret_cast<const void*>(&elt_kernel<2>);
+  return launch(fn, m_grid, 256, 0, stream, &p);
+}
+
+}  // namespace specq
+
+using namespace specq;
+
+extern "C" int specq_silu_mul(const void* gate, int64_t ld_gate, const void* up, int64_t ld_up, void* h,
+                              int64_t ld_h, int M, int N, int grid_m_max, const int32_t* plan, void* stream) {
+  clear_error();
+  SPECQ_REQUIRE(gate && up && h, SPECQ_EINVAL, "silu_mul: null tensor pointer");
+  SPECQ_REQUIRE(M >= 0 && N > 0 && ld_gate >= N && ld_up >= N && ld_h >= N, SPECQ_EINVAL,
+                "silu_mul: bad sizes or strides");
+  SPECQ_REQUIRE(grid_m_max == 0 || grid_m_max >= M, SPECQ_EINVAL, "silu_mul: grid_m_max < M");
+  EltParams p = {};
+  p.x = (const _Float16*)gate; p.ldx = ld_gate; p.up = (const _Float16*)up; p.ld_up = ld_up;
+  p.h = (_Float16*)h; p.ldh = ld_h; p.plan = plan; p.M = M; p.N = N; p.m_grid = grid_m_max > 0 ? grid_m_max : M;
+  return launch_elt(0, p, (hipStream_t)stream);
+}
+
+extern "C" int specq_quantize_act_int8(const void* x, int64_t ldx, int8_t* q, int64_t ldq, float* s, int M, int K,
+                                       int grid_m_max, const int32_t* plan, void* stream) {
+  clear_error();
+  SPECQ_REQUIRE(x && q && s, SPECQ_EINVAL, "quantize_act_int8: null tensor pointer");
+  SPECQ_REQUIRE(M >= 0 && K > 0 && ldx >= K && ldq >= K, SPECQ_EINVAL, "quantize_act_int8: bad sizes or strides");
+  SPECQ_REQUIRE(grid_m_max == 0 || grid_m_max >= M, SPECQ_EINVAL, "quantize_act_int8: grid_m_max < M");
+  EltParams p = {};
+  p.x = (const _Float16*)x; p.ldx = ldx; p.q = q; p.ldq = ldq; p.s = s; p.plan = plan;
+  p.M = M; p.N = K; p.m_grid = grid_m_max > 0 ? grid_m_max : M;
+  return launch_elt(1, p, (hipStream_t)stream);
+}
+
+extern "C" int specq_silu_mul_quant_int8(const void* gate, int64_t ld_gate, const void* up, int64_t ld_up, int8_t* q,
+                                         int64_t ldq, float* s, int M, int N, int grid_m_max, const int32_t* plan,
+                                         void* stream) {
+  clear_error();
+  SPECQ_REQUIRE(gate && up && q && s, SPECQ_EINVAL, "silu_mul_quant_int8: null tensor pointer");
+  SPECQ_REQUIRE(M >= 0 && N > 0 && ld_gate >= N && ld_up >= N && ldq >= N, SPECQ_EINVAL,
+                "silu_mul_quant_int8: bad sizes or strides");
+  SPECQ_REQUIRE(grid_m_max == 0 || grid_m_max >= M, SPECQ_EINVAL, "silu_mul_quant_int8: grid_m_max < M");
+  EltParams p = {};
+  p.x = (const _Float16*)gate; p.ldx = ld_gate; p.up = (const _Float16*)up; p.ld_up = ld_up;
+  p.q = q; p.ldq = ldq; p.s = s; p.plan = plan; p.M = M; p.N = N; p.m_grid = grid_m_max > 0 ? grid_m_max : M;
+  return launch_elt(2, p, (hipStream_t)stream);
+}

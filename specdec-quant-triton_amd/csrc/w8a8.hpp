@@ -1,0 +1,218 @@
+// W8A8 GEMM for gfx950:  C[m, n] = fp16( (float(sum_k A[m,k] * W[n,k]) * sa[m]) * sw[n] )
+//
+// Follows the arithmetic of the reference Triton kernel (kernels.py:27-55): INT8 x INT8
+// products accumulated exactly in INT32, then the per-token and per-channel scales applied
+// left to right in fp32, then one RNE cast to fp16.  The schedule is MI355X-specific:
+//
+//  * Weight-streaming orientation.  W (the large operand) is the MFMA A-operand and is loaded
+//    straight from HBM into VGPRs, 16 contiguous bytes per lane per 64-wide K step, so each
+//    weight byte crosses the memory system once per M-chunk.  The activations (small, L2
+//    resident) are the MFMA B-operand.  v_mfma_i32_16x16x64_i8 produces a 16(n) x 16(m) tile.
+//  * A workgroup owns BN = RW*16 output channels and one M-chunk of BM = MT*16 tokens, which
+//    it keeps in INT32 accumulators for its whole K range.  With BLOCK_M >= M the weights are
+//    read exactly once; smaller BLOCK_M re-reads them once per M-chunk like the reference.
+//  * The waves of a workgroup split its K range (interleaved 64-byte steps, so the waves of
+//    one workgroup read adjacent memory), then reduce their accumulators through LDS.
+//  * To fill 256 CUs the K range is further split across workgroups (split-K).  INT32 sums are
+//    order independent, so the split is exact by construction: each split writes its INT32
+//    partial tile, and the last workgroup to arrive (agent-scope atomic counter) sums the
+//    partials, applies the epilogue and resets the counter, so the workspace needs no memset
+//    between calls and the kernel is legal inside a captured graph.
+//  * Plan mode: the active M is read from a device int32 (plan[0]) and clamped to the rows
+//    the grid was sized for; M-chunks at or beyond it exit before touching memory, so one
+//    graph captured at the maximum grid replays every M and never writes rows >= M.
+#pragma once
+#include "common.hpp"
+
+namespace specq {
+
+struct W8A8Params {
+  const int8_t* A; int64_t lda;
+  const int8_t* W; int64_t ldw;
+  const float* sa; const float* sw;
+  __half* C; int64_t ldc;
+  const int32_t* plan;
+  int M, N, K;
+  int m_grid;          // rows the grid covers (grid_m_max, or M)
+  int n_tiles, m_chunks, splits;
+  int k_range;         // K bytes per split, a multiple of 64
+  int32_t* partials;   // [m_chunks][n_tiles][splits][BM*BN] when splits > 1
+  int32_t* counters;   // [m_chunks][n_tiles], zero between calls
+  int vec_store;       // 1 when C rows allow 8-byte aligned stores of 4 halves
+};
+
+constexpr int kW8A8Pad = 4;  // int32 padding per LDS row
+
+template <int MT>
+struct W8A8Unroll { static constexpr int value = MT <= 2 ? 4 : (MT <= 6 ? 2 : 1); };
+
+template <int MT, int RW, int VEC>
+__device__ __forceinline__ void w8a8_load_step(const int8_t* const (&wrow)[RW], const int8_t* const (&arow)[MT],
+                                               int koff, int kend, v4i (&wf)[RW], v4i (&af)[MT]) {
+#pragma unroll
+  for (int i = 0; i < RW; ++i) wf[i] = load16_masked<VEC>(wrow[i], koff, kend);
+#pragma unroll
+  for (int j = 0; j < MT; ++j) af[j] = load16_masked<VEC>(arow[j], koff, kend);
+}
+
+template <int MT, int RW>
+__device__ __forceinline__ void w8a8_mma_step(const v4i (&wf)[RW], const v4i (&af)[MT], v4i (&acc)[RW][MT]) {
+#pragma unroll
+  for (int i = 0; i < RW; ++i)
+#pragma unroll
+    for (int j = 0; j < MT; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[i], af[j], acc[i][j], 0, 0, 0);
+}
+
+// Epilogue for 4 consecutive output channels of one token row.
+__device__ __forceinline__ void w8a8_store4(const W8A8Params& p, int m, int n, v4i s) {
+  const float a = p.sa[m];
+  __half* dst = p.C + (int64_t)m * p.ldc + n;
+  float v[4] = {(float)s.x, (float)s.y, (float)s.z, (float)s.w};
+  if (p.vec_store && n + 3 < p.N) {
+    v4f w = *reinterpret_cast<const v4f*>(p.sw + n);
+    _Float16 h0 = (_Float16)((v[0] * a) * w.x), h1 = (_Float16)((v[1] * a) * w.y);
+    _Float16 h2 = (_Float16)((v[2] * a) * w.z), h3 = (_Float16)((v[3] * a) * w.w);
+    typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+    v4h o = {h0, h1, h2, h3};
+    *reinterpret_cast<v4h*>(dst) = o;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (n + i < p.N) dst[i] = __float2half_rn((v[i] * a) * p.sw[n + i]);
+  }
+}
+
+template <int MT, int RW, int VEC>
+__global__ __launch_bounds__(256) void w8a8_kernel(W8A8Params p) {
+  constexpr int BM = MT * 16, BN = RW * 16, U = W8A8Unroll<MT>::value;
+  constexpr int LDW = BN + kW8A8Pad;  // LDS row pitch in int32
+  extern __shared__ int32_t smem[];
+
+  const int nw = blockDim.x / kWave;
+  int id = blockIdx.x;
+  const int mc = id % p.m_chunks; id /= p.m_chunks;
+  const int split = id % p.splits;
+  const int tile = id / p.splits;
+
+  int M = p.M;
+  if (p.plan != nullptr) M = min(max(p.plan[0], 0), p.m_grid);
+  M = uniform(M);
+  const int m0 = mc * BM;
+  if (m0 >= M) return;  // plan guard: inactive M-chunk, nothing read or written
+
+  const int n0 = tile * BN;
+  const int kb = split * p.k_range;
+  const int ke = min(p.K, kb + p.k_range);
+  const int lane = lane_id(), w = wave_id(), g = lane >> 4, r = lane & 15;
+
+  const int8_t* wrow[RW];
+  const int8_t* arow[MT];
+#pragma unroll
+  for (int i = 0; i < RW; ++i) wrow[i] = p.W + (int64_t)min(n0 + i * 16 + r, p.N - 1) * p.ldw;
+#pragma unroll
+  for (int j = 0; j < MT; ++j) arow[j] = p.A + (int64_t)min(m0 + j * 16 + r, M - 1) * p.lda;
+
+  v4i acc[RW][MT];
+#pragma unroll
+  for (int i = 0; i < RW; ++i)
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  // This wave's K steps: kb + (w + t*nw)*64 for t = 0..nsteps-1, batched U at a time and
+  // double-buffered in registers (loads of batch b+1 are in flight during batch b's MFMAs).
+  const int stride = nw * 64;
+  const int k_first = kb + w * 64 + g * 16;
+  const int nsteps = (kb + w * 64 < ke) ? (ke - (kb + w * 64) + stride - 1) / stride : 0;
+  const int nbatch = (nsteps + U - 1) / U;
+
+  v4i wa[U][RW], aa[U][MT], wb[U][RW], ab[U][MT];
+  auto load_batch = [&](int b, v4i (&wv)[U][RW], v4i (&av)[U][MT]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      w8a8_load_step<MT, RW, VEC>(wrow, arow, k_first + (b * U + u) * stride, ke, wv[u], av[u]);
+  };
+  auto mma_batch = [&](v4i (&wv)[U][RW], v4i (&av)[U][MT]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) w8a8_mma_step<MT, RW>(wv[u], av[u], acc);
+  };
+
+  if (nbatch > 0) load_batch(0, wa, aa);
+  for (int b = 0; b < nbatch; b += 2) {
+    if (b + 1 < nbatch) load_batch(b + 1, wb, ab);
+    mma_batch(wa, aa);
+    if (b + 2 < nbatch) load_batch(b + 2, wa, aa);
+    if (b + 1 < nbatch) mma_batch(wb, ab);
+  }
+
+  // Cross-wave reduction through one LDS slice [BM][LDW]: waves nw-1 .. 1 each deposit their
+  // accumulators in turn and wave 0 adds them into its registers.  Lane (r, g) of 16x16 block
+  // (i, j) holds channels n = i*16 + 4g + {0..3} of token m = j*16 + r.
+  for (int src = nw - 1; src >= 1; --src) {
+    if (w == src) {
+#pragma unroll
+      for (int i = 0; i < RW; ++i)
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+          *reinterpret_cast<v4i*>(smem + (j * 16 + r) * LDW + i * 16 + 4 * g) = acc[i][j];
+    }
+    __syncthreads();
+    if (w == 0) {
+#pragma unroll
+      for (int i = 0; i < RW; ++i)
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+          acc[i][j] += *reinterpret_cast<const v4i*>(smem + (j * 16 + r) * LDW + i * 16 + 4 * g);
+    }
+    __syncthreads();
+  }
+
+  const int cidx = mc * p.n_tiles + tile;
+  if (p.splits == 1) {
+    if (w == 0) {
+#pragma unroll
+      for (int i = 0; i < RW; ++i)
+#pragma unroll
+        for (int j = 0; j < MT; ++j) {
+          const int m = m0 + j * 16 + r, n = n0 + i * 16 + 4 * g;
+          if (m < M && n < p.N) w8a8_store4(p, m, n, acc[i][j]);
+        }
+    }
+    return;
+  }
+
+  // Split-K fix-up: every split stores its INT32 tile ([BM][BN], row = token); the last
+  // workgroup of this (M-chunk, N-tile) to arrive sums all splits and applies the epilogue.
+  int32_t* base = p.partials + (int64_t)cidx * p.splits * (BM * BN);
+  if (w == 0) {
+    int32_t* mine = base + (int64_t)split * (BM * BN);
+#pragma unroll
+    for (int i = 0; i < RW; ++i)
+#pragma unroll
+      for (int j = 0; j < MT; ++j)
+        *reinterpret_cast<v4i*>(mine + (j * 16 + r) * BN + i * 16 + 4 * g) = acc[i][j];
+  }
+  __shared__ int s_last;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = atomicAdd(p.counters + cidx, 1);
+    s_last = (prev == p.splits - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  constexpr int QUADS = BM * BN / 4;
+  for (int q = threadIdx.x; q < QUADS; q += blockDim.x) {
+    const int ml = q / (BN / 4), nl = (q % (BN / 4)) * 4;
+    const int m = m0 + ml, n = n0 + nl;
+    if (m >= M || n >= p.N) continue;
+    v4i s = {0, 0, 0, 0};
+    for (int sp = 0; sp < p.splits; ++sp)
+      s += __builtin_nontemporal_load(reinterpret_cast<const v4i*>(base + (int64_t)sp * (BM * BN) + ml * BN + nl));
+    w8a8_store4(p, m, n, s);
+  }
+  if (threadIdx.x == 0) atomicExch(p.counters + cidx, 0);
+}
+
+}  // namespace specq

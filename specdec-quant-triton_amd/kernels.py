@@ -1,0 +1,442 @@
+"""Quantized speculative-decoding verification kernels for MI355X (gfx950).
+
+Drop-in counterpart of the reference's kernels.py: the same public names, signatures,
+defaults and return values, so correctness and benchmark scripts written against the
+reference run unchanged (`from kernels import *`).  The kernels themselves are hand-written
+HIP for gfx950 in csrc/, reached through the C ABI of libspecq.so (include/specq.h):
+
+  w8a8_matmul      INT8 x INT8 -> INT32 MFMA GEMM, per-token x per-channel scale epilogue
+                   (reference kernels.py:27-55, 71-86)
+  w4a16_matmul     packed-INT4 (group scales) x FP16 GEMM, dequantised once per weight
+                   element and fed to FP16 MFMA (reference kernels.py:94-135, 150-166)
+  paged_attention  INT8 paged-KV verification attention, GQA x (k+1) rows packed per
+                   program, QPP=1 (decode style) or QPP=q_len (fused)
+                   (reference kernels.py:178-236, 239-262)
+
+Every launcher takes `plan` (an int32 device tensor read by the kernel at run time) and a
+fixed grid size, so a single captured graph replays every (B, k) (reference kernels.py:14-17).
+Launches go to torch's current stream and never synchronise or allocate (except the
+optional output allocation and the first growth of the shared workspace).
+
+The host-side helpers (quantizers, INT4 packer, paged-KV generator, dense attention
+reference) restate the reference formulas in torch and run on any device.
+
+Differences a caller may notice:
+  * BLOCK_K and num_stages are accepted and ignored (the MFMA K step and register
+    pipelining are fixed per kernel).  BLOCK_M=None (or 0) picks the tile from the measured
+    M staircase.  W8A8 BLOCK_N is 16/32/64 channels per workgroup (larger values are taken
+    as 64); W4A16 BLOCK_N is 64 or 128.
+  * `ck` is a KernelInfo with n_regs / n_spills / metadata.shared like Triton's compiled
+    kernel, plus the resolved tile configuration.
+  * w4a16_matmul also accepts the int32 "8 nibbles per word along K" packing.
+"""
+from __future__ import annotations
+
+import math
+import os
+import sys
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+if _HERE not in sys.path:
+    sys.path.insert(0, _HERE)
+
+from specq import _lib  # noqa: E402
+from specq import workspace as _ws  # noqa: E402
+from specq.tiles import pick_block_m  # noqa: E402
+
+__all__ = [
+    "w8a8_matmul", "w4a16_matmul", "paged_attention",
+    "quantize_act_int8", "quantize_weight_int8", "quantize_weight_int4",
+    "make_paged_kv", "paged_attention_ref",
+    "silu_mul", "quantize_act_int8_gpu", "silu_mul_quant_int8",
+    "pack_int4_i32", "KernelInfo",
+]
+
+
+# ----------------------------------------------------------------------------------------
+# Kernel bookkeeping: the reference's `ck` object and the JIT-cache stand-ins read by
+# correctness.py:18-24 (n_compiled).
+# ----------------------------------------------------------------------------------------
+class _Meta:
+    def __init__(self, shared: int):
+        self.shared = shared
+
+    def __getitem__(self, key):
+        return getattr(self, key)
+
+
+class KernelInfo:
+    """Resource usage of the kernel a call launched (lazy: queried on first access)."""
+
+    def __init__(self, kind: int, variant: int, m_grid: int, N: int, K: int, block_m: int, block_n: int,
+                 num_warps: int, split_k: int):
+        self._key = (kind, variant, m_grid, N, K, block_m, block_n, num_warps, split_k)
+        self._attrs = None
+
+    def _get(self):
+        if self._attrs is None:
+            self._attrs = _attrs_cached(*self._key)
+        return self._attrs
+
+    @property
+    def name(self) -> str:
+        return self._get().name.decode()
+
+    @property
+    def n_regs(self) -> int:
+        return self._get().num_regs
+
+    @property
+    def n_spills(self) -> int:
+        return self._get().scratch_bytes // 4
+
+    @property
+    def metadata(self) -> _Meta:
+        return _Meta(self._get().lds_bytes)
+
+    @property
+    def config(self) -> dict:
+        a = self._get()
+        return dict(block_m=a.block_m, block_n=a.block_n, num_warps=a.num_warps, split_k=a.split_k,
+                    threads=a.threads, grid=a.grid)
+
+    def __repr__(self):
+        return f"KernelInfo({self.name}, regs={self.n_regs}, spills={self.n_spills}, lds={self.metadata.shared})"
+
+
+_ATTRS: dict = {}
+
+
+def _attrs_cached(*key):
+    a = _ATTRS.get(key)
+    if a is None:
+        a = _ATTRS[key] = _lib.kernel_attrs(*key)
+    return a
+
+
+class _KernelRegistry:
+    """Stand-in for a Triton JITFunction's cache: counts the distinct binaries launched."""
+
+    def __init__(self, name: str):
+        self.__name__ = name
+        self.device_caches: dict = {}
+
+    def _note(self, device_index: int, key) -> None:
+        self.device_caches.setdefault(device_index, (set(),))[0].add(key)
+
+    @property
+    def cache(self) -> dict:
+        return {d: v[0] for d, v in self.device_caches.items()}
+
+
+_w8a8_kernel = _KernelRegistry("_w8a8_kernel")
+_w4a16_kernel = _KernelRegistry("_w4a16_kernel")
+_paged_attn_kernel = _KernelRegistry("_paged_attn_kernel")
+
+
+def _stream_ptr(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+def _require_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t.device.type != "cuda":
+            raise RuntimeError(f"specq kernels run on the GPU only; got a {t.device} tensor")
+
+
+def _rowmajor(t: torch.Tensor) -> torch.Tensor:
+    """2-D view with a unit inner stride (copies only when the inner stride is not 1)."""
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _plan_ptr(plan) -> int:
+    if plan is None:
+        return 0
+    if plan.dtype != torch.int32 or plan.device.type != "cuda":
+        raise RuntimeError("plan must be an int32 device tensor")
+    return plan.data_ptr()
+
+
+# ----------------------------------------------------------------------------------------
+# W8A8
+# ----------------------------------------------------------------------------------------
+def _w8a8_block_n(block_n) -> int:
+    if not block_n:
+        return 0
+    return 16 if block_n <= 16 else (32 if block_n <= 32 else 64)
+
+
+def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=64, BLOCK_K=128,
+                num_warps=4, num_stages=3, plan=None, grid_m_max=None, split_k=0, workspace=None):
+    """C[M, N] = fp16((int32(a_q @ w_q.T) * sa[:, None]) * sw[None, :]).  Returns (out, ck).
+
+    a_q int8 [M, K]; w_q int8 [N, K]; sa fp32 [M]; sw fp32 [N].  With `plan`, M is read from
+    plan[0] on the device and the grid covers grid_m_max rows (reference kernels.py:71-86).
+    """
+    _require_gpu(a_q, w_q, sa, sw)
+    if a_q.dtype != torch.int8 or w_q.dtype != torch.int8:
+        raise RuntimeError("w8a8_matmul expects int8 activations and weights")
+    M, K = a_q.shape
+    N = w_q.shape[0]
+    if w_q.shape[1] != K:
+        raise RuntimeError(f"w8a8_matmul: K mismatch {a_q.shape} vs {w_q.shape}")
+    a_q, w_q = _rowmajor(a_q), _rowmajor(w_q)
+    sa = sa.float().contiguous()
+    sw = sw.float().contiguous()
+    if out is None:
+        out = torch.empty((M, N), device=a_q.device, dtype=torch.float16)
+    if out.dtype != torch.float16 or out.stride(-1) != 1:
+        raise RuntimeError("w8a8_matmul: out must be fp16 with unit inner stride")
+    m_grid = int(grid_m_max) if grid_m_max is not None else M
+    bm = BLOCK_M if BLOCK_M else pick_block_m("w8a8", m_grid, N, K)
+    bn = _w8a8_block_n(BLOCK_N)
+    nw = int(num_warps) if num_warps else 4
+    ws = workspace or _ws.shared(a_q.device)
+    need = _lib.lib().specq_w8a8_workspace_size(m_grid, N, K, bm, bn, nw, split_k)
+    wptr, wbytes = ws.ensure(need)
+    _lib.call("specq_w8a8", a_q.data_ptr(), a_q.stride(0), w_q.data_ptr(), w_q.stride(0),
+              sa.data_ptr(), sw.data_ptr(), out.data_ptr(), out.stride(0),
+              M, N, K, int(grid_m_max or 0), _plan_ptr(plan), bm, bn, nw, split_k,
+              wptr, wbytes, _stream_ptr(a_q))
+    _w8a8_kernel._note(a_q.device.index or 0, (bm, bn, nw))
+    return out, KernelInfo(0, 0, m_grid, N, K, bm, bn, nw, split_k)
+
+
+def quantize_act_int8(x):
+    """Dynamic per-token symmetric INT8 quantisation (reference kernels.py:58-62)."""
+    s = x.abs().amax(dim=-1).float().clamp(min=1e-8) / 127.0
+    q = torch.round(x.float() / s[:, None]).clamp(-127, 127).to(torch.int8)
+    return q, s
+
+
+def quantize_weight_int8(w):
+    """Per-output-channel symmetric INT8 quantisation (reference kernels.py:65-68)."""
+    s = w.abs().amax(dim=-1).float().clamp(min=1e-8) / 127.0
+    q = torch.round(w.float() / s[:, None]).clamp(-127, 127).to(torch.int8)
+    return q, s
+
+
+# ----------------------------------------------------------------------------------------
+# W4A16
+# ----------------------------------------------------------------------------------------
+def quantize_weight_int4(w, group=128):
+    """Group-wise symmetric INT4 (reference kernels.py:138-147).
+
+    Returns (packed uint8 [N, K/2], scales fp16 [N, K/group], dequantised fp16 [N, K]).
+    Byte j of a packed row holds k = j (low nibble) and k = j + K/2 (high nibble), each as
+    q + 8 with q in [-8, 7].
+    """
+    N, K = w.shape
+    assert K % 2 == 0 and (K // 2) % group == 0
+    wg = w.float().reshape(N, K // group, group)
+    sc = wg.abs().amax(-1).clamp(min=1e-8) / 7.0
+    q = torch.round(wg / sc[..., None]).clamp(-8, 7).reshape(N, K).to(torch.int16) + 8
+    half = K // 2
+    packed = (q[:, :half] | (q[:, half:] << 4)).to(torch.uint8).contiguous()
+    deq = ((q - 8).float().reshape(N, K // group, group) * sc[..., None]).reshape(N, K)
+    return packed, sc.to(torch.float16).contiguous(), deq.to(torch.float16)
+
+
+def pack_int4_i32(q_unsigned):
+    """Pack unsigned nibbles [N, K] (values 0..15) as int32 [N, K/8]: nibble i of word j = k 8j+i."""
+    N, K = q_unsigned.shape
+    assert K % 8 == 0
+    v = q_unsigned.to(torch.int64).reshape(N, K // 8, 8)
+    shifts = torch.arange(0, 32, 4, device=v.device, dtype=torch.int64)
+    word = (v << shifts).sum(-1)
+    word = torch.where(word >= 2 ** 31, word - 2 ** 32, word)
+    return word.to(torch.int32).contiguous()
+
+
+def w4a16_matmul(a, wp, sc, group=128, out=None, BLOCK_M=16, BLOCK_N=64, BLOCK_K=64,
+                 num_warps=4, num_stages=3, plan=None, grid_m_max=None, split_k=0, workspace=None):
+    """C[M, N] = fp16(a @ dequant(wp, sc).T) (reference kernels.py:150-166).  Returns (out, ck).
+
+    a fp16 [M, K].  wp is uint8 [N, K/2] (reference packing) or int32 [N, K/8] (8 nibbles per
+    word along K).  sc fp16 [N, K/group].
+    """
+    _require_gpu(a, wp, sc)
+    assert BLOCK_K <= group and group % BLOCK_K == 0
+    M, K = a.shape
+    N = wp.shape[0]
+    if wp.dtype == torch.uint8:
+        layout = 0
+        if wp.shape[1] * 2 != K:
+            raise RuntimeError(f"w4a16_matmul: packed uint8 weights {tuple(wp.shape)} do not match K={K}")
+    elif wp.dtype == torch.int32:
+        layout = 1
+        if wp.shape[1] * 8 != K:
+            raise RuntimeError(f"w4a16_matmul: packed int32 weights {tuple(wp.shape)} do not match K={K}")
+    else:
+        raise RuntimeError("w4a16_matmul: wp must be uint8 [N, K/2] or int32 [N, K/8]")
+    if a.dtype != torch.float16 or sc.dtype != torch.float16:
+        raise RuntimeError("w4a16_matmul expects fp16 activations and fp16 scales")
+    a, wp, sc = _rowmajor(a), _rowmajor(wp), _rowmajor(sc)
+    if a.data_ptr() % 16 or a.stride(0) % 8:
+        a = a.contiguous() if a.data_ptr() % 16 == 0 else a.clone()
+    if out is None:
+        out = torch.empty((M, N), device=a.device, dtype=torch.float16)
+    if out.dtype != torch.float16 or out.stride(-1) != 1:
+        raise RuntimeError("w4a16_matmul: out must be fp16 with unit inner stride")
+    m_grid = int(grid_m_max) if grid_m_max is not None else M
+    bm = BLOCK_M if BLOCK_M else pick_block_m("w4a16", m_grid, N, K)
+    bn = 0 if not BLOCK_N else (64 if BLOCK_N <= 64 else 128)
+    ws = workspace or _ws.shared(a.device)
+    need = _lib.lib().specq_w4a16_workspace_size(m_grid, N, K, bm, bn, 4, split_k)
+    wptr, wbytes = ws.ensure(need)
+    _lib.call("specq_w4a16", a.data_ptr(), a.stride(0), wp.data_ptr(), wp.stride(0), layout,
+              sc.data_ptr(), sc.stride(0), out.data_ptr(), out.stride(0),
+              M, N, K, int(group), int(grid_m_max or 0), _plan_ptr(plan), bm, bn, 4, split_k,
+              wptr, wbytes, _stream_ptr(a))
+    _w4a16_kernel._note(a.device.index or 0, (bm, bn, layout))
+    return out, KernelInfo(1, layout, m_grid, N, K, bm, bn, 4, split_k)
+
+
+# ----------------------------------------------------------------------------------------
+# Paged verification attention
+# ----------------------------------------------------------------------------------------
+def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len, QPP=None, BLOCK_N=64,
+                    num_warps=4, num_stages=2, plan=None, n_seqs=None, out=None, workspace=None):
+    """Verification attention over an INT8 paged KV cache (reference kernels.py:239-262).
+
+    q fp16 [B, QLMAX, H, D]; kc/vc int8 [pages, PAGE, H_KV, D]; ks/vs fp16 or fp32
+    [pages, PAGE, H_KV]; block_tbl int32 [B, max_pages]; ctx_len int32 [B] (includes the
+    q_len query tokens).  QPP query tokens per program (default q_len = fused).  With
+    `plan`, (n_seqs, q_len) = plan[0:2] on the device and the grid covers (B, QLMAX).
+    Returns (out, ck).
+    """
+    _require_gpu(q, kc, vc, ks, vs, block_tbl, ctx_len)
+    B, QLMAX, H, D = q.shape
+    PAGE, H_KV = kc.shape[1], kc.shape[2]
+    if QPP is None:
+        QPP = q_len
+    if out is None:
+        out = torch.zeros_like(q)
+    n_seqs = B if n_seqs is None else n_seqs
+    if q.dtype != torch.float16 or out.dtype != torch.float16:
+        raise RuntimeError("paged_attention expects fp16 q and out")
+    if kc.dtype != torch.int8 or vc.dtype != torch.int8:
+        raise RuntimeError("paged_attention expects an int8 KV cache")
+    if kc.stride() != vc.stride() or ks.stride() != vs.stride() or ks.dtype != vs.dtype:
+        raise RuntimeError("paged_attention: K and V (and their scales) must share layout and dtype")
+    if ks.dtype not in (torch.float16, torch.float32):
+        raise RuntimeError("paged_attention: scales must be fp16 or fp32")
+    if q.stride(3) != 1 or out.stride(3) != 1 or kc.stride(3) != 1:
+        raise RuntimeError("paged_attention: head_dim must be contiguous")
+    if block_tbl.dtype != torch.int32 or ctx_len.dtype != torch.int32:
+        raise RuntimeError("paged_attention: block_tbl and ctx_len must be int32")
+    block_tbl = _rowmajor(block_tbl)
+    ctx_len = ctx_len.contiguous()
+    B_grid = B if plan is not None else int(n_seqs)
+    G = H // H_KV
+    max_pages = block_tbl.shape[1]
+    ws = workspace or _ws.shared(q.device)
+    need = _lib.lib().specq_paged_attn_workspace_size(B_grid, H, H_KV, QLMAX, int(QPP), max_pages, PAGE)
+    wptr, wbytes = ws.ensure(need)
+    _lib.call("specq_paged_attn",
+              q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+              kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2),
+              ks.data_ptr(), vs.data_ptr(), ks.stride(0), ks.stride(1), ks.stride(2),
+              1 if ks.dtype == torch.float32 else 0,
+              block_tbl.data_ptr(), block_tbl.stride(0), max_pages, ctx_len.data_ptr(),
+              out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+              B_grid, int(n_seqs), int(q_len), QLMAX, H, H_KV, D, PAGE, int(QPP),
+              1.0 / math.sqrt(D), _plan_ptr(plan), wptr, wbytes, _stream_ptr(q))
+    rows = int(QPP) * G
+    _paged_attn_kernel._note(q.device.index or 0, (D, (rows + 15) // 16, str(ks.dtype)))
+    return out, KernelInfo(2, D, 0, 0, 0, rows, 0, 4, 0)
+
+
+def make_paged_kv(B, ctx_len, H_KV, D, PAGE=16, device="cuda", seed=0):
+    """Random INT8 KV cache with a shuffled page table (reference kernels.py:265-286).
+
+    Same generator calls in the same order as the reference, so a given seed yields the
+    same cache.  Returns (kc, vc, ks, vs, block_tbl, ctx_len) with fp16 scales.
+    """
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    pages_per_seq = [(int(l) + PAGE - 1) // PAGE for l in ctx_len]
+    total = sum(pages_per_seq)
+    perm = torch.randperm(total, generator=g)
+    bt = torch.zeros((B, max(pages_per_seq)), dtype=torch.int32)
+    start = 0
+    for b, n in enumerate(pages_per_seq):
+        bt[b, :n] = perm[start:start + n].to(torch.int32)
+        start += n
+    kf = torch.randn((total, PAGE, H_KV, D), generator=g).half()
+    vf = torch.randn((total, PAGE, H_KV, D), generator=g).half()
+
+    def q8(x):
+        s = x.float().abs().amax(-1).clamp(min=1e-8) / 127.0
+        return torch.round(x.float() / s[..., None]).clamp(-127, 127).to(torch.int8), s.half()
+
+    kc, ks = q8(kf)
+    vc, vs = q8(vf)
+    dev = lambda t: t.to(device).contiguous()  # noqa: E731
+    return dev(kc), dev(vc), dev(ks), dev(vs), dev(bt), torch.tensor(list(ctx_len), dtype=torch.int32, device=device)
+
+
+def paged_attention_ref(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len):
+    """Dense fp32 verification attention (reference kernels.py:289-309), any device."""
+    B, _, H, D = q.shape
+    PAGE, H_KV = kc.shape[1], kc.shape[2]
+    G = H // H_KV
+    out = torch.zeros(q.shape, dtype=torch.float32, device=q.device)
+    for b in range(B):
+        L = int(ctx_len[b])
+        pos = torch.arange(L, device=q.device)
+        page = block_tbl[b, pos // PAGE].long()
+        slot = pos % PAGE
+        k = (kc[page, slot].float() * ks[page, slot].float()[..., None]).repeat_interleave(G, dim=1)
+        v = (vc[page, slot].float() * vs[page, slot].float()[..., None]).repeat_interleave(G, dim=1)
+        qq = q[b, :q_len].float()
+        s = torch.einsum("qhd,khd->hqk", qq, k) / math.sqrt(D)
+        qpos = L - q_len + torch.arange(q_len, device=q.device)
+        s = s.masked_fill(pos[None, None, :] > qpos[None, :, None], float("-inf"))
+        out[b, :q_len] = torch.einsum("hqk,khd->qhd", s.softmax(-1), v)
+    return out.half()
+
+
+# ----------------------------------------------------------------------------------------
+# Device-side steps of a verification layer (no reference counterpart on the device)
+# ----------------------------------------------------------------------------------------
+def silu_mul(gate, up, out=None, plan=None, grid_m_max=None):
+    """h = fp16(silu(gate) * up) on the GPU; gate/up fp16 [M, N]."""
+    _require_gpu(gate, up)
+    M, N = gate.shape
+    gate, up = _rowmajor(gate), _rowmajor(up)
+    if out is None:
+        out = torch.empty((M, N), device=gate.device, dtype=torch.float16)
+    _lib.call("specq_silu_mul", gate.data_ptr(), gate.stride(0), up.data_ptr(), up.stride(0),
+              out.data_ptr(), out.stride(0), M, N, int(grid_m_max or 0), _plan_ptr(plan), _stream_ptr(gate))
+    return out
+
+
+def quantize_act_int8_gpu(x, q=None, s=None, plan=None, grid_m_max=None):
+    """quantize_act_int8 on the GPU (bit-identical to the torch formula); x fp16 [M, K]."""
+    _require_gpu(x)
+    M, K = x.shape
+    x = _rowmajor(x)
+    q = torch.empty((M, K), device=x.device, dtype=torch.int8) if q is None else q
+    s = torch.empty((M,), device=x.device, dtype=torch.float32) if s is None else s
+    _lib.call("specq_quantize_act_int8", x.data_ptr(), x.stride(0), q.data_ptr(), q.stride(0), s.data_ptr(),
+              M, K, int(grid_m_max or 0), _plan_ptr(plan), _stream_ptr(x))
+    return q, s
+
+
+def silu_mul_quant_int8(gate, up, q=None, s=None, plan=None, grid_m_max=None):
+    """quantize_act_int8(silu_mul(gate, up)) fused on the GPU; returns (int8 [M, N], fp32 [M])."""
+    _require_gpu(gate, up)
+    M, N = gate.shape
+    gate, up = _rowmajor(gate), _rowmajor(up)
+    q = torch.empty((M, N), device=gate.device, dtype=torch.int8) if q is None else q
+    s = torch.empty((M,), device=gate.device, dtype=torch.float32) if s is None else s
+    _lib.call("specq_silu_mul_quant_int8", gate.data_ptr(), gate.stride(0), up.data_ptr(), up.stride(0),
+              q.data_ptr(), q.stride(0), s.data_ptr(), M, N, int(grid_m_max or 0), _plan_ptr(plan),
+              _stream_ptr(gate))
+    return q, s

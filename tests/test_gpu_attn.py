@@ -1,0 +1,107 @@
+"""INT8 paged verification attention on the GPU against the float64 CPU oracle.
+
+Tolerance (stated): max |out - ref| <= 4e-3 + 2**-9 * |ref| elementwise, well inside the
+reference's 2e-2 (correctness.py:100).  The kernel's deviations from the exact float64
+result are the fp16 rounding of p * vs before the PV product (as the reference,
+kernels.py:232), fp32 accumulation, exp2 rounding and the final fp16 store.
+Bit-exact properties: QPP=1 and fused QPP=k+1 give identical outputs; plan mode equals
+eager and leaves inactive sequences / query slots untouched.
+"""
+import numpy as np
+import pytest
+import torch
+
+import kernels as K
+from gpu_util import note
+from oracle import oracle as O
+from specq import gen
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+H, H_KV, D = 32, 8, 128
+
+
+def check(out, ref, ql, what):
+    o = out[:, :ql].float().cpu().numpy().astype(np.float64)
+    r = ref[:, :ql]
+    err = np.abs(o - r)
+    bound = 4e-3 + 2.0 ** -9 * np.abs(r)
+    assert (err <= bound).all(), f"{what}: max err {err.max():.3e}"
+    return float(err.max())
+
+
+def cpu(*ts):
+    return [t.cpu().numpy() for t in ts]
+
+
+@pytest.mark.parametrize("B", [1, 3, 8])
+@pytest.mark.parametrize("k", [2, 4, 8])
+def test_attention_correctness_py_cases(B, k):
+    # correctness.py:89-100: random context in [k+1, 700), reference generator, QPP in {1, k+1}
+    ql = k + 1
+    g = torch.Generator().manual_seed(100 * B + k)
+    ctx = [int(x) for x in torch.randint(ql, 700, (B,), generator=g)]
+    kc, vc, ks, vs, bt, cl = K.make_paged_kv(B, ctx, H_KV, D, device=DEV, seed=B * 10 + k)
+    q = torch.randn(B, ql, H, D, generator=g).half().to(DEV)
+    ref = O.paged_attention(*cpu(q, kc, vc, ks, vs, bt, cl), ql)
+    note(f"attn B={B} k={k} ctx={ctx}")
+    outs = {}
+    for QPP in (1, ql):
+        out, _ = K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=QPP)
+        torch.cuda.synchronize()
+        check(out, ref, ql, f"B={B} k={k} QPP={QPP}")
+        outs[QPP] = out
+    assert torch.equal(outs[1], outs[ql]), "QPP=1 and fused results differ"
+
+
+@pytest.mark.parametrize("ctx", [1024, 4096])
+@pytest.mark.parametrize("k", [0, 3, 8])
+def test_attention_config3_fp32_scales(ctx, k):
+    B, ql = 8, k + 1
+    note(f"attn config3 B={B} ctx={ctx} k={k}")
+    kc, vc, ks, vs, bt, cl = gen.paged_kv(B, [ctx + ql] * B, H_KV, D, seed=ctx + k)
+    q = gen.queries(B, ql, H, D, seed=k)
+    ref = O.paged_attention(*cpu(q, kc, vc, ks, vs, bt, cl), ql)
+    kc, vc, ks, vs, bt, cl, q = (t.to(DEV) for t in (kc, vc, ks, vs, bt, cl, q))
+    o1, _ = K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=ql)
+    o2, _ = K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=1)
+    torch.cuda.synchronize()
+    check(o1, ref, ql, "fused")
+    assert torch.equal(o1, o2)
+
+
+def test_attention_plan_mode_sentinels():
+    # correctness.py:103-120: one grid (B_MAX=8, QLMAX=9), active (B, q_len) from plan[1:3].
+    BMAX, QLMAX = 8, 9
+    g = torch.Generator().manual_seed(99)
+    ctx = [int(x) for x in torch.randint(QLMAX, 700, (BMAX,), generator=g)]
+    kc, vc, ks, vs, bt, cl = K.make_paged_kv(BMAX, ctx, H_KV, D, device=DEV, seed=99)
+    qfull = torch.randn(BMAX, QLMAX, H, D, generator=g).half().to(DEV)
+    plan = torch.zeros(8, dtype=torch.int32, device=DEV)
+    for B_act, ql in ((1, 3), (3, 5), (8, 9), (5, 3), (8, 5), (0, 4), (8, 1)):
+        note(f"attn plan B={B_act} ql={ql}")
+        plan[1], plan[2] = B_act, ql
+        out = torch.full_like(qfull, 7.0)
+        K.paged_attention(qfull, kc, vc, ks, vs, bt, cl, QLMAX, QPP=QLMAX, plan=plan[1:], out=out)
+        torch.cuda.synchronize()
+        if B_act:
+            eager = torch.full_like(qfull[:B_act], 7.0)
+            K.paged_attention(qfull[:B_act], kc, vc, ks, vs, bt[:B_act], cl[:B_act], ql, QPP=ql, out=eager)
+            torch.cuda.synchronize()
+            assert torch.equal(out[:B_act, :ql], eager[:, :ql])
+            ref = O.paged_attention(*cpu(qfull[:B_act], kc, vc, ks, vs, bt[:B_act], cl[:B_act]), ql)
+            check(out[:B_act], ref, ql, f"plan B={B_act} ql={ql}")
+        assert bool((out[B_act:] == 7.0).all()) and bool((out[:B_act, ql:] == 7.0).all())
+
+
+def test_attention_head_dim_64_and_no_visible_key():
+    note("attn D=64, L < q_len")
+    kc, vc, ks, vs, bt, cl = gen.paged_kv(2, [600, 2], 4, 64, seed=3, scale_dtype=torch.float16)
+    q = gen.queries(2, 4, 16, 64, seed=4)
+    cl[1] = 2  # only 2 tokens but 4 queries: the first two query rows see no key -> 0
+    ref = O.paged_attention(*cpu(q, kc, vc, ks, vs, bt, cl), 4)
+    kc, vc, ks, vs, bt, cl, q = (t.to(DEV) for t in (kc, vc, ks, vs, bt, cl, q))
+    out, _ = K.paged_attention(q, kc, vc, ks, vs, bt, cl, 4)
+    torch.cuda.synchronize()
+    check(out, ref, 4, "D=64")
+    assert bool((out[1, :2] == 0).all())

@@ -1,0 +1,123 @@
+"""W4A16 GEMM on the GPU against the float64 CPU oracle.
+
+Tolerance (stated): the kernel rounds fp16 weights exactly like the reference and sums
+exact fp16 x fp16 products in fp32, so its error is the final fp16 rounding plus fp32
+accumulation: elementwise |out - ref| <= 2**-10 * |ref| + 2e-3 * rms(ref), and the
+reference's own criterion, relative Frobenius error < 2e-3 (correctness.py:77-79).
+Plan mode is bit-identical to eager and never writes rows >= M.
+"""
+import numpy as np
+import pytest
+import torch
+
+import kernels as K
+from gpu_util import note
+from oracle import oracle as O
+from specq import gen
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def check_tol(out, ref, what):
+    o = out.float().cpu().numpy().astype(np.float64)
+    rms = float(np.sqrt(np.mean(ref ** 2))) or 1.0
+    err = np.abs(o - ref)
+    bound = 2.0 ** -10 * np.abs(ref) + 2e-3 * rms
+    fro = float(np.linalg.norm(o - ref) / (np.linalg.norm(ref) or 1.0))
+    assert (err <= bound).all(), f"{what}: max excess {float((err - bound).max())} (rms {rms})"
+    assert fro < 2e-3, f"{what}: rel-Frobenius {fro}"
+    return fro
+
+
+@pytest.fixture(scope="module")
+def ref_case():
+    # correctness.py:68-71: N=1000, K=1024, group 128, weights from the reference quantizer.
+    torch.manual_seed(0)
+    w4 = torch.randn(1000, 1024, dtype=torch.float16)
+    wp, sc, deq = K.quantize_weight_int4(w4, group=128)
+    x4 = torch.randn(300, 1024, dtype=torch.float16)
+    qu = O.unpack_int4_u8(wp.numpy())
+    ref = O.w4a16(x4.numpy(), qu, sc.numpy(), 128)
+    return x4.to(DEV), wp.to(DEV), sc.to(DEV), qu, ref
+
+
+MS = list(range(1, 65)) + [72, 99, 128, 129, 200, 288, 300]
+
+
+@pytest.mark.parametrize("BM", [16, 32, 64, 128])
+def test_w4a16_reference_layout_m_sweep(ref_case, BM):
+    x4, wp, sc, _, ref = ref_case
+    note(f"w4a16 layout0 N=1000 K=1024 BLOCK_M={BM}")
+    outs = [K.w4a16_matmul(x4[:M], wp, sc, BLOCK_M=BM)[0] for M in MS]
+    torch.cuda.synchronize()
+    worst = 0.0
+    for M, out in zip(MS, outs):
+        worst = max(worst, check_tol(out, ref[:M], f"BLOCK_M={BM} M={M}"))
+    print(f"max rel-Frobenius {worst:.2e}")
+
+
+def test_w4a16_int32_layout_and_auto_tile(ref_case):
+    x4, _, sc, qu, ref = ref_case
+    note("w4a16 layout1 auto BLOCK_M")
+    wi = torch.from_numpy(O.pack_int4_i32(qu)).to(DEV)
+    outs = [K.w4a16_matmul(x4[:M], wi, sc, BLOCK_M=None)[0] for M in MS]
+    torch.cuda.synchronize()
+    for M, out in zip(MS, outs):
+        check_tol(out, ref[:M], f"layout1 M={M}")
+
+
+@pytest.mark.parametrize("shape", gen.CONFIG1_SHAPES)
+def test_w4a16_config2_shapes(shape):
+    N, Kd = shape
+    note(f"w4a16 config2 N={N} K={Kd}")
+    qu, sc = gen.int4_weights(N, Kd, 128, seed=2000 + N)
+    a = gen.fp16_acts(300, Kd, seed=3000 + Kd)
+    ref = O.w4a16(a.numpy(), qu.numpy(), sc.numpy(), 128)
+    wi = gen.pack_i32(qu).to(DEV)
+    wu = gen.pack_u8_reference(qu).to(DEV)
+    a, sc = a.to(DEV), sc.to(DEV)
+    for M in (1, 8, 72, 300):
+        for wp in (wi, wu):
+            out, ck = K.w4a16_matmul(a[:M], wp, sc, BLOCK_M=None)
+            torch.cuda.synchronize()
+            check_tol(out, ref[:M], f"N={N} K={Kd} M={M} {wp.dtype}")
+    assert ck.n_spills == 0
+
+
+def test_w4a16_kats():
+    note("w4a16 KATs")
+    a = gen.fp16_acts(16, 256, seed=1).to(DEV)
+    zero_u8 = torch.full((64, 128), 0x88, dtype=torch.uint8, device=DEV)
+    sc = torch.full((64, 2), 0.01, dtype=torch.float16, device=DEV)
+    out, _ = K.w4a16_matmul(a, zero_u8, sc, BLOCK_M=None)
+    assert bool((out == 0).all())
+    one = zero_u8.clone()
+    one[5, 17] = 0x8D            # k = 17 holds q = +5 (low nibble); k = 145 stays 0
+    out, _ = K.w4a16_matmul(a, one, sc, BLOCK_M=None)
+    w = np.float16(np.float16(5.0) * np.float16(0.01))
+    want = (a[:, 17].float().cpu().numpy() * np.float32(w)).astype(np.float16)
+    assert np.array_equal(out[:, 5].cpu().numpy(), want)
+    assert bool((out[:, :5] == 0).all()) and bool((out[:, 6:] == 0).all())
+
+
+def test_w4a16_plan_mode_bit_identical_to_eager():
+    note("w4a16 plan mode")
+    qu, sc = gen.int4_weights(4096, 4096, 128, seed=7)
+    wi, sc = gen.pack_i32(qu).to(DEV), sc.to(DEV)
+    a = gen.fp16_acts(288, 4096, seed=8).to(DEV)
+    plan = torch.zeros(8, dtype=torch.int32, device=DEV)
+    for bm in (16, 128):
+        for M in (1, 9, 27, 72, 288):
+            eager, _ = K.w4a16_matmul(a[:M], wi, sc, BLOCK_M=bm)
+            plan[0] = M
+            out = torch.full((288, 4096), 7.0, dtype=torch.float16, device=DEV)
+            K.w4a16_matmul(a, wi, sc, out=out, plan=plan, grid_m_max=288, BLOCK_M=bm)
+            torch.cuda.synchronize()
+            assert torch.equal(out[:M], eager), f"plan != eager at BLOCK_M={bm} M={M}"
+            assert bool((out[M:] == 7.0).all())
+    # the fp32 summation order does not depend on BLOCK_M either
+    e16, _ = K.w4a16_matmul(a[:100], wi, sc, BLOCK_M=16)
+    e128, _ = K.w4a16_matmul(a[:100], wi, sc, BLOCK_M=128)
+    torch.cuda.synchronize()
+    assert torch.equal(e16, e128)

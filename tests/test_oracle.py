@@ -1,0 +1,230 @@
+"""Pins for the CPU oracle (oracle/oracle.py), each independent of the oracle's formula.
+
+The reference ships no golden vectors (its results/correctness.json holds scalar maxima
+only), so every oracle function is pinned by what the mathematics fixes:
+  w8a8_int32         torch._int_mm (library), pure-Python brute force, all-127 closed form
+  w8a8               torch fp32 epilogue in the reference order; closed-form KAT; a
+                     reordered epilogue is shown to differ (the order is really tested)
+  quantize_rows_int8 hand-computed KATs incl. round-half-to-even and the 1e-8 clamp;
+                     torch restatement (library round)
+  int4 pack/unpack   byte KATs 0x88 -> (0, 0), 0x0F -> (+7, -8); exhaustive round trips;
+                     u8 <-> int32 layouts agree on every nibble
+  dequant / w4a16    all-0x88 -> 0; single nonzero nibble -> a[:, k] * (q - 8) * s; torch
+                     float64 matmul
+  paged_attention    torch scaled_dot_product_attention in float64 (library) on a dense
+                     gather; brute-force Python softmax; constant-V and single-key closed
+                     forms; invariance under a consistent pool permutation
+  silu_mul           torch.nn.functional.silu
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------- W8A8
+def test_w8a8_int32_matches_torch_int_mm():
+    r = rng(0)
+    a = r.integers(-127, 128, (32, 520), dtype=np.int8)
+    w = r.integers(-127, 128, (1000, 520), dtype=np.int8)
+    ref = torch._int_mm(torch.from_numpy(a), torch.from_numpy(w).T.contiguous()).numpy()
+    assert np.array_equal(O.w8a8_int32(a, w), ref)
+
+
+def test_w8a8_int32_brute_force_tiny():
+    r = rng(1)
+    a = r.integers(-127, 128, (3, 7), dtype=np.int8)
+    w = r.integers(-127, 128, (5, 7), dtype=np.int8)
+    got = O.w8a8_int32(a, w)
+    for m in range(3):
+        for n in range(5):
+            assert got[m, n] == sum(int(a[m, k]) * int(w[n, k]) for k in range(7))
+
+
+def test_w8a8_all_127_closed_form_exceeds_fp32_exact_range():
+    K = 4096
+    a = np.full((2, K), 127, np.int8)
+    w = np.full((3, K), -127, np.int8)
+    acc = O.w8a8_int32(a, w)
+    assert (acc == -16129 * K).all() and 16129 * K > 2 ** 24
+
+
+def test_w8a8_epilogue_matches_torch_reference_order():
+    r = rng(2)
+    a = r.integers(-127, 128, (20, 256), dtype=np.int8)
+    w = r.integers(-127, 128, (64, 256), dtype=np.int8)
+    sa = r.uniform(0.005, 0.02, 20).astype(np.float32)
+    sw = r.uniform(0.001, 0.01, 64).astype(np.float32)
+    acc = torch._int_mm(torch.from_numpy(a), torch.from_numpy(w).T.contiguous())
+    ref = ((acc.float() * torch.from_numpy(sa)[:, None]) * torch.from_numpy(sw)[None, :]).half().numpy()
+    got = O.w8a8(a, sa, w, sw)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    # The order matters: acc * (sa * sw) rounds differently somewhere in this block.
+    other = (acc.float() * (torch.from_numpy(sa)[:, None] * torch.from_numpy(sw)[None, :])).half().numpy()
+    assert not np.array_equal(other.view(np.uint16), ref.view(np.uint16))
+
+
+def test_w8a8_kat_single_term():
+    a = np.zeros((1, 64), np.int8); a[0, 5] = 100
+    w = np.zeros((2, 64), np.int8); w[1, 5] = -3
+    out = O.w8a8(a, np.array([0.5], np.float32), w, np.array([1.0, 0.25], np.float32))
+    assert out[0, 0] == 0 and out[0, 1] == np.float16(-300 * 0.5 * 0.25)
+
+
+# ---------------------------------------------------------------- quantisers
+def test_quantize_rows_kats():
+    x = np.array([[127.0, -63.5, 0.5, 1.5, 2.5, -2.5, 0.0]], np.float32)
+    q, s = O.quantize_rows_int8(x)
+    assert s[0] == np.float32(1.0)
+    assert q.tolist() == [[127, -64, 0, 2, 2, -2, 0]]  # half-to-even at .5
+    z, sz = O.quantize_rows_int8(np.zeros((1, 4), np.float32))
+    assert sz[0] == np.float32(1e-8) / np.float32(127.0) and (z == 0).all()
+
+
+def test_quantize_rows_matches_torch_formula():
+    x = torch.randn(40, 300, generator=torch.Generator().manual_seed(3)).half()
+    s_t = x.abs().amax(-1).float().clamp(min=1e-8) / 127.0
+    q_t = torch.round(x.float() / s_t[:, None]).clamp(-127, 127).to(torch.int8)
+    q, s = O.quantize_rows_int8(x.numpy())
+    assert np.array_equal(q, q_t.numpy()) and np.array_equal(s, s_t.numpy())
+
+
+# ---------------------------------------------------------------- INT4
+def test_int4_byte_kats():
+    assert O.unpack_int4_u8(np.array([[0x88]], np.uint8)).astype(int).tolist() == [[8, 8]]
+    lo_hi = O.unpack_int4_u8(np.array([[0x0F]], np.uint8)).astype(int) - 8
+    assert lo_hi.tolist() == [[7, -8]]
+
+
+def test_int4_round_trips_exhaustive():
+    vals = np.array(np.meshgrid(np.arange(16), np.arange(16))).reshape(2, -1).T  # all nibble pairs
+    qu = np.concatenate([vals[:, :1], vals[:, 1:]], axis=1).astype(np.uint8).reshape(1, -1)
+    qu = np.concatenate([qu, qu[:, ::-1]], axis=0)  # [2, 512]
+    assert np.array_equal(O.unpack_int4_u8(O.pack_int4_u8(qu)), qu)
+    assert np.array_equal(O.unpack_int4_i32(O.pack_int4_i32(qu)), qu)
+    words = O.pack_int4_i32(np.arange(8, dtype=np.uint8).reshape(1, 8))
+    assert words.view(np.uint32)[0, 0] == 0x76543210
+
+
+def test_int4_quantizer_matches_torch_restatement():
+    w = torch.randn(64, 512, generator=torch.Generator().manual_seed(4))
+    packed, sc, deq = O.quantize_weight_int4(w.numpy(), 128)
+    wg = w.float().view(64, 4, 128)
+    sct = wg.abs().amax(-1).clamp(min=1e-8) / 7.0
+    q = torch.round(wg / sct[..., None]).clamp(-8, 7).view(64, 512).to(torch.int16) + 8
+    ref_packed = (q[:, :256] | (q[:, 256:] << 4)).to(torch.uint8)
+    assert np.array_equal(packed, ref_packed.numpy())
+    assert np.array_equal(sc, sct.half().numpy())
+    ref_deq = ((q - 8).float().view(64, 4, 128) * sct[..., None]).view(64, 512).half()
+    assert np.array_equal(deq.view(np.uint16), ref_deq.numpy().view(np.uint16))
+
+
+def test_w4a16_kats_and_torch():
+    r = rng(5)
+    N, K, G = 32, 256, 128
+    a = r.standard_normal((4, K)).astype(np.float16)
+    zero = O.w4a16(a, np.full((N, K), 8, np.uint8), np.ones((N, K // G), np.float16), G)
+    assert (zero == 0).all()
+    qu = np.full((N, K), 8, np.uint8); qu[3, 200] = 8 + 5
+    sc = np.full((N, K // G), 0.0123, np.float16)
+    one = O.w4a16(a, qu, sc, G)
+    expect = a[:, 200].astype(np.float64) * float(np.float16(5 * np.float32(np.float16(0.0123))))
+    assert np.array_equal(one[:, 3], expect) and (np.delete(one, 3, axis=1) == 0).all()
+    qu = r.integers(0, 16, (N, K)).astype(np.uint8)
+    sc = r.uniform(0.002, 0.02, (N, K // G)).astype(np.float16)
+    deq_t = ((torch.from_numpy(qu.astype(np.int16)) - 8).half() * torch.from_numpy(sc).repeat_interleave(G, 1)).double()
+    ref = torch.from_numpy(a).double() @ deq_t.T
+    assert np.allclose(O.w4a16(a, qu, sc, G), ref.numpy(), rtol=0, atol=1e-12)
+
+
+# ---------------------------------------------------------------- attention
+def _small_cache(seed, B=2, ctx=(37, 20), H=8, H_KV=2, D=16, PAGE=16):
+    r = rng(seed)
+    pages = [(c + PAGE - 1) // PAGE for c in ctx]
+    total = sum(pages)
+    perm = r.permutation(total)
+    bt = np.zeros((B, max(pages)), np.int32)
+    i = 0
+    for b, n in enumerate(pages):
+        bt[b, :n] = perm[i:i + n]; i += n
+    kc = r.integers(-127, 128, (total, PAGE, H_KV, D), dtype=np.int8)
+    vc = r.integers(-127, 128, (total, PAGE, H_KV, D), dtype=np.int8)
+    ks = r.uniform(0.005, 0.02, (total, PAGE, H_KV)).astype(np.float32)
+    vs = r.uniform(0.005, 0.02, (total, PAGE, H_KV)).astype(np.float32)
+    return kc, vc, ks, vs, bt, np.array(ctx, np.int32)
+
+
+def test_attention_matches_torch_sdpa_float64():
+    kc, vc, ks, vs, bt, cl = _small_cache(6)
+    B, QL, H, D, H_KV, PAGE, G = 2, 3, 8, 16, 2, 16, 4
+    q = rng(7).standard_normal((B, QL, H, D)).astype(np.float16)
+    got = O.paged_attention(q, kc, vc, ks, vs, bt, cl, QL)
+    for b in range(B):
+        L = int(cl[b]); pos = np.arange(L)
+        pg, sl = bt[b, pos // PAGE], pos % PAGE
+        k = torch.from_numpy(kc[pg, sl].astype(np.float64) * ks[pg, sl][..., None])
+        v = torch.from_numpy(vc[pg, sl].astype(np.float64) * vs[pg, sl][..., None])
+        k = k.repeat_interleave(G, 1).permute(1, 0, 2)
+        v = v.repeat_interleave(G, 1).permute(1, 0, 2)
+        qq = torch.from_numpy(q[b].astype(np.float64)).permute(1, 0, 2)
+        qpos = L - QL + torch.arange(QL)
+        mask = torch.arange(L)[None, :] <= qpos[:, None]
+        ref = torch.nn.functional.scaled_dot_product_attention(qq, k, v, attn_mask=mask)
+        assert np.allclose(got[b], ref.permute(1, 0, 2).numpy(), atol=1e-12, rtol=1e-10)
+
+
+def test_attention_brute_force_python():
+    kc, vc, ks, vs, bt, cl = _small_cache(8, B=1, ctx=(19,), H=2, H_KV=1, D=4)
+    q = rng(9).standard_normal((1, 2, 2, 4)).astype(np.float16)
+    got = O.paged_attention(q, kc, vc, ks, vs, bt, cl, 2)
+    L = 19
+    for i in range(2):
+        for h in range(2):
+            qp = L - 2 + i
+            sc = []
+            for t in range(qp + 1):
+                pg, sl = bt[0, t // 16], t % 16
+                sc.append(sum(float(q[0, i, h, d]) * kc[pg, sl, 0, d] * float(ks[pg, sl, 0]) for d in range(4)) / 2.0)
+            mx = max(sc); e = [math.exp(x - mx) for x in sc]; den = sum(e)
+            for d in range(4):
+                o = sum(e[t] / den * vc[bt[0, t // 16], t % 16, 0, d] * float(vs[bt[0, t // 16], t % 16, 0])
+                        for t in range(qp + 1))
+                assert abs(got[0, i, h, d] - o) < 1e-9
+
+
+def test_attention_closed_forms():
+    kc, vc, ks, vs, bt, cl = _small_cache(10)
+    q = rng(11).standard_normal((2, 2, 8, 16)).astype(np.float16)
+    vc[:] = 50
+    vs[:] = 0.01
+    got = O.paged_attention(q, kc, vc, ks, vs, bt, cl, 2)
+    assert np.allclose(got[:, :2], 0.5, atol=1e-12)           # constant V -> V
+    # single visible key: L = q_len = 1 -> output is that key's scaled value
+    kc2, vc2, ks2, vs2, bt2, _ = _small_cache(12, B=1, ctx=(1,))
+    one = O.paged_attention(q[:1, :1], kc2, vc2, ks2, vs2, bt2, np.array([1], np.int32), 1)
+    expect = vc2[bt2[0, 0], 0].astype(np.float64) * vs2[bt2[0, 0], 0][:, None]
+    assert np.allclose(one[0, 0], np.repeat(expect, 4, axis=0), atol=1e-12)
+
+
+def test_attention_pool_permutation_invariance():
+    kc, vc, ks, vs, bt, cl = _small_cache(13)
+    q = rng(14).standard_normal((2, 3, 8, 16)).astype(np.float16)
+    base = O.paged_attention(q, kc, vc, ks, vs, bt, cl, 3)
+    perm = rng(15).permutation(kc.shape[0])
+    inv = np.argsort(perm)
+    got = O.paged_attention(q, kc[perm], vc[perm], ks[perm], vs[perm], inv[bt].astype(np.int32), cl, 3)
+    assert np.array_equal(base, got)
+
+
+def test_silu_mul_matches_torch():
+    g = torch.randn(8, 64, generator=torch.Generator().manual_seed(16)).half()
+    u = torch.randn(8, 64, generator=torch.Generator().manual_seed(17)).half()
+    ref = torch.nn.functional.silu(g.double()) * u.double()
+    assert np.allclose(O.silu_mul(g.numpy(), u.numpy()), ref.numpy(), atol=1e-12)
