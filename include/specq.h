@@ -74,6 +74,28 @@ int specq_w8a8(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
                int block_m, int block_n, int num_warps, int split_k,
                void* workspace, size_t workspace_bytes, void* stream);
 
+/* W8A8 with the weight pre-packed once into MFMA fragments (the layout production inference
+ * stacks "pre-shuffle" weights into at load time): packed[t][s][l*16 + b] =
+ * w[16t + l%16][64s + 16*(l/16) + b] for 16-row tile t, 64-byte K step s, lane l, byte b,
+ * zero-padded to whole tiles; specq_w8a8_packed_bytes() bytes.  Each 1 KB fragment is one
+ * MFMA operand, so the GEMM reads it contiguously.  Results are bit-identical to specq_w8a8
+ * on the unpacked weight.  No reference counterpart: w8a8_matmul (kernels.py:71-86) takes
+ * the row-major weight only. */
+size_t specq_w8a8_packed_bytes(int N, int K);
+int specq_w8a8_pack_weight(const int8_t* w, int64_t ldw, int N, int K, void* packed, void* stream);
+size_t specq_w8a8_packed_workspace_size(int m_grid, int N, int K, int block_m, int block_n,
+                                        int num_warps, int split_k);
+int specq_w8a8_packed(const int8_t* a, int64_t lda, const void* w_packed,
+                      const float* sa, const float* sw, void* c, int64_t ldc,
+                      int M, int N, int K, int grid_m_max, const int32_t* plan,
+                      int block_m, int block_n, int num_warps, int split_k,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Tuning options.  "w8a8_path": W8A8 kernel family for 16-byte aligned row-major weights,
+ * 0 = automatic, 1 = register streaming, 2 = LDS-DMA ring, 3 = byte-granular register
+ * kernel.  Every family computes the same INT32 sums, so results do not change. */
+int specq_set_option(const char* name, int value);
+
 /* ---------------------------------------------------------------------------------------
  * W4A16 GEMM: C[m, n] = fp16( sum_k a[m,k] * fp16(fp16(q[n,k]) * sc[n, k/group]) )
  * with q the signed int4 weight in [-8, 7] stored as an unsigned nibble with offset 8.

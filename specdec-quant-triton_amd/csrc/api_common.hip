@@ -1,6 +1,7 @@
 // Shared host-side pieces of the C ABI: thread-local error text, launch wrapper, device info,
 // and the kernel-attribute query that dispatches to each kernel family.
 #include <mutex>
+#include <set>
 #include <vector>
 
 #include "api_common.hpp"
@@ -26,6 +27,21 @@ int launch(const void* fn, int grid, int threads, size_t lds, hipStream_t stream
     set_error("hipLaunchKernel failed: %s (grid=%d threads=%d lds=%zu)", hipGetErrorString(e), grid, threads, lds);
     return SPECQ_EIO;
   }
+  return SPECQ_OK;
+}
+
+int ensure_lds(const void* fn, size_t lds) {
+  if (lds <= 65536) return SPECQ_OK;
+  static std::mutex mu;
+  static std::set<const void*> done;
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count(fn)) return SPECQ_OK;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) {
+    set_error("cannot enable %zu bytes of LDS: %s", lds, hipGetErrorString(e));
+    return SPECQ_EIO;
+  }
+  done.insert(fn);
   return SPECQ_OK;
 }
 

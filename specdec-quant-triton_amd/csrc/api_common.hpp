@@ -44,6 +44,9 @@ inline int common_vec(std::initializer_list<uint64_t> vals) {
 
 int launch(const void* fn, int grid, int threads, size_t lds, hipStream_t stream, void* params);
 
+// Kernels using more than 64 KiB of dynamic LDS opt in once per kernel.
+int ensure_lds(const void* fn, size_t lds);
+
 // Number of CUs of the current device (cached per device).
 int device_cus();
 

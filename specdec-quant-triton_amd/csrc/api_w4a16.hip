@@ -1,7 +1,4 @@
 // C ABI for the W4A16 GEMM: argument validation, tile / split-K selection and launch.
-#include <mutex>
-#include <set>
-
 #include "api_common.hpp"
 #include "w4a16.hpp"
 
@@ -66,22 +63,6 @@ int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, in
                 "w4a16: %d x %d tiles exceed the counter region", cfg->m_chunks, cfg->n_tiles);
   cfg->fn = layout == 0 ? w4a16_kernel_l0(mt, rw) : w4a16_kernel_l1(mt, rw);
   SPECQ_REQUIRE(cfg->fn != nullptr, SPECQ_ENOTSUP, "w4a16: kernel MT=%d RW=%d not built", mt, rw);
-  return SPECQ_OK;
-}
-
-// Kernels using more than 64 KiB of dynamic LDS must opt in once.
-int ensure_lds(const void* fn, size_t lds) {
-  if (lds <= 65536) return SPECQ_OK;
-  static std::mutex mu;
-  static std::set<const void*> done;
-  std::lock_guard<std::mutex> lock(mu);
-  if (done.count(fn)) return SPECQ_OK;
-  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) {
-    set_error("w4a16: cannot enable %zu bytes of LDS: %s", lds, hipGetErrorString(e));
-    return SPECQ_EIO;
-  }
-  done.insert(fn);
   return SPECQ_OK;
 }
 

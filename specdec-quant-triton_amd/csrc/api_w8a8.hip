@@ -1,22 +1,78 @@
-// C ABI for the W8A8 GEMM: argument validation, tile / split-K selection and launch.
+// C ABI for the W8A8 GEMM: argument validation, kernel-family and tile selection, launch.
+//
+// Kernel families (all compute identical INT32 sums, so every choice is bit-identical):
+//   STREAM  register-streaming kernel (w8a8_stream.hpp), 16-byte aligned operands; takes the
+//           row-major weight or the packed-fragment weight.  Default.
+//   DMA     LDS-DMA ring kernel (w8a8_dma.hpp), 16-byte aligned row-major weights.
+//   LEGACY  register-pipelined kernel with 16/8/4/1-byte loads (w8a8.hpp): any alignment.
+#include <algorithm>
+#include <atomic>
+
 #include "api_common.hpp"
 #include "w8a8.hpp"
+#include "w8a8_stream.hpp"
 
 namespace specq {
 
 const void* w8a8_kernel_rw1(int mt, int vec);
 const void* w8a8_kernel_rw2(int mt, int vec);
 const void* w8a8_kernel_rw4(int mt, int vec);
+#define SPECQ_DMA_DECL(R, N)                     \
+  const void* w8a8_dma_kernel_r##R##n##N(int mt); \
+  int w8a8_dma_lds_r##R##n##N(int mt);
+SPECQ_DMA_DECL(1, 1)
+SPECQ_DMA_DECL(1, 2)
+SPECQ_DMA_DECL(1, 4)
+SPECQ_DMA_DECL(2, 1)
+SPECQ_DMA_DECL(2, 2)
+SPECQ_DMA_DECL(2, 4)
+#undef SPECQ_DMA_DECL
+const void* w8a8_stream_kernel_l0r1(int mt);
+const void* w8a8_stream_kernel_l0r2(int mt);
+const void* w8a8_stream_kernel_l1r1(int mt);
+const void* w8a8_stream_kernel_l1r2(int mt);
+
+// Packs a row-major int8 weight [N, K] (row stride ldw) into MFMA fragments:
+// packed[t][s][l*16 + b] = W[16t + l%16][64s + 16*(l/16) + b], zero-padded to whole tiles.
+__global__ __launch_bounds__(256) void w8a8_pack_kernel(const int8_t* __restrict__ W, int64_t ldw, int N, int K,
+                                                        int8_t* __restrict__ out) {
+  const int ksteps = (K + 63) / 64;
+  const int64_t frag = blockIdx.x * 4 + (threadIdx.x >> 6);  // one wave per fragment
+  const int ntiles = (N + 15) / 16;
+  if (frag >= (int64_t)ntiles * ksteps) return;
+  const int t = (int)(frag / ksteps), s = (int)(frag % ksteps);
+  const int l = threadIdx.x & 63;
+  const int row = 16 * t + (l & 15), k0 = 64 * s + 16 * (l >> 4);
+  int w4[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int v = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int k = k0 + 4 * i + b;
+      const int x = (row < N && k < K) ? (int)(uint8_t)W[(int64_t)row * ldw + k] : 0;
+      v |= x << (8 * b);
+    }
+    w4[i] = v;
+  }
+  *reinterpret_cast<v4i*>(out + frag * 1024 + l * 16) = v4i{w4[0], w4[1], w4[2], w4[3]};
+}
+
+// Kernel family override (0 = automatic), set through specq_set_option("w8a8_path", v).
+std::atomic<int> g_w8a8_path{0};
 
 namespace {
 
+enum Family { kStream = 1, kDma = 2, kLegacy = 3 };
+
 struct W8A8Cfg {
+  int family, layout;
   int mt, rw, nw, vec, splits, k_range, n_tiles, m_chunks;
+  int nwn, bn;  // DMA: waves along N; channels per workgroup (all families)
   size_t lds, ws_partials, ws_counters;
   const void* fn;
 };
 
-// MT values built for operands that are not 16-byte aligned.
 int round_mt_for_vec(int mt, int vec, int rw) {
   if (vec == 16) return mt;
   static const int avail[] = {1, 2, 4, 8, 16, 20};
@@ -25,7 +81,7 @@ int round_mt_for_vec(int mt, int vec, int rw) {
   return -1;
 }
 
-const void* w8a8_fn(int mt, int rw, int vec) {
+const void* legacy_fn(int mt, int rw, int vec) {
   switch (rw) {
     case 1: return w8a8_kernel_rw1(mt, vec);
     case 2: return w8a8_kernel_rw2(mt, vec);
@@ -34,65 +90,171 @@ const void* w8a8_fn(int mt, int rw, int vec) {
   return nullptr;
 }
 
-// Resolve the tile configuration.  `vec` is the operand alignment (16 when unknown).
-int w8a8_config(int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k, int vec,
-                W8A8Cfg* cfg) {
+const void* dma_fn(int mt, int rw, int nwn, int* lds) {
+  const void* fn = nullptr;
+#define SPECQ_DMA_PICK(R, N)             \
+  if (rw == R && nwn == N) {             \
+    fn = w8a8_dma_kernel_r##R##n##N(mt); \
+    *lds = w8a8_dma_lds_r##R##n##N(mt);  \
+  }
+  SPECQ_DMA_PICK(1, 1) SPECQ_DMA_PICK(1, 2) SPECQ_DMA_PICK(1, 4)
+  SPECQ_DMA_PICK(2, 1) SPECQ_DMA_PICK(2, 2) SPECQ_DMA_PICK(2, 4)
+#undef SPECQ_DMA_PICK
+  return fn;
+}
+
+const void* stream_fn(int layout, int mt, int rw) {
+  if (layout == 0) return rw == 1 ? w8a8_stream_kernel_l0r1(mt) : w8a8_stream_kernel_l0r2(mt);
+  return rw == 1 ? w8a8_stream_kernel_l1r1(mt) : w8a8_stream_kernel_l1r2(mt);
+}
+
+// Resolve the kernel and its tiles.  `vec` is the operand alignment (16 when unknown),
+// `layout` 0 = row-major weight, 1 = packed fragments.
+int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k,
+                int vec, W8A8Cfg* cfg) {
   SPECQ_REQUIRE(m_grid >= 0 && N > 0 && K > 0, SPECQ_EINVAL, "w8a8: bad sizes M=%d N=%d K=%d", m_grid, N, K);
-  int rows16 = ceil_div(m_grid > 0 ? m_grid : 1, 16);
+  SPECQ_REQUIRE(block_n == 0 || block_n == 16 || block_n == 32 || block_n == 64 || block_n == 128, SPECQ_ENOTSUP,
+                "w8a8: BLOCK_N=%d must be 16, 32, 64 or 128", block_n);
+  const int rows16 = ceil_div(m_grid > 0 ? m_grid : 1, 16);
   int mt;
   if (block_m > 0) {
     SPECQ_REQUIRE(block_m % 16 == 0 && block_m <= 320, SPECQ_ENOTSUP,
                   "w8a8: BLOCK_M=%d must be a multiple of 16 and at most 320", block_m);
     mt = block_m / 16;
   } else {
-    int chunks = ceil_div(rows16, 20);
+    const int chunks = ceil_div(rows16, 20);
     mt = ceil_div(rows16, chunks);
   }
-  int rw;
-  if (block_n > 0) {
-    SPECQ_REQUIRE(block_n == 16 || block_n == 32 || block_n == 64, SPECQ_ENOTSUP,
-                  "w8a8: BLOCK_N=%d must be 16, 32 or 64", block_n);
-    rw = block_n / 16;
-  } else {
-    rw = N <= 16 ? 1 : 2;
-  }
-  while (rw > 1 && rw * mt > 40) rw >>= 1;
-  int mt_eff = round_mt_for_vec(mt, vec, rw);
-  if (mt_eff < 0 && rw > 1) { rw = 1; mt_eff = round_mt_for_vec(mt, vec, rw); }
-  SPECQ_REQUIRE(mt_eff > 0, SPECQ_ENOTSUP, "w8a8: no kernel for BLOCK_M=%d at %d-byte alignment", mt * 16, vec);
-  mt = mt_eff;
   int nw = num_warps <= 0 ? 4 : (num_warps >= 4 ? 4 : (num_warps >= 2 ? 2 : 1));
+  const int path = g_w8a8_path.load();
+  int family;
+  if (layout == 1) family = kStream;
+  else if (vec != 16) family = kLegacy;
+  else family = (path == kDma || path == kLegacy) ? path : kStream;
 
-  cfg->mt = mt; cfg->rw = rw; cfg->nw = nw; cfg->vec = vec;
-  cfg->n_tiles = ceil_div(N, rw * 16);
+  int rw = 1, nwn = 1, dma_lds = 0;
+  const void* fn = nullptr;
+  if (family == kDma) {
+    // 4 waves: NWN along N (RW x 16 channels each), 4/NWN along K.
+    const int bn = block_n > 0 ? block_n : (N <= 2048 ? 16 : 64);
+    if (bn == 16) { rw = 1; nwn = 1; }
+    else if (bn == 32) { rw = num_warps == 2 ? 2 : 1; nwn = num_warps == 2 ? 1 : 2; }
+    else if (bn == 64) { rw = num_warps == 2 ? 2 : 1; nwn = num_warps == 2 ? 2 : 4; }
+    else { rw = 2; nwn = 4; }
+    nw = 4;
+    fn = dma_fn(mt, rw, nwn, &dma_lds);
+    if (!fn) { rw = 1; nwn = 1; fn = dma_fn(mt, rw, nwn, &dma_lds); }  // deepest M tiles
+    if (!fn) family = kStream;                                          // BLOCK_M > 288
+  }
+  if (family == kStream) {
+    rw = (block_n >= 32) ? 2 : (block_n == 16 ? 1 : (N <= 2048 ? 1 : 2));
+    fn = stream_fn(layout, mt, rw);
+  }
+  if (family == kLegacy) {
+    rw = block_n > 0 ? (block_n >= 64 ? 4 : block_n / 16) : (N <= 16 ? 1 : 2);
+    while (rw > 1 && rw * mt > 40) rw >>= 1;
+    int mt_eff = round_mt_for_vec(mt, vec, rw);
+    if (mt_eff < 0 && rw > 1) { rw = 1; mt_eff = round_mt_for_vec(mt, vec, rw); }
+    SPECQ_REQUIRE(mt_eff > 0, SPECQ_ENOTSUP, "w8a8: no kernel for BLOCK_M=%d at %d-byte alignment", mt * 16, vec);
+    mt = mt_eff;
+    fn = legacy_fn(mt, rw, vec);
+  }
+  SPECQ_REQUIRE(fn != nullptr, SPECQ_ENOTSUP, "w8a8: no kernel for BLOCK_M=%d BLOCK_N=%d", mt * 16, block_n);
+
+  cfg->family = family; cfg->layout = layout; cfg->fn = fn;
+  cfg->mt = mt; cfg->rw = rw; cfg->nw = nw; cfg->vec = vec; cfg->nwn = nwn;
+  cfg->bn = family == kDma ? nwn * rw * 16 : rw * 16;
+  cfg->n_tiles = ceil_div(N, cfg->bn);
   cfg->m_chunks = ceil_div(m_grid > 0 ? m_grid : 1, mt * 16);
+  const int BM = mt * 16, BN = cfg->bn;
+  if (family == kDma) {
+    cfg->lds = (size_t)dma_lds;
+  } else if (family == kStream) {
+    const size_t stage = layout == 0 ? (size_t)nw * rw * 4096 : 0;
+    const size_t red = nw > 1 ? (size_t)BM * (BN + kW8A8Pad) * 4 : 0;
+    cfg->lds = stage > red ? stage : red;
+  } else {
+    cfg->lds = nw > 1 ? (size_t)BM * (BN + kW8A8Pad) * 4 : 0;
+  }
+
   const int ksteps = ceil_div(K, 64);
   int splits;
   if (split_k > 0) {
     splits = split_k;
   } else {
-    // Aim for about two resident workgroups per CU, and keep at least 2 K steps per wave.
-    const int target = 2 * device_cus();
+    // Fill the CUs: about two resident workgroups per CU (LDS permitting), >= 2 K steps per wave.
+    const int per_cu = family == kDma ? (dma_lds > 0 ? std::max(1, 163840 / dma_lds) : 1) : 2;
+    const int target = per_cu * device_cus();
     const int base = cfg->n_tiles * cfg->m_chunks;
     splits = base >= target ? 1 : ceil_div(target, base);
     int max_splits = ksteps / (2 * nw);
     if (max_splits < 1) max_splits = 1;
     if (splits > max_splits) splits = max_splits;
   }
-  if (splits > ksteps) splits = ksteps;
-  int k_range = ceil_div(ksteps, splits) * 64;
+  // Split boundaries on whole 256-byte blocks keep the streaming kernel's fetches aligned.
+  const int quantum = family == kStream ? 4 : 1;
+  const int kq = ceil_div(ksteps, quantum);
+  if (splits > kq) splits = kq;
+  const int k_range = ceil_div(kq, splits) * quantum * 64;
   splits = ceil_div(K, k_range);
   cfg->splits = splits;
   cfg->k_range = k_range;
-  const int BM = mt * 16, BN = rw * 16;
-  cfg->lds = nw > 1 ? (size_t)BM * (BN + kW8A8Pad) * 4 : 0;
   cfg->ws_partials = splits > 1 ? align_up((size_t)cfg->m_chunks * cfg->n_tiles * splits * BM * BN * 4, 256) : 0;
   cfg->ws_counters = splits > 1 ? kCounterBytes : 0;
   SPECQ_REQUIRE((int64_t)cfg->m_chunks * cfg->n_tiles <= kMaxCounters, SPECQ_ENOTSUP,
                 "w8a8: %d x %d tiles exceed the counter region", cfg->m_chunks, cfg->n_tiles);
-  cfg->fn = w8a8_fn(mt, rw, vec);
-  SPECQ_REQUIRE(cfg->fn != nullptr, SPECQ_ENOTSUP, "w8a8: kernel MT=%d RW=%d VEC=%d not built", mt, rw, vec);
   return SPECQ_OK;
+}
+
+int run_w8a8(int layout, const int8_t* a, int64_t lda, const void* w, int64_t ldw, const float* sa, const float* sw,
+             void* c, int64_t ldc, int M, int N, int K, int grid_m_max, const int32_t* plan, int block_m, int block_n,
+             int num_warps, int split_k, void* workspace, size_t workspace_bytes, void* stream) {
+  SPECQ_REQUIRE(M >= 0 && N > 0 && K > 0, SPECQ_EINVAL, "w8a8: bad sizes M=%d N=%d K=%d", M, N, K);
+  SPECQ_REQUIRE(a && w && sa && sw && c, SPECQ_EINVAL, "w8a8: null tensor pointer");
+  SPECQ_REQUIRE(lda >= K && (layout == 1 || ldw >= K) && ldc >= N, SPECQ_EINVAL,
+                "w8a8: row strides must cover a row (lda=%lld ldw=%lld ldc=%lld)", (long long)lda, (long long)ldw,
+                (long long)ldc);
+  SPECQ_REQUIRE(grid_m_max == 0 || grid_m_max >= M, SPECQ_EINVAL, "w8a8: grid_m_max=%d < M=%d", grid_m_max, M);
+  const int m_grid = grid_m_max > 0 ? grid_m_max : M;
+  if (m_grid == 0) return SPECQ_OK;
+  int vec = common_vec({(uint64_t)(uintptr_t)a, (uint64_t)lda, (uint64_t)K});
+  if (layout == 0) vec = std::min(vec, common_vec({(uint64_t)(uintptr_t)w, (uint64_t)ldw}));
+  SPECQ_REQUIRE(layout == 0 || vec == 16, SPECQ_ENOTSUP,
+                "w8a8: packed weights need 16-byte aligned activations and K %% 16 == 0");
+  SPECQ_REQUIRE(layout == 0 || (uintptr_t)w % 16 == 0, SPECQ_EINVAL, "w8a8: misaligned packed weight");
+  W8A8Cfg cfg;
+  int rc = w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, vec, &cfg);
+  if (rc) return rc;
+  const size_t need = cfg.ws_partials + cfg.ws_counters;
+  SPECQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), SPECQ_ENOSPC,
+                "w8a8: workspace of %zu bytes required, %zu given", need, workspace ? workspace_bytes : 0);
+  rc = ensure_lds(cfg.fn, cfg.lds);
+  if (rc) return rc;
+  W8A8Params p;
+  p.A = a; p.lda = lda; p.W = (const int8_t*)w; p.ldw = ldw; p.sa = sa; p.sw = sw;
+  p.C = reinterpret_cast<__half*>(c); p.ldc = ldc; p.plan = plan;
+  p.M = M; p.N = N; p.K = K; p.m_grid = m_grid;
+  p.n_tiles = cfg.n_tiles; p.m_chunks = cfg.m_chunks; p.splits = cfg.splits; p.k_range = cfg.k_range;
+  p.counters = need ? reinterpret_cast<int32_t*>(workspace) : nullptr;
+  p.partials = need ? reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + kCounterBytes) : nullptr;
+  p.vec_store = ((uintptr_t)c % 8 == 0) && (ldc % 4 == 0) && ((uintptr_t)sw % 16 == 0);
+  const int grid = cfg.m_chunks * cfg.n_tiles * cfg.splits;
+  return launch(cfg.fn, grid, cfg.nw * 64, cfg.lds, reinterpret_cast<hipStream_t>(stream), &p);
+}
+
+size_t workspace_size(int layout, int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k) {
+  W8A8Cfg cfg;
+  size_t best = 0;
+  // Size for every alignment class the call could resolve to.
+  for (int vec : {16, 1}) {
+    if (layout == 1 && vec != 16) continue;
+    if (w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, vec, &cfg) == SPECQ_OK) {
+      const size_t s = cfg.ws_partials + cfg.ws_counters;
+      if (s > best) best = s;
+    }
+  }
+  clear_error();
+  return best;
 }
 
 }  // namespace
@@ -100,17 +262,22 @@ int w8a8_config(int m_grid, int N, int K, int block_m, int block_n, int num_warp
 int w8a8_attrs(int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k,
                specq_kernel_attrs* out) {
   W8A8Cfg cfg;
-  int rc = w8a8_config(m_grid, N, K, block_m, block_n, num_warps, split_k, 16, &cfg);
+  int rc = w8a8_config(0, m_grid, N, K, block_m, block_n, num_warps, split_k, 16, &cfg);
   if (rc) return rc;
   hipFuncAttributes fa;
   if (hipFuncGetAttributes(&fa, cfg.fn) != hipSuccess) return fail(SPECQ_EIO, "w8a8: hipFuncGetAttributes failed");
-  snprintf(out->name, sizeof(out->name), "specq::w8a8_kernel<%d,%d,%d>", cfg.mt, cfg.rw, cfg.vec);
+  if (cfg.family == kDma)
+    snprintf(out->name, sizeof(out->name), "specq::w8a8_dma_kernel<%d,%d,%d>", cfg.mt, cfg.rw, cfg.nwn);
+  else if (cfg.family == kStream)
+    snprintf(out->name, sizeof(out->name), "specq::w8a8_stream_kernel<%d,%d,%d>", cfg.mt, cfg.rw, cfg.layout);
+  else
+    snprintf(out->name, sizeof(out->name), "specq::w8a8_kernel<%d,%d,%d>", cfg.mt, cfg.rw, cfg.vec);
   out->num_regs = fa.numRegs;
   out->lds_bytes = (int)(fa.sharedSizeBytes + cfg.lds);
   out->scratch_bytes = (int)fa.localSizeBytes;
   out->threads = cfg.nw * 64;
   out->grid = cfg.m_chunks * cfg.n_tiles * cfg.splits;
-  out->block_m = cfg.mt * 16; out->block_n = cfg.rw * 16; out->num_warps = cfg.nw; out->split_k = cfg.splits;
+  out->block_m = cfg.mt * 16; out->block_n = cfg.bn; out->num_warps = cfg.nw; out->split_k = cfg.splits;
   return SPECQ_OK;
 }
 
@@ -120,18 +287,7 @@ using namespace specq;
 
 extern "C" size_t specq_w8a8_workspace_size(int m_grid, int N, int K, int block_m, int block_n, int num_warps,
                                             int split_k) {
-  W8A8Cfg cfg;
-  // Sub-16-byte alignments only ever round MT up, which can only shrink the split count's
-  // base; size for the worst case over the alignments.
-  size_t best = 0;
-  for (int vec : {16, 1}) {
-    if (w8a8_config(m_grid, N, K, block_m, block_n, num_warps, split_k, vec, &cfg) == SPECQ_OK) {
-      size_t s = cfg.ws_partials + cfg.ws_counters;
-      if (s > best) best = s;
-    }
-  }
-  clear_error();
-  return best;
+  return workspace_size(0, m_grid, N, K, block_m, block_n, num_warps, split_k);
 }
 
 extern "C" int specq_w8a8(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, const float* sa,
@@ -139,30 +295,55 @@ extern "C" int specq_w8a8(const int8_t* a, int64_t lda, const int8_t* w, int64_t
                           const int32_t* plan, int block_m, int block_n, int num_warps, int split_k,
                           void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
-  SPECQ_REQUIRE(M >= 0 && N > 0 && K > 0, SPECQ_EINVAL, "w8a8: bad sizes M=%d N=%d K=%d", M, N, K);
-  SPECQ_REQUIRE(a && w && sa && sw && c, SPECQ_EINVAL, "w8a8: null tensor pointer");
-  SPECQ_REQUIRE(lda >= K && ldw >= K && ldc >= N, SPECQ_EINVAL,
-                "w8a8: row strides must cover a row (lda=%lld ldw=%lld ldc=%lld)", (long long)lda,
-                (long long)ldw, (long long)ldc);
-  SPECQ_REQUIRE(grid_m_max == 0 || grid_m_max >= M, SPECQ_EINVAL, "w8a8: grid_m_max=%d < M=%d", grid_m_max, M);
-  const int m_grid = grid_m_max > 0 ? grid_m_max : M;
-  if (m_grid == 0) return SPECQ_OK;
-  const int vec = common_vec({(uint64_t)(uintptr_t)a, (uint64_t)(uintptr_t)w, (uint64_t)lda, (uint64_t)ldw,
-                              (uint64_t)K});
-  W8A8Cfg cfg;
-  int rc = w8a8_config(m_grid, N, K, block_m, block_n, num_warps, split_k, vec, &cfg);
-  if (rc) return rc;
-  const size_t need = cfg.ws_partials + cfg.ws_counters;
-  SPECQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), SPECQ_ENOSPC,
-                "w8a8: workspace of %zu bytes required, %zu given", need, workspace ? workspace_bytes : 0);
-  W8A8Params p;
-  p.A = a; p.lda = lda; p.W = w; p.ldw = ldw; p.sa = sa; p.sw = sw;
-  p.C = reinterpret_cast<__half*>(c); p.ldc = ldc; p.plan = plan;
-  p.M = M; p.N = N; p.K = K; p.m_grid = m_grid;
-  p.n_tiles = cfg.n_tiles; p.m_chunks = cfg.m_chunks; p.splits = cfg.splits; p.k_range = cfg.k_range;
-  p.counters = need ? reinterpret_cast<int32_t*>(workspace) : nullptr;
-  p.partials = need ? reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + kCounterBytes) : nullptr;
-  p.vec_store = ((uintptr_t)c % 8 == 0) && (ldc % 4 == 0) && ((uintptr_t)sw % 16 == 0);
-  const int grid = cfg.m_chunks * cfg.n_tiles * cfg.splits;
-  return launch(cfg.fn, grid, cfg.nw * 64, cfg.lds, reinterpret_cast<hipStream_t>(stream), &p);
+  return run_w8a8(0, a, lda, w, ldw, sa, sw, c, ldc, M, N, K, grid_m_max, plan, block_m, block_n, num_warps,
+                  split_k, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t specq_w8a8_packed_bytes(int N, int K) {
+  if (N <= 0 || K <= 0) return 0;
+  return (size_t)ceil_div(N, 16) * ceil_div(K, 64) * 1024;
+}
+
+extern "C" int specq_w8a8_pack_weight(const int8_t* w, int64_t ldw, int N, int K, void* packed, void* stream) {
+  clear_error();
+  SPECQ_REQUIRE(w && packed, SPECQ_EINVAL, "w8a8_pack_weight: null tensor pointer");
+  SPECQ_REQUIRE(N > 0 && K > 0 && ldw >= K, SPECQ_EINVAL, "w8a8_pack_weight: bad sizes N=%d K=%d ldw=%lld", N, K,
+                (long long)ldw);
+  SPECQ_REQUIRE((uintptr_t)packed % 16 == 0, SPECQ_EINVAL, "w8a8_pack_weight: misaligned output");
+  const int64_t frags = (int64_t)ceil_div(N, 16) * ceil_div(K, 64);
+  SPECQ_REQUIRE(ceil_div64(frags, 4) <= INT32_MAX, SPECQ_ENOTSUP, "w8a8_pack_weight: weight too large");
+  void* args[] = {(void*)&w, (void*)&ldw, (void*)&N, (void*)&K, (void*)&packed};
+  hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&w8a8_pack_kernel),
+                                 dim3((unsigned)ceil_div64(frags, 4)), dim3(256), args, 0, (hipStream_t)stream);
+  if (e != hipSuccess) {
+    set_error("w8a8_pack_weight: hipLaunchKernel failed: %s", hipGetErrorString(e));
+    return SPECQ_EIO;
+  }
+  return SPECQ_OK;
+}
+
+extern "C" size_t specq_w8a8_packed_workspace_size(int m_grid, int N, int K, int block_m, int block_n,
+                                                   int num_warps, int split_k) {
+  return workspace_size(1, m_grid, N, K, block_m, block_n, num_warps, split_k);
+}
+
+extern "C" int specq_w8a8_packed(const int8_t* a, int64_t lda, const void* w_packed, const float* sa,
+                                 const float* sw, void* c, int64_t ldc, int M, int N, int K, int grid_m_max,
+                                 const int32_t* plan, int block_m, int block_n, int num_warps, int split_k,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  return run_w8a8(1, a, lda, w_packed, 0, sa, sw, c, ldc, M, N, K, grid_m_max, plan, block_m, block_n, num_warps,
+                  split_k, workspace, workspace_bytes, stream);
+}
+
+extern "C" int specq_set_option(const char* name, int value) {
+  clear_error();
+  SPECQ_REQUIRE(name != nullptr, SPECQ_EINVAL, "set_option: null name");
+  if (strcmp(name, "w8a8_path") == 0) {
+    SPECQ_REQUIRE(value >= 0 && value <= 3, SPECQ_EINVAL, "set_option: w8a8_path must be 0..3");
+    g_w8a8_path.store(value);
+    return SPECQ_OK;
+  }
+  set_error("set_option: unknown option '%s'", name);
+  return SPECQ_EINVAL;
 }

@@ -29,6 +29,49 @@ __device__ __forceinline__ int wave_id() { return threadIdx.x / kWave; }
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 // ---------------------------------------------------------------------------------------
+// Raw buffer loads with hardware range checking.
+//
+// A buffer resource covers one workgroup's slab of a matrix (num_records bytes from its
+// first row).  Lanes whose offset is >= num_records read zeros, so rows past the end of the
+// matrix and K positions past the end of a row are masked without branches: the masked lane
+// is handed the offset kOOB.  Keeping loads free of control flow lets the compiler count
+// outstanding loads exactly (vmcnt), which is what makes register double-buffering work.
+// ---------------------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOOB = 0x80000000u;
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer descriptor (32-bit data format)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t num_records) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)num_records, kRsrcWord3);
+}
+
+// 16 bytes at row_off + k of the slab; VEC-byte pieces at or beyond kend read as zero.
+template <int VEC>
+__device__ __forceinline__ v4i bload16(rsrc_t rs, uint32_t row_off, int k, int kend) {
+  if constexpr (VEC == 16) {
+    return __builtin_amdgcn_raw_buffer_load_b128(rs, k < kend ? row_off + k : kOOB, 0, 0);
+  } else if constexpr (VEC == 8) {
+    const auto lo = __builtin_amdgcn_raw_buffer_load_b64(rs, k < kend ? row_off + k : kOOB, 0, 0);
+    const auto hi = __builtin_amdgcn_raw_buffer_load_b64(rs, k + 8 < kend ? row_off + k + 8 : kOOB, 0, 0);
+    return v4i{(int)lo[0], (int)lo[1], (int)hi[0], (int)hi[1]};
+  } else if constexpr (VEC == 4) {
+    v4i r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      r[i] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs, k + 4 * i < kend ? row_off + k + 4 * i : kOOB, 0, 0);
+    return r;
+  } else {
+    int w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int b = __builtin_amdgcn_raw_buffer_load_b8(rs, k + i < kend ? row_off + k + i : kOOB, 0, 0);
+      w[i >> 2] |= (b & 0xff) << (8 * (i & 3));
+    }
+    return v4i{w[0], w[1], w[2], w[3]};
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // 16-byte operand loads with K-tail masking at VEC-byte granularity.
 // VEC is the largest power of two (<=16) dividing K, the row stride and the base pointer,
 // so a VEC chunk is either entirely inside [0, K) or entirely outside it.
@@ -89,5 +132,51 @@ __device__ __forceinline__ v8h i8x8_to_h8(uint32_t x0, uint32_t x1) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------------------
+// Cross-workgroup hand-off without cache-wide fences.
+//
+// A split reduction publishes partial results that the last workgroup to arrive combines.
+// An agent-scope release/acquire fence would write back and invalidate the whole L2 of the
+// XCD (buffer_wbl2 / buffer_inv), which serialises across the XCD's workgroups and costs
+// microseconds per call.  Instead every published value is written with an agent-scope
+// atomic store (coherent at device scope, so nothing dirty stays behind in a non-coherent
+// cache), the writer waits until those stores have completed (s_waitcnt vmcnt(0)) before it
+// increments the arrival counter, and the consumer reads the values with agent-scope atomic
+// loads after observing the final count.  This is the ordering the compiler's memory model
+// produces for release/acquire, without the cache-wide maintenance that is only needed for
+// ordinary (non-atomic) data.
+// ---------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void publish(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T collect(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// All of this wave's outstanding memory operations have completed.
+__device__ __forceinline__ void wait_all_memory() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// Called by every thread after the workgroup's publish() calls: returns true in the last
+// workgroup to arrive (of `expected`) at counter `ctr`, which is then reset to zero.
+// The caller reads the published values with collect() only when this returns true.
+__device__ __forceinline__ bool arrive_last(int32_t* ctr, int expected, int* s_flag) {
+  wait_all_memory();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = (prev == expected - 1);
+    if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = last;
+  }
+  __syncthreads();
+  const bool last = *s_flag != 0;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  return last;
+}
 
 }  // namespace specq

@@ -335,42 +335,37 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
   const int64_t prog_base = (int64_t)prog * p.n_splits;
   float* opart = p.part;
   float* mlpart = p.part + (int64_t)gridDim.y * gridDim.z * p.n_splits * ROWS * D;
-  for (int e = threadIdx.x; e < ROWS * (D / 4); e += blockDim.x) {
-    const int row = e / (D / 4), d0 = (e % (D / 4)) * 4;
-    v4f v = {o_lds[row][d0], o_lds[row][d0 + 1], o_lds[row][d0 + 2], o_lds[row][d0 + 3]};
-    *reinterpret_cast<v4f*>(opart + ((prog_base + split) * ROWS + row) * D + d0) = v;
+  for (int e = threadIdx.x; e < ROWS * D; e += blockDim.x) {
+    const int row = e / D, d = e % D;
+    publish(opart + ((prog_base + split) * ROWS + row) * D + d, o_lds[row][d]);
   }
   if (threadIdx.x < ROWS) {
     float* mlp = mlpart + ((prog_base + split) * ROWS + threadIdx.x) * 2;
-    mlp[0] = ml_lds[0][0][threadIdx.x];
-    mlp[1] = ml_lds[0][1][threadIdx.x];
+    publish(mlp, ml_lds[0][0][threadIdx.x]);
+    publish(mlp + 1, ml_lds[0][1][threadIdx.x]);
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = (atomicAdd(p.counters + prog, 1) == n_active - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+  if (!arrive_last(p.counters + prog, n_active, &s_last)) return;
   for (int e = threadIdx.x; e < ROWS * DCH; e += blockDim.x) {
     const int row = e / DCH, d0 = (e % DCH) * 8;
     const int qi = qc * p.QPP + row / G;
     if (!(row < p.QPP * G && qi < q_len)) continue;
     const int head = kvh * G + row % G;
     float mx = -INFINITY;
-    for (int s = 0; s < n_active; ++s)
-      mx = fmaxf(mx, __builtin_nontemporal_load(mlpart + ((prog_base + s) * ROWS + row) * 2));
+    for (int s = 0; s < n_active; ++s) mx = fmaxf(mx, collect(mlpart + ((prog_base + s) * ROWS + row) * 2));
     const float ms = (mx == -INFINITY) ? 0.f : mx;
-    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float o[8];
     float l = 0.f;
     for (int s = 0; s < n_active; ++s) {
       const float* mlp = mlpart + ((prog_base + s) * ROWS + row) * 2;
-      const float ws = fast_exp2(__builtin_nontemporal_load(mlp) - ms);
-      l += ws * __builtin_nontemporal_load(mlp + 1);
+      const float ws = fast_exp2(collect(mlp) - ms);
+      const float ls = ws * collect(mlp + 1);
+      l = (s == 0) ? ls : l + ls;
       const float* op = opart + ((prog_base + s) * ROWS + row) * D + d0;
-      const v4f a = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(op));
-      const v4f c = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(op + 4));
-      o[0] += ws * a.x; o[1] += ws * a.y; o[2] += ws * a.z; o[3] += ws * a.w;
-      o[4] += ws * c.x; o[5] += ws * c.y; o[6] += ws * c.z; o[7] += ws * c.w;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = ws * collect(op + i);
+        o[i] = (s == 0) ? v : o[i] + v;
+      }
     }
     const float inv = (l == 0.f) ? 0.f : 1.f / l;
     v8h out;
@@ -378,7 +373,6 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
     for (int i = 0; i < 8; ++i) out[i] = (_Float16)(o[i] * inv);
     *reinterpret_cast<v8h*>(p.out + (int64_t)b * p.s_ob + (int64_t)qi * p.s_ot + (int64_t)head * p.s_oh + d0) = out;
   }
-  if (threadIdx.x == 0) atomicExch(p.counters + prog, 0);
 }
 
 }  // namespace specq

@@ -242,26 +242,24 @@ __global__ __launch_bounds__(256) void w4a16_kernel(W4A16Params p) {
     for (int i = 0; i < RW; ++i)
 #pragma unroll
       for (int j = 0; j < MT; ++j)
-        *reinterpret_cast<v4f*>(mine + (j * 16 + r) * BN + w * BNW + i * 16 + 4 * g) = acc[i][j];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) publish(mine + (j * 16 + r) * BN + w * BNW + i * 16 + 4 * g + c, acc[i][j][c]);
   }
   __shared__ int s_last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = (atomicAdd(p.counters + cidx, 1) == p.splits - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+  if (!arrive_last(p.counters + cidx, p.splits, &s_last)) return;
   const int quads = BM * BN / 4;
   for (int q = threadIdx.x; q < quads; q += blockDim.x) {
     const int ml = q / (BN / 4), nl = (q % (BN / 4)) * 4;
     const int m = m0 + ml, n = tile * BN + nl;
     if (m >= M || n >= p.N) continue;
-    v4f s = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(base + ml * BN + nl));
-    for (int sp = 1; sp < p.splits; ++sp)
-      s += __builtin_nontemporal_load(reinterpret_cast<const v4f*>(base + (int64_t)sp * (BM * BN) + ml * BN + nl));
+    v4f s = {0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < p.splits; ++sp) {
+      const float* src = base + (int64_t)sp * (BM * BN) + ml * BN + nl;
+      const v4f t = {collect(src), collect(src + 1), collect(src + 2), collect(src + 3)};
+      if (sp == 0) s = t; else s += t;
+    }
     store4(m, n, s);
   }
-  if (threadIdx.x == 0) atomicExch(p.counters + cidx, 0);
 }
 
 }  // namespace specq

@@ -14,10 +14,11 @@
 //  * The waves of a workgroup split its K range (interleaved 64-byte steps, so the waves of
 //    one workgroup read adjacent memory), then reduce their accumulators through LDS.
 //  * To fill 256 CUs the K range is further split across workgroups (split-K).  INT32 sums are
-//    order independent, so the split is exact by construction: each split writes its INT32
-//    partial tile, and the last workgroup to arrive (agent-scope atomic counter) sums the
-//    partials, applies the epilogue and resets the counter, so the workspace needs no memset
-//    between calls and the kernel is legal inside a captured graph.
+//    order independent, so the split is exact by construction: each split publishes its INT32
+//    partial tile with device-coherent stores, and the last workgroup to arrive (agent-scope
+//    atomic counter, no cache-wide fence) sums the partials, applies the epilogue and resets
+//    the counter, so the workspace needs no memset between calls and the kernel is legal
+//    inside a captured graph.
 //  * Plan mode: the active M is read from a device int32 (plan[0]) and clamped to the rows
 //    the grid was sized for; M-chunks at or beyond it exit before touching memory, so one
 //    graph captured at the maximum grid replays every M and never writes rows >= M.
@@ -43,17 +44,12 @@ struct W8A8Params {
 
 constexpr int kW8A8Pad = 4;  // int32 padding per LDS row
 
-template <int MT>
-struct W8A8Unroll { static constexpr int value = MT <= 2 ? 4 : (MT <= 6 ? 2 : 1); };
-
-template <int MT, int RW, int VEC>
-__device__ __forceinline__ void w8a8_load_step(const int8_t* const (&wrow)[RW], const int8_t* const (&arow)[MT],
-                                               int koff, int kend, v4i (&wf)[RW], v4i (&af)[MT]) {
-#pragma unroll
-  for (int i = 0; i < RW; ++i) wf[i] = load16_masked<VEC>(wrow[i], koff, kend);
-#pragma unroll
-  for (int j = 0; j < MT; ++j) af[j] = load16_masked<VEC>(arow[j], koff, kend);
-}
+// K steps per register batch: about 160 VGPRs of double-buffered operands, at most 8.
+template <int MT, int RW>
+struct W8A8Unroll {
+  static constexpr int raw = 20 / (MT + RW);
+  static constexpr int value = raw < 1 ? 1 : (raw > 8 ? 8 : raw);
+};
 
 template <int MT, int RW>
 __device__ __forceinline__ void w8a8_mma_step(const v4i (&wf)[RW], const v4i (&af)[MT], v4i (&acc)[RW][MT]) {
@@ -85,7 +81,7 @@ __device__ __forceinline__ void w8a8_store4(const W8A8Params& p, int m, int n, v
 
 template <int MT, int RW, int VEC>
 __global__ __launch_bounds__(256) void w8a8_kernel(W8A8Params p) {
-  constexpr int BM = MT * 16, BN = RW * 16, U = W8A8Unroll<MT>::value;
+  constexpr int BM = MT * 16, BN = RW * 16, U = W8A8Unroll<MT, RW>::value;
   constexpr int LDW = BN + kW8A8Pad;  // LDS row pitch in int32
   extern __shared__ int32_t smem[];
 
@@ -106,12 +102,16 @@ __global__ __launch_bounds__(256) void w8a8_kernel(W8A8Params p) {
   const int ke = min(p.K, kb + p.k_range);
   const int lane = lane_id(), w = wave_id(), g = lane >> 4, r = lane & 15;
 
-  const int8_t* wrow[RW];
-  const int8_t* arow[MT];
+  // Buffer resources over this workgroup's slabs: rows past N (or past the active M) and
+  // K positions past the split read as zero, with no branches around the loads.
+  const int n_rows = min(BN, p.N - n0), m_rows = min(BM, M - m0);
+  const rsrc_t wsrc = make_rsrc(p.W + (int64_t)n0 * p.ldw, (uint32_t)((n_rows - 1) * p.ldw + p.K));
+  const rsrc_t asrc = make_rsrc(p.A + (int64_t)m0 * p.lda, (uint32_t)((m_rows - 1) * p.lda + p.K));
+  uint32_t woff[RW], aoff[MT];
 #pragma unroll
-  for (int i = 0; i < RW; ++i) wrow[i] = p.W + (int64_t)min(n0 + i * 16 + r, p.N - 1) * p.ldw;
+  for (int i = 0; i < RW; ++i) woff[i] = (i * 16 + r < n_rows) ? (uint32_t)((i * 16 + r) * p.ldw) : kOOB;
 #pragma unroll
-  for (int j = 0; j < MT; ++j) arow[j] = p.A + (int64_t)min(m0 + j * 16 + r, M - 1) * p.lda;
+  for (int j = 0; j < MT; ++j) aoff[j] = (j * 16 + r < m_rows) ? (uint32_t)((j * 16 + r) * p.lda) : kOOB;
 
   v4i acc[RW][MT];
 #pragma unroll
@@ -129,20 +129,28 @@ __global__ __launch_bounds__(256) void w8a8_kernel(W8A8Params p) {
   v4i wa[U][RW], aa[U][MT], wb[U][RW], ab[U][MT];
   auto load_batch = [&](int b, v4i (&wv)[U][RW], v4i (&av)[U][MT]) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      w8a8_load_step<MT, RW, VEC>(wrow, arow, k_first + (b * U + u) * stride, ke, wv[u], av[u]);
+    for (int u = 0; u < U; ++u) {
+      const int k = k_first + (b * U + u) * stride;
+#pragma unroll
+      for (int i = 0; i < RW; ++i) wv[u][i] = bload16<VEC>(wsrc, woff[i], k, ke);
+#pragma unroll
+      for (int j = 0; j < MT; ++j) av[u][j] = bload16<VEC>(asrc, aoff[j], k, ke);
+    }
   };
   auto mma_batch = [&](v4i (&wv)[U][RW], v4i (&av)[U][MT]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) w8a8_mma_step<MT, RW>(wv[u], av[u], acc);
   };
 
-  if (nbatch > 0) load_batch(0, wa, aa);
+  // The loop body has no branches: batches past this wave's range (the odd tail and the
+  // prefetch beyond the end) read zeros through the range check and add nothing, so the
+  // compiler can keep exactly one batch of loads in flight behind each batch of MFMAs.
+  load_batch(0, wa, aa);
   for (int b = 0; b < nbatch; b += 2) {
-    if (b + 1 < nbatch) load_batch(b + 1, wb, ab);
+    load_batch(b + 1, wb, ab);
     mma_batch(wa, aa);
-    if (b + 2 < nbatch) load_batch(b + 2, wa, aa);
-    if (b + 1 < nbatch) mma_batch(wb, ab);
+    load_batch(b + 2, wa, aa);
+    mma_batch(wb, ab);
   }
 
   // Cross-wave reduction through one LDS slice [BM][LDW]: waves nw-1 .. 1 each deposit their
@@ -181,7 +189,7 @@ __global__ __launch_bounds__(256) void w8a8_kernel(W8A8Params p) {
     return;
   }
 
-  // Split-K fix-up: every split stores its INT32 tile ([BM][BN], row = token); the last
+  // Split-K fix-up: every split publishes its INT32 tile ([BM][BN], row = token); the last
   // workgroup of this (M-chunk, N-tile) to arrive sums all splits and applies the epilogue.
   int32_t* base = p.partials + (int64_t)cidx * p.splits * (BM * BN);
   if (w == 0) {
@@ -190,29 +198,23 @@ __global__ __launch_bounds__(256) void w8a8_kernel(W8A8Params p) {
     for (int i = 0; i < RW; ++i)
 #pragma unroll
       for (int j = 0; j < MT; ++j)
-        *reinterpret_cast<v4i*>(mine + (j * 16 + r) * BN + i * 16 + 4 * g) = acc[i][j];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) publish(mine + (j * 16 + r) * BN + i * 16 + 4 * g + c, acc[i][j][c]);
   }
   __shared__ int s_last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = atomicAdd(p.counters + cidx, 1);
-    s_last = (prev == p.splits - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+  if (!arrive_last(p.counters + cidx, p.splits, &s_last)) return;
   constexpr int QUADS = BM * BN / 4;
   for (int q = threadIdx.x; q < QUADS; q += blockDim.x) {
     const int ml = q / (BN / 4), nl = (q % (BN / 4)) * 4;
     const int m = m0 + ml, n = n0 + nl;
     if (m >= M || n >= p.N) continue;
     v4i s = {0, 0, 0, 0};
-    for (int sp = 0; sp < p.splits; ++sp)
-      s += __builtin_nontemporal_load(reinterpret_cast<const v4i*>(base + (int64_t)sp * (BM * BN) + ml * BN + nl));
+    for (int sp = 0; sp < p.splits; ++sp) {
+      const int32_t* src = base + (int64_t)sp * (BM * BN) + ml * BN + nl;
+      s += v4i{collect(src), collect(src + 1), collect(src + 2), collect(src + 3)};
+    }
     w8a8_store4(p, m, n, s);
   }
-  if (threadIdx.x == 0) atomicExch(p.counters + cidx, 0);
 }
 
 }  // namespace specq

@@ -24,8 +24,10 @@ reference) restate the reference formulas in torch and run on any device.
 Differences a caller may notice:
   * BLOCK_K and num_stages are accepted and ignored (the MFMA K step and register
     pipelining are fixed per kernel).  BLOCK_M=None (or 0) picks the tile from the measured
-    M staircase.  W8A8 BLOCK_N is 16/32/64 channels per workgroup (larger values are taken
-    as 64); W4A16 BLOCK_N is 64 or 128.
+    M staircase.  W8A8 BLOCK_N is 16/32/64/128 channels per workgroup (larger values are taken
+    as 128); W4A16 BLOCK_N is 64 or 128.
+  * w8a8_matmul also accepts a PackedWeightInt8 (pack_weight_int8), the weight pre-packed
+    once into MFMA fragments, with bit-identical results.
   * `ck` is a KernelInfo with n_regs / n_spills / metadata.shared like Triton's compiled
     kernel, plus the resolved tile configuration.
   * w4a16_matmul also accepts the int32 "8 nibbles per word along K" packing.
@@ -51,7 +53,7 @@ __all__ = [
     "quantize_act_int8", "quantize_weight_int8", "quantize_weight_int4",
     "make_paged_kv", "paged_attention_ref",
     "silu_mul", "quantize_act_int8_gpu", "silu_mul_quant_int8",
-    "pack_int4_i32", "KernelInfo",
+    "pack_int4_i32", "KernelInfo", "PackedWeightInt8", "pack_weight_int8",
 ]
 
 
@@ -169,24 +171,57 @@ def _plan_ptr(plan) -> int:
 def _w8a8_block_n(block_n) -> int:
     if not block_n:
         return 0
-    return 16 if block_n <= 16 else (32 if block_n <= 32 else 64)
+    return 16 if block_n <= 16 else (32 if block_n <= 32 else (64 if block_n <= 64 else 128))
+
+
+class PackedWeightInt8:
+    """An int8 weight [N, K] pre-packed once into MFMA fragments for w8a8_matmul.
+
+    Fragment (16-row tile t, 64-byte K step s) is 1 KB holding, for lane l and byte b,
+    w[16t + l%16][64s + 16*(l/16) + b] (zero-padded), so the GEMM streams it contiguously.
+    Results are bit-identical to passing the row-major weight.
+    """
+
+    def __init__(self, w_q: torch.Tensor):
+        _require_gpu(w_q)
+        if w_q.dtype != torch.int8 or w_q.dim() != 2:
+            raise RuntimeError("PackedWeightInt8 expects an int8 [N, K] weight")
+        w_q = _rowmajor(w_q)
+        self.N, self.K = w_q.shape
+        self.shape = (self.N, self.K)
+        self.device = w_q.device
+        nbytes = _lib.lib().specq_w8a8_packed_bytes(self.N, self.K)
+        self.data = torch.empty(nbytes, dtype=torch.int8, device=w_q.device)
+        _lib.call("specq_w8a8_pack_weight", w_q.data_ptr(), w_q.stride(0), self.N, self.K, self.data.data_ptr(),
+                  _stream_ptr(w_q))
+
+
+def pack_weight_int8(w_q):
+    """Pack an int8 [N, K] weight for w8a8_matmul (see PackedWeightInt8)."""
+    return PackedWeightInt8(w_q)
 
 
 def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=64, BLOCK_K=128,
                 num_warps=4, num_stages=3, plan=None, grid_m_max=None, split_k=0, workspace=None):
     """C[M, N] = fp16((int32(a_q @ w_q.T) * sa[:, None]) * sw[None, :]).  Returns (out, ck).
 
-    a_q int8 [M, K]; w_q int8 [N, K]; sa fp32 [M]; sw fp32 [N].  With `plan`, M is read from
-    plan[0] on the device and the grid covers grid_m_max rows (reference kernels.py:71-86).
+    a_q int8 [M, K]; w_q int8 [N, K] (or a PackedWeightInt8); sa fp32 [M]; sw fp32 [N].
+    With `plan`, M is read from plan[0] on the device and the grid covers grid_m_max rows
+    (reference kernels.py:71-86).
     """
-    _require_gpu(a_q, w_q, sa, sw)
-    if a_q.dtype != torch.int8 or w_q.dtype != torch.int8:
+    packed = isinstance(w_q, PackedWeightInt8)
+    _require_gpu(a_q, sa, sw)
+    if not packed:
+        _require_gpu(w_q)
+    if a_q.dtype != torch.int8 or (not packed and w_q.dtype != torch.int8):
         raise RuntimeError("w8a8_matmul expects int8 activations and weights")
     M, K = a_q.shape
     N = w_q.shape[0]
     if w_q.shape[1] != K:
-        raise RuntimeError(f"w8a8_matmul: K mismatch {a_q.shape} vs {w_q.shape}")
-    a_q, w_q = _rowmajor(a_q), _rowmajor(w_q)
+        raise RuntimeError(f"w8a8_matmul: K mismatch {tuple(a_q.shape)} vs {tuple(w_q.shape)}")
+    a_q = _rowmajor(a_q)
+    if not packed:
+        w_q = _rowmajor(w_q)
     sa = sa.float().contiguous()
     sw = sw.float().contiguous()
     if out is None:
@@ -198,12 +233,20 @@ def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=64, BLOCK_K=128,
     bn = _w8a8_block_n(BLOCK_N)
     nw = int(num_warps) if num_warps else 4
     ws = workspace or _ws.shared(a_q.device)
-    need = _lib.lib().specq_w8a8_workspace_size(m_grid, N, K, bm, bn, nw, split_k)
-    wptr, wbytes = ws.ensure(need)
-    _lib.call("specq_w8a8", a_q.data_ptr(), a_q.stride(0), w_q.data_ptr(), w_q.stride(0),
-              sa.data_ptr(), sw.data_ptr(), out.data_ptr(), out.stride(0),
-              M, N, K, int(grid_m_max or 0), _plan_ptr(plan), bm, bn, nw, split_k,
-              wptr, wbytes, _stream_ptr(a_q))
+    if packed:
+        need = _lib.lib().specq_w8a8_packed_workspace_size(m_grid, N, K, bm, bn, nw, split_k)
+        wptr, wbytes = ws.ensure(need)
+        _lib.call("specq_w8a8_packed", a_q.data_ptr(), a_q.stride(0), w_q.data.data_ptr(),
+                  sa.data_ptr(), sw.data_ptr(), out.data_ptr(), out.stride(0),
+                  M, N, K, int(grid_m_max or 0), _plan_ptr(plan), bm, bn, nw, split_k,
+                  wptr, wbytes, _stream_ptr(a_q))
+    else:
+        need = _lib.lib().specq_w8a8_workspace_size(m_grid, N, K, bm, bn, nw, split_k)
+        wptr, wbytes = ws.ensure(need)
+        _lib.call("specq_w8a8", a_q.data_ptr(), a_q.stride(0), w_q.data_ptr(), w_q.stride(0),
+                  sa.data_ptr(), sw.data_ptr(), out.data_ptr(), out.stride(0),
+                  M, N, K, int(grid_m_max or 0), _plan_ptr(plan), bm, bn, nw, split_k,
+                  wptr, wbytes, _stream_ptr(a_q))
     _w8a8_kernel._note(a_q.device.index or 0, (bm, bn, nw))
     return out, KernelInfo(0, 0, m_grid, N, K, bm, bn, nw, split_k)
 

@@ -38,6 +38,13 @@ SIGNATURES = {
     "specq_w8a8": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_i64,
                             _c_int, _c_int, _c_int, _c_int, _c_vp,
                             _c_int, _c_int, _c_int, _c_int, _c_vp, _c_size, _c_vp]),
+    "specq_w8a8_packed_bytes": (_c_size, [_c_int, _c_int]),
+    "specq_w8a8_pack_weight": (_c_int, [_c_vp, _c_i64, _c_int, _c_int, _c_vp, _c_vp]),
+    "specq_w8a8_packed_workspace_size": (_c_size, [_c_int] * 7),
+    "specq_w8a8_packed": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
+                                   _c_int, _c_int, _c_int, _c_int, _c_vp,
+                                   _c_int, _c_int, _c_int, _c_int, _c_vp, _c_size, _c_vp]),
+    "specq_set_option": (_c_int, [ctypes.c_char_p, _c_int]),
     "specq_w4a16_workspace_size": (_c_size, [_c_int] * 7),
     "specq_w4a16": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_vp, _c_i64, _c_vp, _c_i64,
                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp,
@@ -92,6 +99,10 @@ def call(name: str, *args) -> int:
     rc = getattr(lib(), name)(*args)
     check(rc, name)
     return rc
+
+
+def set_option(name: str, value: int) -> None:
+    call("specq_set_option", name.encode(), int(value))
 
 
 def kernel_attrs(kind: int, variant: int, m_grid: int, N: int, K: int, block_m: int, block_n: int,

@@ -85,10 +85,59 @@ def test_w8a8_split_k_and_tiles_bit_identical(split_k):
     a, w, sa, sw = gen.w8a8_inputs(72, 4096, 4096, seed=5)
     ref = O.w8a8(a.numpy(), sa.numpy(), w.numpy(), sw.numpy())
     a, w, sa, sw = (t.to(DEV) for t in (a, w, sa, sw))
-    for bn, nw in ((16, 4), (32, 2), (64, 1), (32, 4)):
+    for bn, nw in ((16, 4), (32, 2), (64, 1), (32, 4), (64, 2), (128, 4)):
         out, _ = K.w8a8_matmul(a, sa, w, sw, BLOCK_M=80, BLOCK_N=bn, num_warps=nw, split_k=split_k)
         torch.cuda.synchronize()
         assert_bitexact_fp16(out, ref, f"split_k={split_k} BLOCK_N={bn} warps={nw}")
+
+
+@pytest.mark.parametrize("bn_nw", [(16, 4), (32, 4), (32, 2), (64, 4), (64, 2), (128, 4)])
+def test_w8a8_every_tile_shape_and_block_m(bn_nw):
+    # Every channel-block shape of the aligned (LDS-DMA) path at every BLOCK_M bucket,
+    # including the deep tiles that change the K-chunk length.
+    bn, nw = bn_nw
+    note(f"w8a8 tile sweep BLOCK_N={bn} warps={nw}")
+    a, w, sa, sw = gen.w8a8_inputs(300, 1000, 1536, seed=31)
+    ref = O.w8a8(a.numpy(), sa.numpy(), w.numpy(), sw.numpy())
+    a, w, sa, sw = (t.to(DEV) for t in (a, w, sa, sw))
+    for bm in (16, 32, 48, 80, 144, 192, 208, 304, 320):
+        for M in sorted({1, min(bm, 300), min(bm + 5, 300), 300}):
+            out, ck = K.w8a8_matmul(a[:M], sa[:M], w, sw, BLOCK_M=bm, BLOCK_N=bn, num_warps=nw)
+            torch.cuda.synchronize()
+            assert_bitexact_fp16(out, ref[:M], f"BLOCK_N={bn} warps={nw} BLOCK_M={bm} M={M} ({ck.name})")
+
+
+@pytest.mark.parametrize("shape", [(1000, 1536)] + gen.CONFIG1_SHAPES)
+def test_w8a8_packed_weight_bit_exact(shape):
+    N, Kd = shape
+    note(f"w8a8 packed weight N={N} K={Kd}")
+    a, w, sa, sw = gen.w8a8_inputs(300, N, Kd, seed=41 + N)
+    ref = O.w8a8(a.numpy(), sa.numpy(), w.numpy(), sw.numpy())
+    a, w, sa, sw = (t.to(DEV) for t in (a, w, sa, sw))
+    wp = K.pack_weight_int8(w)
+    for M in (1, 8, 72, 300):
+        for bn, nw, sk in ((None, 4, 0), (16, 4, 0), (32, 2, 3), (16, 1, 0)):
+            out, _ = K.w8a8_matmul(a[:M], sa[:M], wp, sw, BLOCK_M=None, BLOCK_N=bn, num_warps=nw, split_k=sk)
+            torch.cuda.synchronize()
+            assert_bitexact_fp16(out, ref[:M], f"packed N={N} K={Kd} M={M} bn={bn} nw={nw} sk={sk}")
+
+
+@pytest.mark.parametrize("path", [1, 2, 3])
+def test_w8a8_kernel_families_bit_identical(path):
+    from specq import _lib
+    note(f"w8a8 kernel family {path}")
+    a, w, sa, sw = gen.w8a8_inputs(300, 1000, 1536, seed=51)
+    ref = O.w8a8(a.numpy(), sa.numpy(), w.numpy(), sw.numpy())
+    a, w, sa, sw = (t.to(DEV) for t in (a, w, sa, sw))
+    _lib.set_option("w8a8_path", path)
+    try:
+        for M in (1, 17, 72, 300):
+            for bm in (None, 16, 64):
+                out, ck = K.w8a8_matmul(a[:M], sa[:M], w, sw, BLOCK_M=bm, BLOCK_N=32, num_warps=4)
+                torch.cuda.synchronize()
+                assert_bitexact_fp16(out, ref[:M], f"path={path} M={M} BLOCK_M={bm} ({ck.name})")
+    finally:
+        _lib.set_option("w8a8_path", 0)
 
 
 def test_w8a8_plan_mode_sentinel_rows():
