@@ -91,9 +91,11 @@ int specq_w8a8_packed(const int8_t* a, int64_t lda, const void* w_packed,
                       int block_m, int block_n, int num_warps, int split_k,
                       void* workspace, size_t workspace_bytes, void* stream);
 
-/* Tuning options.  "w8a8_path": W8A8 kernel family for 16-byte aligned row-major weights,
- * 0 = automatic, 1 = register streaming, 2 = LDS-DMA ring, 3 = byte-granular register
- * kernel.  Every family computes the same INT32 sums, so results do not change. */
+/* Tuning options.  "w8a8_path": W8A8 kernel family for 16-byte aligned operands,
+ * 0 = automatic, 1 = register streaming, 2 = LDS-DMA ring (row-major weights only),
+ * 3 = byte-granular register kernel (row-major weights only), 4 = streaming with
+ * LDS-shared activations.  Every family computes the same INT32 sums, so results do not
+ * change. */
 int specq_set_option(const char* name, int value);
 
 /* ---------------------------------------------------------------------------------------
@@ -172,7 +174,8 @@ int specq_silu_mul_quant_int8(const void* gate, int64_t ld_gate, const void* up,
 /* ---------------------------------------------------------------------------------------
  * Resource usage of the kernel a call with these arguments would launch (the reference's
  * compiled-kernel metadata ck.n_regs / ck.n_spills / ck.metadata.shared, regs.py:29-32).
- * kind: 0 = W8A8, 1 = W4A16 (layout in `variant`), 2 = paged attention (D in `variant`).
+ * kind: 0 = W8A8 (weight layout in `variant`: 0 row-major, 1 packed), 1 = W4A16 (layout in
+ * `variant`), 2 = paged attention (D in `variant`).
  * ------------------------------------------------------------------------------------- */
 typedef struct specq_kernel_attrs {
   char name[160];          /* kernel symbol */

@@ -60,7 +60,7 @@ int device_cus() {
   return cache[dev];
 }
 
-int w8a8_attrs(int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k,
+int w8a8_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k,
                specq_kernel_attrs* out);
 int w4a16_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k,
                 specq_kernel_attrs* out);
@@ -78,7 +78,7 @@ extern "C" int specq_kernel_attrs_query(int kind, int variant, int m_grid, int N
   if (!out) return specq::fail(SPECQ_EINVAL, "kernel_attrs: null output");
   memset(out, 0, sizeof(*out));
   switch (kind) {
-    case 0: return specq::w8a8_attrs(m_grid, N, K, block_m, block_n, num_warps, split_k, out);
+    case 0: return specq::w8a8_attrs(variant, m_grid, N, K, block_m, block_n, num_warps, split_k, out);
     case 1: return specq::w4a16_attrs(variant, m_grid, N, K, block_m, block_n, num_warps, split_k, out);
     case 2: return specq::attn_attrs(variant, block_m, out);
   }

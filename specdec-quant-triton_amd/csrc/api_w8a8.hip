@@ -3,6 +3,8 @@
 // Kernel families (all compute identical INT32 sums, so every choice is bit-identical):
 //   STREAM  register-streaming kernel (w8a8_stream.hpp), 16-byte aligned operands; takes the
 //           row-major weight or the packed-fragment weight.  Default.
+//   STREAM2 streaming kernel with LDS-shared activations (w8a8_stream2.hpp) for deeper M
+//           tiles, 16-byte aligned operands, either weight layout.
 //   DMA     LDS-DMA ring kernel (w8a8_dma.hpp), 16-byte aligned row-major weights.
 //   LEGACY  register-pipelined kernel with 16/8/4/1-byte loads (w8a8.hpp): any alignment.
 #include <algorithm>
@@ -31,6 +33,10 @@ const void* w8a8_stream_kernel_l0r1(int mt);
 const void* w8a8_stream_kernel_l0r2(int mt);
 const void* w8a8_stream_kernel_l1r1(int mt);
 const void* w8a8_stream_kernel_l1r2(int mt);
+const void* w8a8_stream2_kernel_l0r1(int mt, int* lds);
+const void* w8a8_stream2_kernel_l0r2(int mt, int* lds);
+const void* w8a8_stream2_kernel_l1r1(int mt, int* lds);
+const void* w8a8_stream2_kernel_l1r2(int mt, int* lds);
 
 // Packs a row-major int8 weight [N, K] (row stride ldw) into MFMA fragments:
 // packed[t][s][l*16 + b] = W[16t + l%16][64s + 16*(l/16) + b], zero-padded to whole tiles.
@@ -63,7 +69,7 @@ std::atomic<int> g_w8a8_path{0};
 
 namespace {
 
-enum Family { kStream = 1, kDma = 2, kLegacy = 3 };
+enum Family { kStream = 1, kDma = 2, kLegacy = 3, kStream2 = 4 };
 
 struct W8A8Cfg {
   int family, layout;
@@ -108,6 +114,11 @@ const void* stream_fn(int layout, int mt, int rw) {
   return rw == 1 ? w8a8_stream_kernel_l1r1(mt) : w8a8_stream_kernel_l1r2(mt);
 }
 
+const void* stream2_fn(int layout, int mt, int rw, int* lds) {
+  if (layout == 0) return rw == 1 ? w8a8_stream2_kernel_l0r1(mt, lds) : w8a8_stream2_kernel_l0r2(mt, lds);
+  return rw == 1 ? w8a8_stream2_kernel_l1r1(mt, lds) : w8a8_stream2_kernel_l1r2(mt, lds);
+}
+
 // Resolve the kernel and its tiles.  `vec` is the operand alignment (16 when unknown),
 // `layout` 0 = row-major weight, 1 = packed fragments.
 int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k,
@@ -128,12 +139,23 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   int nw = num_warps <= 0 ? 4 : (num_warps >= 4 ? 4 : (num_warps >= 2 ? 2 : 1));
   const int path = g_w8a8_path.load();
   int family;
-  if (layout == 1) family = kStream;
-  else if (vec != 16) family = kLegacy;
-  else family = (path == kDma || path == kLegacy) ? path : kStream;
+  if (vec != 16) family = kLegacy;
+  else if (layout == 1) family = path == kStream2 ? kStream2 : kStream;
+  else family = (path == kDma || path == kLegacy || path == kStream2) ? path : kStream;
 
   int rw = 1, nwn = 1, dma_lds = 0;
   const void* fn = nullptr;
+  if (family == kStream2) {
+    // 4 waves side by side along N, RW x 16 channels each.
+    if (block_n == 16 || block_n == 32) {
+      family = kStream;
+    } else {
+      rw = block_n == 128 ? 2 : 1;
+      nw = 4;
+      fn = stream2_fn(layout, mt, rw, &dma_lds);
+      if (!fn) family = kStream;  // tile too deep for the LDS activation ring
+    }
+  }
   if (family == kDma) {
     // 4 waves: NWN along N (RW x 16 channels each), 4/NWN along K.
     const int bn = block_n > 0 ? block_n : (N <= 2048 ? 16 : 64);
@@ -163,12 +185,14 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
 
   cfg->family = family; cfg->layout = layout; cfg->fn = fn;
   cfg->mt = mt; cfg->rw = rw; cfg->nw = nw; cfg->vec = vec; cfg->nwn = nwn;
-  cfg->bn = family == kDma ? nwn * rw * 16 : rw * 16;
+  cfg->bn = family == kDma ? nwn * rw * 16 : (family == kStream2 ? 4 * rw * 16 : rw * 16);
   cfg->n_tiles = ceil_div(N, cfg->bn);
   cfg->m_chunks = ceil_div(m_grid > 0 ? m_grid : 1, mt * 16);
   const int BM = mt * 16, BN = cfg->bn;
   if (family == kDma) {
     cfg->lds = (size_t)dma_lds;
+  } else if (family == kStream2) {
+    cfg->lds = 0;  // static LDS (one variable per ring slot)
   } else if (family == kStream) {
     const size_t stage = layout == 0 ? (size_t)nw * rw * 4096 : 0;
     const size_t red = nw > 1 ? (size_t)BM * (BN + kW8A8Pad) * 4 : 0;
@@ -183,16 +207,18 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
     splits = split_k;
   } else {
     // Fill the CUs: about two resident workgroups per CU (LDS permitting), >= 2 K steps per wave.
-    const int per_cu = family == kDma ? (dma_lds > 0 ? std::max(1, 163840 / dma_lds) : 1) : 2;
+    const bool lds_bound = family == kDma || family == kStream2;
+    const int per_cu = lds_bound ? (dma_lds > 0 ? std::max(1, 163840 / dma_lds) : 1) : 2;
     const int target = per_cu * device_cus();
     const int base = cfg->n_tiles * cfg->m_chunks;
     splits = base >= target ? 1 : ceil_div(target, base);
-    int max_splits = ksteps / (2 * nw);
+    // K steps per split: >= 2 per wave when waves split K, >= 2 blocks when they split N.
+    int max_splits = family == kStream2 ? ksteps / 8 : ksteps / (2 * nw);
     if (max_splits < 1) max_splits = 1;
     if (splits > max_splits) splits = max_splits;
   }
   // Split boundaries on whole 256-byte blocks keep the streaming kernel's fetches aligned.
-  const int quantum = family == kStream ? 4 : 1;
+  const int quantum = (family == kStream || family == kStream2) ? 4 : 1;
   const int kq = ceil_div(ksteps, quantum);
   if (splits > kq) splits = kq;
   const int k_range = ceil_div(kq, splits) * quantum * 64;
@@ -259,10 +285,11 @@ size_t workspace_size(int layout, int m_grid, int N, int K, int block_m, int blo
 
 }  // namespace
 
-int w8a8_attrs(int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k,
+int w8a8_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k,
                specq_kernel_attrs* out) {
   W8A8Cfg cfg;
-  int rc = w8a8_config(0, m_grid, N, K, block_m, block_n, num_warps, split_k, 16, &cfg);
+  SPECQ_REQUIRE(layout == 0 || layout == 1, SPECQ_EINVAL, "w8a8 attrs: layout %d", layout);
+  int rc = w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, 16, &cfg);
   if (rc) return rc;
   hipFuncAttributes fa;
   if (hipFuncGetAttributes(&fa, cfg.fn) != hipSuccess) return fail(SPECQ_EIO, "w8a8: hipFuncGetAttributes failed");
@@ -270,6 +297,8 @@ int w8a8_attrs(int m_grid, int N, int K, int block_m, int block_n, int num_warps
     snprintf(out->name, sizeof(out->name), "specq::w8a8_dma_kernel<%d,%d,%d>", cfg.mt, cfg.rw, cfg.nwn);
   else if (cfg.family == kStream)
     snprintf(out->name, sizeof(out->name), "specq::w8a8_stream_kernel<%d,%d,%d>", cfg.mt, cfg.rw, cfg.layout);
+  else if (cfg.family == kStream2)
+    snprintf(out->name, sizeof(out->name), "specq::w8a8_stream2_kernel<%d,%d,%d>", cfg.mt, cfg.rw, cfg.layout);
   else
     snprintf(out->name, sizeof(out->name), "specq::w8a8_kernel<%d,%d,%d>", cfg.mt, cfg.rw, cfg.vec);
   out->num_regs = fa.numRegs;
@@ -340,7 +369,7 @@ extern "C" int specq_set_option(const char* name, int value) {
   clear_error();
   SPECQ_REQUIRE(name != nullptr, SPECQ_EINVAL, "set_option: null name");
   if (strcmp(name, "w8a8_path") == 0) {
-    SPECQ_REQUIRE(value >= 0 && value <= 3, SPECQ_EINVAL, "set_option: w8a8_path must be 0..3");
+    SPECQ_REQUIRE(value >= 0 && value <= 4, SPECQ_EINVAL, "set_option: w8a8_path must be 0..4");
     g_w8a8_path.store(value);
     return SPECQ_OK;
   }

@@ -8,6 +8,7 @@
 // long as the A- and B-operand loads use the same mapping.  They use that freedom to make
 // every lane load long contiguous runs straight from HBM into VGPRs.
 #pragma once
+#include <type_traits>
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <stdint.h>
@@ -156,6 +157,38 @@ __device__ __forceinline__ T collect(const T* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // All of this wave's outstanding memory operations have completed.
+// Workgroup barriers for software pipelines.  __syncthreads() is a workgroup fence plus
+// s_barrier, and the fence waits for every outstanding load (vmcnt(0)), which drains a
+// prefetch pipeline at each barrier.  These issue s_barrier with compiler-only fences:
+//  * wg_barrier(): orders nothing in hardware; for data the waves made visible themselves
+//    (e.g. LDS DMA completed with an explicit s_waitcnt vmcnt before the barrier).
+//  * wg_barrier_lds(): first waits for this wave's LDS operations (lgkmcnt(0)), so LDS
+//    writes before it are visible to every wave after it and LDS reads before it are done.
+__device__ __forceinline__ void wg_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ void wait_lgkm0() {
+  // s_waitcnt encoding: vmcnt 63 (no wait), expcnt 7 (no wait), lgkmcnt 0.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ void wg_barrier_lds() {
+  wait_lgkm0();
+  wg_barrier();
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 __device__ __forceinline__ void wait_all_memory() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);

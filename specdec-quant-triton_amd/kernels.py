@@ -248,7 +248,7 @@ def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=64, BLOCK_K=128,
                   M, N, K, int(grid_m_max or 0), _plan_ptr(plan), bm, bn, nw, split_k,
                   wptr, wbytes, _stream_ptr(a_q))
     _w8a8_kernel._note(a_q.device.index or 0, (bm, bn, nw))
-    return out, KernelInfo(0, 0, m_grid, N, K, bm, bn, nw, split_k)
+    return out, KernelInfo(0, 1 if packed else 0, m_grid, N, K, bm, bn, nw, split_k)
 
 
 def quantize_act_int8(x):

@@ -122,7 +122,7 @@ def test_w8a8_packed_weight_bit_exact(shape):
             assert_bitexact_fp16(out, ref[:M], f"packed N={N} K={Kd} M={M} bn={bn} nw={nw} sk={sk}")
 
 
-@pytest.mark.parametrize("path", [1, 2, 3])
+@pytest.mark.parametrize("path", [1, 2, 3, 4])
 def test_w8a8_kernel_families_bit_identical(path):
     from specq import _lib
     note(f"w8a8 kernel family {path}")
@@ -136,6 +136,30 @@ def test_w8a8_kernel_families_bit_identical(path):
                 out, ck = K.w8a8_matmul(a[:M], sa[:M], w, sw, BLOCK_M=bm, BLOCK_N=32, num_warps=4)
                 torch.cuda.synchronize()
                 assert_bitexact_fp16(out, ref[:M], f"path={path} M={M} BLOCK_M={bm} ({ck.name})")
+    finally:
+        _lib.set_option("w8a8_path", 0)
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_w8a8_lds_shared_activation_family(layout):
+    # Streaming kernel with LDS-shared activations: every tile depth it is built for, both
+    # channel widths, K tails that are not whole 256-byte blocks, N tails, explicit split-K.
+    from specq import _lib
+    _lib.set_option("w8a8_path", 4)
+    try:
+        for N, Kd in ((1000, 1552), (4096, 4096)):
+            note(f"w8a8 stream2 layout={layout} N={N} K={Kd}")
+            a, w, sa, sw = gen.w8a8_inputs(300, N, Kd, seed=61 + N)
+            ref = O.w8a8(a.numpy(), sa.numpy(), w.numpy(), sw.numpy())
+            a, w, sa, sw = (t.to(DEV) for t in (a, w, sa, sw))
+            wt = K.pack_weight_int8(w) if layout == 1 else w
+            for bm in (None, 32, 80, 160, 256):
+                for M in (1, 17, 72, 130, 300):
+                    for bn, sk in ((None, 0), (64, 1), (128, 0), (64, 3)):
+                        out, ck = K.w8a8_matmul(a[:M], sa[:M], wt, sw, BLOCK_M=bm, BLOCK_N=bn, split_k=sk)
+                        torch.cuda.synchronize()
+                        assert_bitexact_fp16(out, ref[:M], f"stream2 N={N} K={Kd} M={M} BLOCK_M={bm} "
+                                                           f"BLOCK_N={bn} sk={sk} ({ck.name})")
     finally:
         _lib.set_option("w8a8_path", 0)
 
