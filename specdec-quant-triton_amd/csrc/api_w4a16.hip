@@ -45,10 +45,11 @@ int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, in
   if (split_k > 0) {
     splits = split_k;
   } else {
-    // A function of (N, K, BLOCK_N) only, so the fp32 summation order never depends on M.
-    const int target = 256;
+    // A function of (N, K, BLOCK_N) only, so the fp32 summation order never depends on M:
+    // about two workgroups per CU, each split long enough (>= 8 blocks) to fill its prefetch ring.
+    const int target = 2 * device_cus();
     splits = cfg->n_tiles >= target ? 1 : ceil_div(target, cfg->n_tiles);
-    int max_splits = cfg->nblocks / 4;
+    int max_splits = cfg->nblocks / 8;
     if (max_splits < 1) max_splits = 1;
     if (splits > max_splits) splits = max_splits;
   }
@@ -56,7 +57,7 @@ int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, in
   cfg->bps = ceil_div(cfg->nblocks, splits);
   cfg->splits = ceil_div(cfg->nblocks, cfg->bps);
   const int BM = mt * 16, BN = kW4Waves * rw * 16;
-  cfg->lds = (size_t)2 * BM * kW4RowBytes;
+  cfg->lds = 0;  // static LDS (activation ring slots)
   cfg->ws_partials = cfg->splits > 1 ? align_up((size_t)cfg->m_chunks * cfg->n_tiles * cfg->splits * BM * BN * 4, 256) : 0;
   cfg->ws_counters = cfg->splits > 1 ? kCounterBytes : 0;
   SPECQ_REQUIRE((int64_t)cfg->m_chunks * cfg->n_tiles <= kMaxCounters, SPECQ_ENOTSUP,
@@ -111,8 +112,9 @@ extern "C" int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t l
   SPECQ_REQUIRE(a && wq && sc && c, SPECQ_EINVAL, "w4a16: null tensor pointer");
   SPECQ_REQUIRE(wq_layout == 0 || wq_layout == 1, SPECQ_EINVAL, "w4a16: unknown weight layout %d", wq_layout);
   SPECQ_REQUIRE(group > 0 && K % group == 0, SPECQ_EINVAL, "w4a16: group=%d must divide K=%d", group, K);
-  SPECQ_REQUIRE(group % (wq_layout == 1 ? 32 : 16) == 0, SPECQ_ENOTSUP,
-                "w4a16: group=%d must be a multiple of %d for layout %d", group, wq_layout == 1 ? 32 : 16, wq_layout);
+  SPECQ_REQUIRE(group % (wq_layout == 1 ? 32 : 16) == 0 && (group & (group - 1)) == 0, SPECQ_ENOTSUP,
+                "w4a16: group=%d must be a power of two and a multiple of %d for layout %d", group,
+                wq_layout == 1 ? 32 : 16, wq_layout);
   const int64_t row_bytes = wq_layout == 1 ? ldq * 4 : ldq;
   SPECQ_REQUIRE(lda >= K && row_bytes >= K / 2 && ld_sc >= K / group && ldc >= N, SPECQ_EINVAL,
                 "w4a16: row strides must cover a row");
@@ -136,6 +138,7 @@ extern "C" int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t l
   p.A = (const _Float16*)a; p.lda = lda; p.Wq = (const uint8_t*)wq; p.ldq = row_bytes;
   p.sc = (const _Float16*)sc; p.ld_sc = ld_sc; p.C = (_Float16*)c; p.ldc = ldc; p.plan = plan;
   p.M = M; p.N = N; p.K = K; p.group = group; p.m_grid = m_grid;
+  p.group_shift = __builtin_ctz((unsigned)group);
   p.n_tiles = cfg.n_tiles; p.m_chunks = cfg.m_chunks; p.splits = cfg.splits; p.nblocks = cfg.nblocks;
   p.blocks_per_split = cfg.bps;
   p.counters = need ? (int32_t*)workspace : nullptr;

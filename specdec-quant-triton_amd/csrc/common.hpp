@@ -157,6 +157,28 @@ __device__ __forceinline__ T collect(const T* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // All of this wave's outstanding memory operations have completed.
+// s_waitcnt with vmcnt = N (expcnt and lgkmcnt left at their maximum, i.e. not waited on).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Buffer offset `off`, or out of range (reads as zero) when !ok.  Bit 31 is set arithmetically
+// rather than selected: offsets here are < 2^31, and a select on a cheap-to-skip address tends
+// to be turned into a branch around the load, which costs a vmcnt(0) at the join.
+__device__ __forceinline__ uint32_t oob_unless(bool ok, uint32_t off) { return off | ((uint32_t)(!ok) << 31); }
+
+// 16-byte LDS DMA (buffer_load_dwordx4 ... lds): lane l's 16 bytes from voff land at
+// lds_frag + 16*l (lds_frag must be wave-uniform); out-of-range lanes write zeros.
+__device__ __forceinline__ void dma16(rsrc_t rs, uint8_t* lds_frag, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)lds_frag, 16, voff, 0, 0, 0);
+}
+
 // Workgroup barriers for software pipelines.  __syncthreads() is a workgroup fence plus
 // s_barrier, and the fence waits for every outstanding load (vmcnt(0)), which drains a
 // prefetch pipeline at each barrier.  These issue s_barrier with compiler-only fences:

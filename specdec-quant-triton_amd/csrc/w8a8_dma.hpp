@@ -60,20 +60,6 @@ __device__ __forceinline__ uint32_t frag_read_off(int s, int lane) {
   return (uint32_t)((s >> 2) * 4096 + r * 256 + ((c ^ r) & 15) * 16);
 }
 
-// s_waitcnt with vmcnt = N (expcnt and lgkmcnt left at their maximum, i.e. not waited on).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N <= 63, "vmcnt range");
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-__device__ __forceinline__ void dma16(rsrc_t rs, uint8_t* lds_frag, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)lds_frag, 16, voff, 0, 0, 0);
-}
 
 template <int MT, int RW, int NWN>
 __global__ __launch_bounds__(256) void w8a8_dma_kernel(W8A8Params p) {
