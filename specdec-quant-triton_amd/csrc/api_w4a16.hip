@@ -28,7 +28,10 @@ int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, in
                   "w4a16: BLOCK_M=%d must be a multiple of 16 and at most 256", block_m);
     mt = block_m / 16;
   } else {
-    const int chunks = ceil_div(rows16, 16);
+    // Wide N: one M-chunk up to 256 rows (one weight pass); narrow N: 48-row chunks, so more
+    // workgroups share the activation traffic (measured on the Llama-3-8B linears).
+    const int cap = ceil_div(N, 64) >= 128 ? 16 : 3;
+    const int chunks = ceil_div(rows16, cap);
     mt = ceil_div(rows16, chunks);
   }
   // BLOCK_N is the channel width of the whole workgroup (4 waves): 64 or 128.

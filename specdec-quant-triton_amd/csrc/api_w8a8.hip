@@ -138,9 +138,13 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   }
   int nw = num_warps <= 0 ? 4 : (num_warps >= 4 ? 4 : (num_warps >= 2 ? 2 : 1));
   const int path = g_w8a8_path.load();
+  // Automatic family: the LDS-shared-activation kernel once there are 3 or more token blocks
+  // (its activation fragments then no longer fit the register-streaming kernel's budget).
+  const bool s2_auto = path == 0 && rows16 >= 3 && block_n != 16 && block_n != 32;
   int family;
   if (vec != 16) family = kLegacy;
-  else if (layout == 1) family = path == kStream2 ? kStream2 : kStream;
+  else if (layout == 1) family = (path == kStream2 || s2_auto) ? kStream2 : kStream;
+  else if (s2_auto) family = kStream2;
   else family = (path == kDma || path == kLegacy || path == kStream2) ? path : kStream;
 
   int rw = 1, nwn = 1, dma_lds = 0;
@@ -150,7 +154,16 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
     if (block_n == 16 || block_n == 32) {
       family = kStream;
     } else {
-      rw = block_n == 128 ? 2 : 1;
+      const int tiles64 = ceil_div(N, 64);
+      rw = block_n == 128 ? 2 : (block_n == 0 && rows16 >= 18 && tiles64 >= 64 ? 2 : 1);
+      if (block_m <= 0) {
+        // Measured on the Llama-3-8B linears: wide N has tiles enough to fill the CUs with
+        // deep M tiles (one weight pass); narrow N does better with 48-row tiles and more
+        // workgroups (the extra weight passes hit L2).
+        const int cap = tiles64 >= 128 ? 9 : 3;
+        const int chunks = ceil_div(rows16, cap);
+        mt = ceil_div(rows16, chunks);
+      }
       nw = 4;
       fn = stream2_fn(layout, mt, rw, &dma_lds);
       if (!fn) family = kStream;  // tile too deep for the LDS activation ring
@@ -211,9 +224,9 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
     const int per_cu = lds_bound ? (dma_lds > 0 ? std::max(1, 163840 / dma_lds) : 1) : 2;
     const int target = per_cu * device_cus();
     const int base = cfg->n_tiles * cfg->m_chunks;
-    splits = base >= target ? 1 : ceil_div(target, base);
-    // K steps per split: >= 2 per wave when waves split K, >= 2 blocks when they split N.
-    int max_splits = family == kStream2 ? ksteps / 8 : ksteps / (2 * nw);
+    splits = 4 * base >= 3 * target ? 1 : ceil_div(target, base);
+    // K steps per split: >= 2 per wave when waves split K, >= 4 blocks when they split N.
+    int max_splits = family == kStream2 ? ksteps / 16 : ksteps / (2 * nw);
     if (max_splits < 1) max_splits = 1;
     if (splits > max_splits) splits = max_splits;
   }

@@ -1,10 +1,11 @@
-"""BLOCK_M selection (the reference's M-tile choice, bench_matmul.py:76-99, REPORT.md:81).
+"""M-tile selection (the reference's BLOCK_M choice, bench_matmul.py:76-99, REPORT.md:81).
 
-The reference sweeps tile configs per M and reports that BLOCK_M should follow M
-(16 for M <= 16, 32 up to 32, 64 up to 64, 128 above).  On MI355X the kernels keep a whole
-M-chunk of up to 320 (W8A8) or 256 (W4A16) rows in registers while the weights stream
-through once, so the default is one chunk covering M rounded up to 16 rows; STAIRCASE can
-override it per (kind, N, K) with the best measured value for each M bucket.
+The reference sweeps tile configs per M and reports that BLOCK_M should follow M.  Here a
+BLOCK_M of 0 hands the choice to the library, whose rule was fitted to measured sweeps on
+MI355X (W8A8: register-streaming kernel with the whole M-chunk in registers up to 32 rows,
+then the LDS-shared-activation kernel with 48-row tiles for narrow N and up to 144-row tiles
+for wide N; W4A16: one chunk of up to 256 rows for wide N, 48-row chunks for narrow N).
+STAIRCASE overrides it per (kind, N, K) with the best measured BLOCK_M for each M bucket.
 """
 from __future__ import annotations
 
@@ -15,6 +16,7 @@ _MAX_BM = {"w8a8": 320, "w4a16": 256}
 
 
 def default_block_m(kind: str, m: int) -> int:
+    """One chunk covering M rounded up to 16 rows, split evenly above the kernel's maximum."""
     cap = _MAX_BM[kind]
     rows16 = max(1, (m + 15) // 16)
     chunks = (rows16 * 16 + cap - 1) // cap
@@ -22,9 +24,10 @@ def default_block_m(kind: str, m: int) -> int:
 
 
 def pick_block_m(kind: str, m: int, N: int, K: int) -> int:
+    """BLOCK_M for an M of m: the STAIRCASE entry if one covers it, else 0 (library rule)."""
     table = STAIRCASE.get((kind, N, K))
     if table:
         for max_m, bm in table:
             if m <= max_m:
                 return bm
-    return default_block_m(kind, m)
+    return 0
