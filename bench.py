@@ -1,0 +1,438 @@
+"""Benchmark of the quantized verification path on one MI355X (prints one JSON line).
+
+Workload: W8A8 GEMMs over the seven Llama-3-8B-shaped linears
+(q, o 4096x4096; k, v 1024x4096; gate, up 14336x4096; down 4096x14336) at the verification
+batch M = B*(k+1) = 8*9 = 72.  One step is the linears of one verification forward: 32 layers
+x 7 GEMMs = 224 launches streaming 6.98 GB of distinct INT8 weights (far beyond the 256 MiB
+Infinity Cache, so every step reads its weights from HBM).  The step is captured once into a
+hipGraph (torch.cuda.graph over the C-ABI launches) and replayed; inputs are resident in HBM
+before the timed region starts.
+
+  value        algorithmic HBM bytes of a step / step time, in GB/s (whole job, one GPU)
+  roofline     the dominant kernel (the gate/up GEMM, 54% of the bytes): algorithmic bytes per
+               launch / its mean launch duration, measured with HIP events around a graph of
+               back-to-back launches on the stream the kernels run on, against 8 TB/s
+  cpu_baseline the CPU oracle (oracle/oracle.py, numpy) on one layer's seven linears at the
+               same M, timed on the host cores for a bounded ~10 s sample
+  detail       the k=0 decode step (M=8) on the same weights and the verify/decode ratio
+               (target <= 1.1), W4A16 at M=72 and M=8, INT8 paged verification attention at
+               B=8, k=8, and the plan-buffer graph replay of the config-4 stack
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-detail]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "specdec-quant-triton_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+LINEARS = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+           ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+METRIC = "GEMM µs & HBM GB/s vs M=B·(k+1); INT8 verify-attn µs at k=8; graph replay µs"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def w8a8_bytes(M: int, N: int, K: int) -> int:
+    """Algorithmic HBM bytes of one W8A8 call: W, A, sa, sw read once, C written once."""
+    return N * K + M * K + 4 * M + 4 * N + 2 * M * N
+
+
+def w4a16_bytes(M: int, N: int, K: int, group: int = 128) -> int:
+    return N * K // 2 + 2 * N * (K // group) + 2 * M * K + 2 * M * N
+
+
+def attn_bytes(B: int, L: int, q_len: int, H: int, H_KV: int, D: int, scale_bytes: int, page: int = 16) -> int:
+    """K/V int8 + their scales for every context token, q in + out (fp16), block table, lengths."""
+    return (B * L * H_KV * (2 * D + 2 * scale_bytes) + 4 * B * q_len * H * D
+            + 4 * B * ((L + page - 1) // page) + 4 * B)
+
+
+# ------------------------------------------------------------------------------------------
+# GPU helpers
+# ------------------------------------------------------------------------------------------
+def capture(fn):
+    """Capture fn() (already warmed up) into a graph on a side stream."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_replays(g, steps: int, warmup: int) -> float:
+    """Mean ms per replay over `steps` replays bracketed by synchronisation (events on the stream)."""
+    import torch
+
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def make_weights(L: int, seed: int = 0):
+    """L layers of the seven linears: int8 weights and fp32 per-channel scales, on the GPU."""
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    layers = []
+    for _ in range(L):
+        lw = {}
+        for name, N, K in LINEARS:
+            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g)
+            sw = torch.rand((N,), device="cuda", generator=g) * 0.009 + 0.001
+            lw[name] = (w, sw)
+        layers.append(lw)
+    return layers
+
+
+def w8a8_step_fn(K, layers, acts, M, outs):
+    a, sa, a_ff = acts[0][:M], acts[1][:M], acts[2][:M]
+
+    def step():
+        for lw in layers:
+            for name, N, Kd in LINEARS:
+                w, sw = lw[name]
+                K.w8a8_matmul(a if Kd == a.shape[1] else a_ff, sa, w, sw, out=outs[N][:M], BLOCK_M=None)
+    return step
+
+
+# ------------------------------------------------------------------------------------------
+# Parts of the run
+# ------------------------------------------------------------------------------------------
+def bench_w8a8(args, K, torch):
+    layers = make_weights(args.layers, seed=1)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    M_max = 300
+    a = torch.randint(-127, 128, (M_max, 4096), dtype=torch.int8, device="cuda", generator=g)
+    a_ff = torch.randint(-127, 128, (M_max, 14336), dtype=torch.int8, device="cuda", generator=g)
+    sa = torch.rand((M_max,), device="cuda", generator=g) * 0.015 + 0.005
+    acts = (a, sa, a_ff)
+    outs = {N: torch.empty((M_max, N), dtype=torch.float16, device="cuda") for N in {n for _, n, _ in LINEARS}}
+    res = {}
+    for label, M in (("verify", args.B * (args.k + 1)), ("decode", args.B)):
+        step = w8a8_step_fn(K, layers, acts, M, outs)
+        step()
+        torch.cuda.synchronize()
+        graph = capture(step)
+        bytes_step = args.layers * sum(w8a8_bytes(M, N, Kd) for _, N, Kd in LINEARS)
+        log(f"w8a8 {label} M={M}: warmup {args.warmup}, timing {args.steps} steps")
+        ms = time_replays(graph, args.steps, args.warmup)
+        res[label] = dict(M=M, ms=ms, bytes=bytes_step, GBps=bytes_step / (ms * 1e-3) / 1e9)
+        del graph
+
+    # Dominant kernel (gate/up shape): a graph of back-to-back launches over every layer's
+    # gate and up weights, timed with events on the stream the launches run on.
+    M = res["verify"]["M"]
+    N, Kd = 14336, 4096
+    outg = outs[N][:M]
+
+    def dom():
+        for lw in layers:
+            for name in ("gate", "up"):
+                K.w8a8_matmul(a[:M], sa[:M], *lw[name], out=outg, BLOCK_M=None)
+    dom()
+    torch.cuda.synchronize()
+    gdom = capture(dom)
+    launches = 2 * args.layers
+    ms = time_replays(gdom, max(5, args.steps // 2), 2)
+    us_launch = ms * 1e3 / launches
+    _, ck = K.w8a8_matmul(a[:M], sa[:M], *layers[0]["gate"], out=outg, BLOCK_M=None)
+    dom_bytes = w8a8_bytes(M, N, Kd)
+    res["dominant"] = dict(kernel=ck.name, M=M, N=N, K=Kd, us=us_launch, bytes=dom_bytes,
+                           GBps=dom_bytes / (us_launch * 1e-6) / 1e9, config=ck.config)
+    del gdom, layers
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_w4a16(args, K, torch):
+    """W4A16 over the same seven linears, int32-packed INT4 weights, M = 72 and 8."""
+    g = torch.Generator(device="cuda").manual_seed(3)
+    layers = []
+    for _ in range(args.layers):
+        lw = {}
+        for name, N, Kd in LINEARS:
+            wp = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, Kd // 8), dtype=torch.int32, device="cuda", generator=g)
+            sc = (torch.rand((N, Kd // 128), device="cuda", generator=g) * 0.018 + 0.002).half()
+            lw[name] = (wp, sc)
+        layers.append(lw)
+    x = torch.randn((300, 4096), device="cuda", generator=g).half()
+    x_ff = torch.randn((300, 14336), device="cuda", generator=g).half()
+    outs = {N: torch.empty((300, N), dtype=torch.float16, device="cuda") for N in {n for _, n, _ in LINEARS}}
+    res = {}
+    for label, M in (("verify", args.B * (args.k + 1)), ("decode", args.B)):
+        def step():
+            for lw in layers:
+                for name, N, Kd in LINEARS:
+                    K.w4a16_matmul(x[:M] if Kd == 4096 else x_ff[:M], *lw[name], out=outs[N][:M], BLOCK_M=None)
+        step()
+        torch.cuda.synchronize()
+        graph = capture(step)
+        log(f"w4a16 {label} M={M}")
+        ms = time_replays(graph, args.steps, args.warmup)
+        b = args.layers * sum(w4a16_bytes(M, N, Kd) for _, N, Kd in LINEARS)
+        flops = args.layers * sum(2 * M * N * Kd for _, N, Kd in LINEARS)
+        res[label] = dict(M=M, ms=ms, GBps=b / (ms * 1e-3) / 1e9, TFLOPs=flops / (ms * 1e-3) / 1e12)
+        del graph
+    del layers
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_attention(args, K, torch):
+    """INT8 paged verification attention (config 3): B=8, k=8, context 4096, fused vs QPP=1."""
+    from specq import gen
+    from specq.timing import do_bench
+
+    H, H_KV, D = 32, 8, 128
+    res = {}
+    for ctx in (1024, 4096):
+        B, ql = args.B, args.k + 1
+        L = ctx + ql
+        kc, vc, ks, vs, bt, cl = (t.cuda() for t in gen.paged_kv(B, [L] * B, H_KV, D, seed=5))
+        q = gen.queries(B, ql, H, D, seed=6).cuda()
+        out = torch.zeros_like(q)
+        b = attn_bytes(B, L, ql, H, H_KV, D, 4)
+        for name, qpp in (("fused", ql), ("qpp1", 1)):
+            fn = lambda: K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=qpp, out=out)  # noqa: E731
+            ms = do_bench(fn, warmup=5, rep=20)
+            res[f"ctx{ctx}_{name}"] = dict(us=ms * 1e3, GBps=b / (ms * 1e-3) / 1e9)
+        log(f"attention ctx={ctx}: fused {res[f'ctx{ctx}_fused']['us']:.1f} us")
+    return res
+
+
+def bench_plan_graph(args, K, torch):
+    """Config 4: one plan-buffer graph of a 4-layer INT8 stack (d_model 4096) captured at B=32,
+    k=8 (M=288), replayed over a seeded (B, k) trace; eager per-step time for comparison."""
+    import random
+
+    from specq import gen
+    from specq.plan import Plan
+
+    L, HID, QKV, FF = 4, 4096, 6144, 14336
+    H, H_KV, D, CTX = 32, 8, 128, 1024
+    B_MAX, KS = 32, (0, 2, 4, 8)
+    QL_MAX = max(KS) + 1
+    M_MAX = B_MAX * QL_MAX
+    gg = torch.Generator(device="cuda").manual_seed(9)
+
+    def w(N, Kd):
+        return (torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=gg),
+                torch.rand((N,), device="cuda", generator=gg) * 0.009 + 0.001)
+    layers = []
+    for i in range(L):
+        lw = dict(qkv=w(QKV, HID), o=w(HID, HID), gate=w(FF, HID), up=w(FF, HID), down=w(HID, FF))
+        lw["kv"] = [t.cuda() for t in gen.paged_kv(B_MAX, [CTX + QL_MAX] * B_MAX, H_KV, D, seed=20 + i)]
+        layers.append(lw)
+    a = torch.randint(-127, 128, (M_MAX, HID), dtype=torch.int8, device="cuda", generator=gg)
+    sa = torch.rand((M_MAX,), device="cuda", generator=gg) * 0.015 + 0.005
+    q_buf = gen.queries(B_MAX, QL_MAX, H, D, seed=8).cuda()
+    o_buf = torch.zeros_like(q_buf)
+    bufs = {n: torch.zeros(M_MAX, N, device="cuda", dtype=torch.float16)
+            for n, N in (("qkv", QKV), ("o", HID), ("gate", FF), ("up", FF), ("down", HID))}
+    hq = torch.zeros(M_MAX, FF, device="cuda", dtype=torch.int8)
+    hs = torch.zeros(M_MAX, device="cuda", dtype=torch.float32)
+    plan = Plan("cuda")
+
+    def step(B, ql, use_plan):
+        M = B * ql
+        kw = dict(plan=plan.gemm, grid_m_max=M_MAX) if use_plan else {}
+        aa, ss = (a, sa) if use_plan else (a[:M], sa[:M])
+        for lw in layers:
+            K.w8a8_matmul(aa, ss, *lw["qkv"], out=bufs["qkv"], BLOCK_M=None, **kw)
+            kc, vc, ks, vs, bt, cl = lw["kv"]
+            if use_plan:
+                K.paged_attention(q_buf, kc, vc, ks, vs, bt, cl, QL_MAX, QPP=QL_MAX, plan=plan.attn, out=o_buf)
+            else:
+                K.paged_attention(q_buf[:B], kc, vc, ks, vs, bt[:B], cl[:B], ql, QPP=ql, out=o_buf[:B])
+            K.w8a8_matmul(aa, ss, *lw["o"], out=bufs["o"], BLOCK_M=None, **kw)
+            K.w8a8_matmul(aa, ss, *lw["gate"], out=bufs["gate"], BLOCK_M=None, **kw)
+            K.w8a8_matmul(aa, ss, *lw["up"], out=bufs["up"], BLOCK_M=None, **kw)
+            gt, up = (bufs["gate"], bufs["up"]) if use_plan else (bufs["gate"][:M], bufs["up"][:M])
+            K.silu_mul_quant_int8(gt, up, q=hq if use_plan else hq[:M], s=hs if use_plan else hs[:M],
+                                  plan=kw.get("plan"), grid_m_max=kw.get("grid_m_max"))
+            h, hsc = (hq, hs) if use_plan else (hq[:M], hs[:M])
+            K.w8a8_matmul(h, hsc, *lw["down"], out=bufs["down"], BLOCK_M=None, **kw)
+
+    rng = random.Random(0)
+    trace = [(rng.randint(1, B_MAX), rng.choice(KS)) for _ in range(args.trace)]
+    for B in (1, B_MAX):
+        for k in KS:
+            step(B, k + 1, False)
+    plan.set(B_MAX, QL_MAX)
+    graph = capture(lambda: step(B_MAX, QL_MAX, True))
+
+    # Plan-graph replay latency per step (host perf_counter around replay + sync, as the
+    # reference's graph bench does), and eager launches of the same steps.
+    lat_plan, lat_eager = [], []
+    for B, k in trace:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        plan.set(B, k + 1)
+        graph.replay()
+        torch.cuda.synchronize()
+        lat_plan.append((time.perf_counter() - t0) * 1e3)
+    for B, k in trace[: max(20, args.trace // 5)]:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step(B, k + 1, False)
+        torch.cuda.synchronize()
+        lat_eager.append((time.perf_counter() - t0) * 1e3)
+    tokens = sum(B * (k + 1) for B, k in trace)
+    log(f"plan graph: P50 {statistics.median(lat_plan):.3f} ms over {len(trace)} steps")
+    return dict(steps=len(trace), plan_p50_ms=statistics.median(lat_plan),
+                plan_p99_ms=sorted(lat_plan)[int(0.99 * (len(lat_plan) - 1))],
+                plan_tokens_per_s=tokens / (sum(lat_plan) * 1e-3),
+                eager_p50_ms=statistics.median(lat_eager))
+
+
+def cpu_baseline(args, M: int, seconds: float):
+    """The CPU oracle (numpy) on one layer's seven linears at M, repeated for about `seconds`."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        cores = os.cpu_count() or 1
+    rng = np.random.default_rng(0)
+    ws = [(rng.integers(-127, 128, (N, Kd), dtype=np.int8), rng.uniform(0.001, 0.01, N).astype(np.float32))
+          for _, N, Kd in LINEARS]
+    a = rng.integers(-127, 128, (M, 14336), dtype=np.int8)
+    sa = rng.uniform(0.005, 0.02, M).astype(np.float32)
+    b_layer = sum(w8a8_bytes(M, N, Kd) for _, N, Kd in LINEARS)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        for (w, sw), (_, N, Kd) in zip(ws, LINEARS):
+            O.w8a8(a[:, :Kd], sa, w, sw)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 50:
+            break
+    return dict(value=round(reps * b_layer / el / 1e9, 3), unit="GB/s", cores=int(cores), kind="port",
+                sample=f"oracle.w8a8 (numpy) on one layer's 7 Llama-3-8B linears at M={M}, {reps} reps "
+                       f"in {el:.1f} s ({reps * b_layer / 1e9:.2f} GB of weights)")
+
+
+def read_traffic(kernel: str, M: int):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    e = t.get(f"{kernel}@M={M}")
+    return None if e is None else e.get("bytes_per_launch")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--B", type=int, default=8)
+    ap.add_argument("--k", type=int, default=8)
+    ap.add_argument("--trace", type=int, default=200, help="steps of the plan-graph (B, k) trace")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-detail", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: the verification kernels run on one GPU's share "
+              "and no multi-GPU path is built; run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (libspecq.so runs on MI355X only)", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+    import kernels as K
+
+    M = args.B * (args.k + 1)
+    torch.cuda.synchronize()
+    w = bench_w8a8(args, K, torch)
+    v, d, dom = w["verify"], w["decode"], w["dominant"]
+    detail = {"w8a8_verify": dict(M=v["M"], ms=round(v["ms"], 4), GBps=round(v["GBps"], 1)),
+              "w8a8_decode": dict(M=d["M"], ms=round(d["ms"], 4), GBps=round(d["GBps"], 1)),
+              "w8a8_verify_over_decode": round(v["ms"] / d["ms"], 4),
+              "dominant_kernel": dict(name=dom["kernel"], us=round(dom["us"], 3), **dom["config"])}
+    if not args.no_detail:
+        w4 = bench_w4a16(args, K, torch)
+        detail["w4a16_verify"] = {k: round(x, 4) for k, x in w4["verify"].items()}
+        detail["w4a16_decode"] = {k: round(x, 4) for k, x in w4["decode"].items()}
+        detail["w4a16_verify_over_decode"] = round(w4["verify"]["ms"] / w4["decode"]["ms"], 4)
+        detail["w4a16_verify_over_w8a8_decode"] = round(w4["verify"]["ms"] / d["ms"], 4)
+        detail["attention_B8_k8"] = {k: {kk: round(x, 2) for kk, x in r.items()}
+                                     for k, r in bench_attention(args, K, torch).items()}
+        detail["plan_graph_4layer"] = {k: round(x, 4) for k, x in bench_plan_graph(args, K, torch).items()}
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"cpu baseline (~{args.cpu_seconds:.0f} s)")
+        cpu = cpu_baseline(args, M, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(v["GBps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(v["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": f"W8A8 verification linears of Llama-3-8B: {args.layers} layers x 7 "
+                               f"(q,k,v,o,gate,up,down), M=B*(k+1)={M} (B={args.B}, k={args.k}), "
+                               f"one hipGraph replay per step",
+                   "M": M, "layers": args.layers, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic(dom["kernel"], M),
+                     "kernel": dom["kernel"], "algorithmic_bytes": dom["bytes"], "us_per_launch": round(dom["us"], 3)},
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
