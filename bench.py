@@ -6,7 +6,9 @@ batch M = B*(k+1) = 8*9 = 72.  One step is the linears of one verification forwa
 x 7 GEMMs = 224 launches streaming 6.98 GB of distinct INT8 weights (far beyond the 256 MiB
 Infinity Cache, so every step reads its weights from HBM).  The step is captured once into a
 hipGraph (torch.cuda.graph over the C-ABI launches) and replayed; inputs are resident in HBM
-before the timed region starts.
+before the timed region starts.  Weights are packed once, at load time, into the kernel's
+MFMA-fragment layout (pack_weight_int8; bit-identical results); the same step on row-major
+weights (the reference's w_q layout) is reported in `detail`.
 
   value        algorithmic HBM bytes of a step / step time, in GB/s (whole job, one GPU)
   roofline     the dominant kernel (the gate/up GEMM, 54% of the bytes): algorithmic bytes per
@@ -98,19 +100,22 @@ def time_replays(g, steps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) / steps
 
 
-def make_weights(L: int, seed: int = 0):
-    """L layers of the seven linears: int8 weights and fp32 per-channel scales, on the GPU."""
+def make_weights(K, L: int, seed: int = 0, packed: bool = True):
+    """L layers of the seven linears: int8 weights (packed MFMA fragments, or row-major) and
+    fp32 per-channel scales, on the GPU."""
     import torch
 
     g = torch.Generator(device="cuda").manual_seed(seed)
     layers = []
     for _ in range(L):
         lw = {}
-        for name, N, K in LINEARS:
-            w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g)
+        for name, N, Kd in LINEARS:
+            w = torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=g)
             sw = torch.rand((N,), device="cuda", generator=g) * 0.009 + 0.001
-            lw[name] = (w, sw)
+            lw[name] = (K.pack_weight_int8(w) if packed else w, sw)
+            del w
         layers.append(lw)
+    torch.cuda.synchronize()
     return layers
 
 
@@ -129,7 +134,7 @@ def w8a8_step_fn(K, layers, acts, M, outs):
 # Parts of the run
 # ------------------------------------------------------------------------------------------
 def bench_w8a8(args, K, torch):
-    layers = make_weights(args.layers, seed=1)
+    layers = make_weights(K, args.layers, seed=1, packed=True)
     g = torch.Generator(device="cuda").manual_seed(2)
     M_max = 300
     a = torch.randint(-127, 128, (M_max, 4096), dtype=torch.int8, device="cuda", generator=g)
@@ -170,6 +175,17 @@ def bench_w8a8(args, K, torch):
     res["dominant"] = dict(kernel=ck.name, M=M, N=N, K=Kd, us=us_launch, bytes=dom_bytes,
                            GBps=dom_bytes / (us_launch * 1e-6) / 1e9, config=ck.config)
     del gdom, layers
+    torch.cuda.empty_cache()
+    # The same verification step on row-major weights (the reference's w_q layout).
+    layers = make_weights(K, args.layers, seed=1, packed=False)
+    M = res["verify"]["M"]
+    step = w8a8_step_fn(K, layers, acts, M, outs)
+    step()
+    torch.cuda.synchronize()
+    graph = capture(step)
+    ms = time_replays(graph, args.steps, args.warmup)
+    res["verify_rowmajor"] = dict(M=M, ms=ms, GBps=res["verify"]["bytes"] / (ms * 1e-3) / 1e9)
+    del graph, layers
     torch.cuda.empty_cache()
     return res
 
@@ -387,7 +403,9 @@ def main() -> int:
     torch.cuda.synchronize()
     w = bench_w8a8(args, K, torch)
     v, d, dom = w["verify"], w["decode"], w["dominant"]
+    vr = w["verify_rowmajor"]
     detail = {"w8a8_verify": dict(M=v["M"], ms=round(v["ms"], 4), GBps=round(v["GBps"], 1)),
+              "w8a8_verify_rowmajor_weights": dict(M=vr["M"], ms=round(vr["ms"], 4), GBps=round(vr["GBps"], 1)),
               "w8a8_decode": dict(M=d["M"], ms=round(d["ms"], 4), GBps=round(d["GBps"], 1)),
               "w8a8_verify_over_decode": round(v["ms"] / d["ms"], 4),
               "dominant_kernel": dict(name=dom["kernel"], us=round(dom["us"], 3), **dom["config"])}
@@ -421,7 +439,7 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": f"W8A8 verification linears of Llama-3-8B: {args.layers} layers x 7 "
                                f"(q,k,v,o,gate,up,down), M=B*(k+1)={M} (B={args.B}, k={args.k}), "
-                               f"one hipGraph replay per step",
+                               f"weights packed at load, one hipGraph replay per step",
                    "M": M, "layers": args.layers, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),

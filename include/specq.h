@@ -60,10 +60,11 @@ const char* specq_last_error(void);
  *   c        fp16 [M, N], row stride ldc
  *   grid_m_max  rows the grid is sized for (>= M); 0 means M.  The reference's grid_m_max.
  *   plan     NULL, or device int32*: plan[0] = active M (kernels.py:35-38)
- *   block_m  token rows per workgroup: a multiple of 16, at most 320 (the reference's
- *            BLOCK_M; 16/32/64/128 are its values); 0 = choose from the M staircase.
- *   block_n  output channels per workgroup: 16, 32 or 64; 0 = auto.  (BLOCK_N)
- *   num_warps  64-wide waves per workgroup splitting K: 1, 2 or 4 (8 is taken as 4); 0 = 4.
+ *   block_m  token rows per workgroup: a multiple of 16, at most 304 (the reference's
+ *            BLOCK_M; 16/32/64/128 are its values); 0 = one chunk covering M.
+ *   block_n  output channels per workgroup: 16, 32, 64 or 128; 0 = auto.  (BLOCK_N)
+ *   num_warps  waves per workgroup of the byte-granular fallback kernel (unaligned operands):
+ *            1, 2 or 4 (8 is taken as 4); 0 = 4.  The streaming kernels always run 4 waves.
  *   split_k  workgroups splitting K; 0 = auto.  The INT32 result does not depend on it.
  * ------------------------------------------------------------------------------------- */
 size_t specq_w8a8_workspace_size(int m_grid, int N, int K, int block_m, int block_n,
@@ -75,12 +76,13 @@ int specq_w8a8(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
                void* workspace, size_t workspace_bytes, void* stream);
 
 /* W8A8 with the weight pre-packed once into MFMA fragments (the layout production inference
- * stacks "pre-shuffle" weights into at load time): packed[t][s][l*16 + b] =
- * w[16t + l%16][64s + 16*(l/16) + b] for 16-row tile t, 64-byte K step s, lane l, byte b,
- * zero-padded to whole tiles; specq_w8a8_packed_bytes() bytes.  Each 1 KB fragment is one
- * MFMA operand, so the GEMM reads it contiguously.  Results are bit-identical to specq_w8a8
- * on the unpacked weight.  No reference counterpart: w8a8_matmul (kernels.py:71-86) takes
- * the row-major weight only. */
+ * stacks "pre-shuffle" weights into at load time), stored K-step-major:
+ * packed[s][t][l*16 + b] = w[16t + l%16][64s + 16*(l/16) + b] for 64-byte K step s, 16-row
+ * tile t (ceil(N/16) tiles per step), lane l, byte b, zero-padded to whole tiles;
+ * specq_w8a8_packed_bytes() bytes.  Each 1 KB fragment is one MFMA operand, and the
+ * workgroups running at one time read one compact window of the buffer.  Results are
+ * bit-identical to specq_w8a8 on the unpacked weight.  No reference counterpart:
+ * w8a8_matmul (kernels.py:71-86) takes the row-major weight only. */
 size_t specq_w8a8_packed_bytes(int N, int K);
 int specq_w8a8_pack_weight(const int8_t* w, int64_t ldw, int N, int K, void* packed, void* stream);
 size_t specq_w8a8_packed_workspace_size(int m_grid, int N, int K, int block_m, int block_n,
@@ -91,10 +93,10 @@ int specq_w8a8_packed(const int8_t* a, int64_t lda, const void* w_packed,
                       int block_m, int block_n, int num_warps, int split_k,
                       void* workspace, size_t workspace_bytes, void* stream);
 
-/* Tuning options.  "w8a8_path": W8A8 kernel family for 16-byte aligned operands,
- * 0 = automatic, 1 = register streaming, 2 = LDS-DMA ring (row-major weights only),
- * 3 = byte-granular register kernel (row-major weights only), 4 = streaming with
- * LDS-shared activations.  Every family computes the same INT32 sums, so results do not
+/* Tuning options.  "w8a8_path": W8A8 kernel family, 0 = automatic, 1 = direct-activation
+ * streaming kernel (16-row token tiles), 2 = streaming with LDS-staged activations (tiles of
+ * 32 rows or more; 16-row requests use family 1), 3 = byte-granular register kernel
+ * (row-major weights only).  Every family computes the same INT32 sums, so results do not
  * change. */
 int specq_set_option(const char* name, int value);
 

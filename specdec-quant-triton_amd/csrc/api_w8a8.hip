@@ -1,52 +1,35 @@
 // C ABI for the W8A8 GEMM: argument validation, kernel-family and tile selection, launch.
 //
 // Kernel families (all compute identical INT32 sums, so every choice is bit-identical):
-//   STREAM  register-streaming kernel (w8a8_stream.hpp), 16-byte aligned operands; takes the
-//           row-major weight or the packed-fragment weight.  Default.
-//   STREAM2 streaming kernel with LDS-shared activations (w8a8_stream2.hpp) for deeper M
-//           tiles, 16-byte aligned operands, either weight layout.
-//   DMA     LDS-DMA ring kernel (w8a8_dma.hpp), 16-byte aligned row-major weights.
+//   RK      direct-activation streaming kernel (w8a8_rk.hpp) for 16-row token tiles: weights
+//           and activations go straight from memory into MFMA operand registers.
+//   WS      weight streaming with LDS-staged activations (w8a8_ws.hpp) for deeper token tiles.
 //   LEGACY  register-pipelined kernel with 16/8/4/1-byte loads (w8a8.hpp): any alignment.
+// RK and WS read the row-major weight or the packed K-step-major fragments and need 16-byte
+// aligned activation rows.
 #include <algorithm>
 #include <atomic>
 
 #include "api_common.hpp"
 #include "w8a8.hpp"
-#include "w8a8_stream.hpp"
+#include "w8a8_tiles.hpp"
 
 namespace specq {
 
 const void* w8a8_kernel_rw1(int mt, int vec);
 const void* w8a8_kernel_rw2(int mt, int vec);
 const void* w8a8_kernel_rw4(int mt, int vec);
-#define SPECQ_DMA_DECL(R, N)                     \
-  const void* w8a8_dma_kernel_r##R##n##N(int mt); \
-  int w8a8_dma_lds_r##R##n##N(int mt);
-SPECQ_DMA_DECL(1, 1)
-SPECQ_DMA_DECL(1, 2)
-SPECQ_DMA_DECL(1, 4)
-SPECQ_DMA_DECL(2, 1)
-SPECQ_DMA_DECL(2, 2)
-SPECQ_DMA_DECL(2, 4)
-#undef SPECQ_DMA_DECL
-const void* w8a8_stream_kernel_l0r1(int mt);
-const void* w8a8_stream_kernel_l0r2(int mt);
-const void* w8a8_stream_kernel_l1r1(int mt);
-const void* w8a8_stream_kernel_l1r2(int mt);
-const void* w8a8_stream2_kernel_l0r1(int mt, int* lds);
-const void* w8a8_stream2_kernel_l0r2(int mt, int* lds);
-const void* w8a8_stream2_kernel_l1r1(int mt, int* lds);
-const void* w8a8_stream2_kernel_l1r2(int mt, int* lds);
 
-// Packs a row-major int8 weight [N, K] (row stride ldw) into MFMA fragments:
-// packed[t][s][l*16 + b] = W[16t + l%16][64s + 16*(l/16) + b], zero-padded to whole tiles.
+// Packs a row-major int8 weight [N, K] (row stride ldw) into MFMA fragments stored K-step-major:
+// packed[s][t][l*16 + b] = W[16t + l%16][64s + 16*(l/16) + b], zero-padded to whole tiles,
+// with s the 64-byte K step and t the 16-row tile (ntiles = ceil(N/16) tiles per step).
 __global__ __launch_bounds__(256) void w8a8_pack_kernel(const int8_t* __restrict__ W, int64_t ldw, int N, int K,
                                                         int8_t* __restrict__ out) {
   const int ksteps = (K + 63) / 64;
-  const int64_t frag = blockIdx.x * 4 + (threadIdx.x >> 6);  // one wave per fragment
   const int ntiles = (N + 15) / 16;
+  const int64_t frag = blockIdx.x * 4 + (threadIdx.x >> 6);  // one wave per fragment
   if (frag >= (int64_t)ntiles * ksteps) return;
-  const int t = (int)(frag / ksteps), s = (int)(frag % ksteps);
+  const int s = (int)(frag / ntiles), t = (int)(frag % ntiles);
   const int l = threadIdx.x & 63;
   const int row = 16 * t + (l & 15), k0 = 64 * s + 16 * (l >> 4);
   int w4[4];
@@ -69,12 +52,13 @@ std::atomic<int> g_w8a8_path{0};
 
 namespace {
 
-enum Family { kStream = 1, kDma = 2, kLegacy = 3, kStream2 = 4 };
+enum Family { kRk = 1, kWs = 2, kLegacy = 3 };
 
 struct W8A8Cfg {
   int family, layout;
   int mt, rw, nw, vec, splits, k_range, n_tiles, m_chunks;
-  int nwn, bn;  // DMA: waves along N; channels per workgroup (all families)
+  int bn;         // channels per workgroup
+  int bnsel;      // RK/WS channel-width variant (0..3 for 16/32/64/128)
   size_t lds, ws_partials, ws_counters;
   const void* fn;
 };
@@ -96,28 +80,21 @@ const void* legacy_fn(int mt, int rw, int vec) {
   return nullptr;
 }
 
-const void* dma_fn(int mt, int rw, int nwn, int* lds) {
-  const void* fn = nullptr;
-#define SPECQ_DMA_PICK(R, N)             \
-  if (rw == R && nwn == N) {             \
-    fn = w8a8_dma_kernel_r##R##n##N(mt); \
-    *lds = w8a8_dma_lds_r##R##n##N(mt);  \
+const void* ws_fn(int bnsel, int layout, int mt) {
+  switch (bnsel * 2 + layout) {
+    case 0: return w8a8_ws_fn_n16_l0(mt);
+    case 1: return w8a8_ws_fn_n16_l1(mt);
+    case 2: return w8a8_ws_fn_n32_l0(mt);
+    case 3: return w8a8_ws_fn_n32_l1(mt);
+    case 4: return w8a8_ws_fn_n64_l0(mt);
+    case 5: return w8a8_ws_fn_n64_l1(mt);
+    case 6: return w8a8_ws_fn_n128_l0(mt);
+    case 7: return w8a8_ws_fn_n128_l1(mt);
   }
-  SPECQ_DMA_PICK(1, 1) SPECQ_DMA_PICK(1, 2) SPECQ_DMA_PICK(1, 4)
-  SPECQ_DMA_PICK(2, 1) SPECQ_DMA_PICK(2, 2) SPECQ_DMA_PICK(2, 4)
-#undef SPECQ_DMA_PICK
-  return fn;
+  return nullptr;
 }
 
-const void* stream_fn(int layout, int mt, int rw) {
-  if (layout == 0) return rw == 1 ? w8a8_stream_kernel_l0r1(mt) : w8a8_stream_kernel_l0r2(mt);
-  return rw == 1 ? w8a8_stream_kernel_l1r1(mt) : w8a8_stream_kernel_l1r2(mt);
-}
-
-const void* stream2_fn(int layout, int mt, int rw, int* lds) {
-  if (layout == 0) return rw == 1 ? w8a8_stream2_kernel_l0r1(mt, lds) : w8a8_stream2_kernel_l0r2(mt, lds);
-  return rw == 1 ? w8a8_stream2_kernel_l1r1(mt, lds) : w8a8_stream2_kernel_l1r2(mt, lds);
-}
+int bn_of_sel(int sel) { return 16 << sel; }
 
 // Resolve the kernel and its tiles.  `vec` is the operand alignment (16 when unknown),
 // `layout` 0 = row-major weight, 1 = packed fragments.
@@ -129,61 +106,44 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   const int rows16 = ceil_div(m_grid > 0 ? m_grid : 1, 16);
   int mt;
   if (block_m > 0) {
-    SPECQ_REQUIRE(block_m % 16 == 0 && block_m <= 320, SPECQ_ENOTSUP,
-                  "w8a8: BLOCK_M=%d must be a multiple of 16 and at most 320", block_m);
+    SPECQ_REQUIRE(block_m % 16 == 0 && block_m <= 16 * kW8A8MaxMt, SPECQ_ENOTSUP,
+                  "w8a8: BLOCK_M=%d must be a multiple of 16 and at most %d", block_m, 16 * kW8A8MaxMt);
     mt = block_m / 16;
   } else {
-    const int chunks = ceil_div(rows16, 20);
+    // One chunk of token rows covering M (the weight is then read once), split evenly when
+    // M exceeds the deepest tile.
+    const int chunks = ceil_div(rows16, kW8A8MaxMt);
     mt = ceil_div(rows16, chunks);
   }
-  int nw = num_warps <= 0 ? 4 : (num_warps >= 4 ? 4 : (num_warps >= 2 ? 2 : 1));
   const int path = g_w8a8_path.load();
-  // Automatic family: the LDS-shared-activation kernel once there are 3 or more token blocks
-  // (its activation fragments then no longer fit the register-streaming kernel's budget).
-  const bool s2_auto = path == 0 && rows16 >= 3 && block_n != 16 && block_n != 32;
   int family;
   if (vec != 16) family = kLegacy;
-  else if (layout == 1) family = (path == kStream2 || s2_auto) ? kStream2 : kStream;
-  else if (s2_auto) family = kStream2;
-  else family = (path == kDma || path == kLegacy || path == kStream2) ? path : kStream;
+  else if (path == kLegacy && layout == 0) family = kLegacy;
+  else if (path == kRk) family = kRk;
+  else if (path == kWs && mt >= 2) family = kWs;
+  else family = mt == 1 ? kRk : kWs;
 
-  int rw = 1, nwn = 1, dma_lds = 0;
+  int nw = 4, rw = 1, bnsel = 2;
   const void* fn = nullptr;
-  if (family == kStream2) {
-    // 4 waves side by side along N, RW x 16 channels each.
-    if (block_n == 16 || block_n == 32) {
-      family = kStream;
+  if (family == kRk || family == kWs) {
+    if (block_n > 0) {
+      bnsel = block_n == 16 ? 0 : (block_n == 32 ? 1 : (block_n == 64 ? 2 : 3));
     } else {
-      const int tiles64 = ceil_div(N, 64);
-      rw = block_n == 128 ? 2 : (block_n == 0 && rows16 >= 18 && tiles64 >= 64 ? 2 : 1);
-      if (block_m <= 0) {
-        // Measured on the Llama-3-8B linears: wide N has tiles enough to fill the CUs with
-        // deep M tiles (one weight pass); narrow N does better with 48-row tiles and more
-        // workgroups (the extra weight passes hit L2).
-        const int cap = tiles64 >= 128 ? 9 : 3;
-        const int chunks = ceil_div(rows16, cap);
-        mt = ceil_div(rows16, chunks);
-      }
-      nw = 4;
-      fn = stream2_fn(layout, mt, rw, &dma_lds);
-      if (!fn) family = kStream;  // tile too deep for the LDS activation ring
+      // Measured on the Llama-3-8B linears: wide N fills the CUs with 64-channel tiles whose 4
+      // waves share each activation fragment; narrower N gets 16-channel tiles (4 times the
+      // workgroups) whose waves split K.
+      bnsel = ceil_div(N, 64) >= 192 ? 2 : 0;
     }
-  }
-  if (family == kDma) {
-    // 4 waves: NWN along N (RW x 16 channels each), 4/NWN along K.
-    const int bn = block_n > 0 ? block_n : (N <= 2048 ? 16 : 64);
-    if (bn == 16) { rw = 1; nwn = 1; }
-    else if (bn == 32) { rw = num_warps == 2 ? 2 : 1; nwn = num_warps == 2 ? 1 : 2; }
-    else if (bn == 64) { rw = num_warps == 2 ? 2 : 1; nwn = num_warps == 2 ? 2 : 4; }
-    else { rw = 2; nwn = 4; }
-    nw = 4;
-    fn = dma_fn(mt, rw, nwn, &dma_lds);
-    if (!fn) { rw = 1; nwn = 1; fn = dma_fn(mt, rw, nwn, &dma_lds); }  // deepest M tiles
-    if (!fn) family = kStream;                                          // BLOCK_M > 288
-  }
-  if (family == kStream) {
-    rw = (block_n >= 32) ? 2 : (block_n == 16 ? 1 : (N <= 2048 ? 1 : 2));
-    fn = stream_fn(layout, mt, rw);
+    if (family == kRk) {
+      if (mt > 1) {
+        // The direct-activation kernel holds one 16-row token tile: deeper BLOCK_M requests
+        // are served as several 16-row chunks.
+        mt = 1;
+      }
+      fn = w8a8_rk_fn(bnsel, layout);
+    } else {
+      fn = ws_fn(bnsel, layout, mt);
+    }
   }
   if (family == kLegacy) {
     rw = block_n > 0 ? (block_n >= 64 ? 4 : block_n / 16) : (N <= 16 ? 1 : 2);
@@ -192,24 +152,21 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
     if (mt_eff < 0 && rw > 1) { rw = 1; mt_eff = round_mt_for_vec(mt, vec, rw); }
     SPECQ_REQUIRE(mt_eff > 0, SPECQ_ENOTSUP, "w8a8: no kernel for BLOCK_M=%d at %d-byte alignment", mt * 16, vec);
     mt = mt_eff;
+    nw = num_warps <= 0 ? 4 : (num_warps >= 4 ? 4 : (num_warps >= 2 ? 2 : 1));
     fn = legacy_fn(mt, rw, vec);
   }
   SPECQ_REQUIRE(fn != nullptr, SPECQ_ENOTSUP, "w8a8: no kernel for BLOCK_M=%d BLOCK_N=%d", mt * 16, block_n);
 
   cfg->family = family; cfg->layout = layout; cfg->fn = fn;
-  cfg->mt = mt; cfg->rw = rw; cfg->nw = nw; cfg->vec = vec; cfg->nwn = nwn;
-  cfg->bn = family == kDma ? nwn * rw * 16 : (family == kStream2 ? 4 * rw * 16 : rw * 16);
+  cfg->mt = mt; cfg->rw = rw; cfg->nw = nw; cfg->vec = vec; cfg->bnsel = bnsel;
+  cfg->bn = family == kLegacy ? rw * 16 : bn_of_sel(bnsel);
   cfg->n_tiles = ceil_div(N, cfg->bn);
   cfg->m_chunks = ceil_div(m_grid > 0 ? m_grid : 1, mt * 16);
   const int BM = mt * 16, BN = cfg->bn;
-  if (family == kDma) {
-    cfg->lds = (size_t)dma_lds;
-  } else if (family == kStream2) {
-    cfg->lds = 0;  // static LDS (one variable per ring slot)
-  } else if (family == kStream) {
-    const size_t stage = layout == 0 ? (size_t)nw * rw * 4096 : 0;
-    const size_t red = nw > 1 ? (size_t)BM * (BN + kW8A8Pad) * 4 : 0;
-    cfg->lds = stage > red ? stage : red;
+  if (family == kRk) {
+    cfg->lds = bnsel <= 1 ? (size_t)BM * BN * 4 : 0;  // cross-wave reduction slice
+  } else if (family == kWs) {
+    cfg->lds = 0;  // static LDS
   } else {
     cfg->lds = nw > 1 ? (size_t)BM * (BN + kW8A8Pad) * 4 : 0;
   }
@@ -218,22 +175,23 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   int splits;
   if (split_k > 0) {
     splits = split_k;
-  } else {
-    // Fill the CUs: about two resident workgroups per CU (LDS permitting), >= 2 K steps per wave.
-    const bool lds_bound = family == kDma || family == kStream2;
-    const int per_cu = lds_bound ? (dma_lds > 0 ? std::max(1, 163840 / dma_lds) : 1) : 2;
-    const int target = per_cu * device_cus();
+  } else if (family == kLegacy) {
+    const int target = 2 * device_cus();
     const int base = cfg->n_tiles * cfg->m_chunks;
     splits = 4 * base >= 3 * target ? 1 : ceil_div(target, base);
-    // K steps per split: >= 2 per wave when waves split K, >= 4 blocks when they split N.
-    int max_splits = family == kStream2 ? ksteps / 16 : ksteps / (2 * nw);
-    if (max_splits < 1) max_splits = 1;
-    if (splits > max_splits) splits = max_splits;
+    const int max_splits = std::max(1, ksteps / (2 * nw));
+    splits = std::min(splits, max_splits);
+  } else if (family == kWs && bnsel == 0 && cfg->n_tiles * cfg->m_chunks < 128) {
+    // Few 16-channel tiles (e.g. the 1024-wide k/v projections): split K up to 4 ways.
+    splits = std::min(4, std::max(1, 256 / (cfg->n_tiles * cfg->m_chunks)));
+  } else {
+    splits = 1;
   }
-  // Split boundaries on whole 256-byte blocks keep the streaming kernel's fetches aligned.
-  const int quantum = (family == kStream || family == kStream2) ? 4 : 1;
+  // Split boundaries on whole 256-byte blocks (one activation chunk of the streaming kernels).
+  const int quantum = family == kLegacy ? 1 : 4;
   const int kq = ceil_div(ksteps, quantum);
   if (splits > kq) splits = kq;
+  if (splits < 1) splits = 1;
   const int k_range = ceil_div(kq, splits) * quantum * 64;
   splits = ceil_div(K, k_range);
   cfg->splits = splits;
@@ -306,12 +264,10 @@ int w8a8_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, i
   if (rc) return rc;
   hipFuncAttributes fa;
   if (hipFuncGetAttributes(&fa, cfg.fn) != hipSuccess) return fail(SPECQ_EIO, "w8a8: hipFuncGetAttributes failed");
-  if (cfg.family == kDma)
-    snprintf(out->name, sizeof(out->name), "specq::w8a8_dma_kernel<%d,%d,%d>", cfg.mt, cfg.rw, cfg.nwn);
-  else if (cfg.family == kStream)
-    snprintf(out->name, sizeof(out->name), "specq::w8a8_stream_kernel<%d,%d,%d>", cfg.mt, cfg.rw, cfg.layout);
-  else if (cfg.family == kStream2)
-    snprintf(out->name, sizeof(out->name), "specq::w8a8_stream2_kernel<%d,%d,%d>", cfg.mt, cfg.rw, cfg.layout);
+  if (cfg.family == kRk)
+    snprintf(out->name, sizeof(out->name), "specq::w8a8_rk_kernel<1,BN%d,%d>", cfg.bn, cfg.layout);
+  else if (cfg.family == kWs)
+    snprintf(out->name, sizeof(out->name), "specq::w8a8_ws_kernel<%d,BN%d,%d>", cfg.mt, cfg.bn, cfg.layout);
   else
     snprintf(out->name, sizeof(out->name), "specq::w8a8_kernel<%d,%d,%d>", cfg.mt, cfg.rw, cfg.vec);
   out->num_regs = fa.numRegs;
@@ -382,7 +338,7 @@ extern "C" int specq_set_option(const char* name, int value) {
   clear_error();
   SPECQ_REQUIRE(name != nullptr, SPECQ_EINVAL, "set_option: null name");
   if (strcmp(name, "w8a8_path") == 0) {
-    SPECQ_REQUIRE(value >= 0 && value <= 4, SPECQ_EINVAL, "set_option: w8a8_path must be 0..4");
+    SPECQ_REQUIRE(value >= 0 && value <= 3, SPECQ_EINVAL, "set_option: w8a8_path must be 0..3");
     g_w8a8_path.store(value);
     return SPECQ_OK;
   }

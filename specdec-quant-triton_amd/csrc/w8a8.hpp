@@ -79,6 +79,39 @@ __device__ __forceinline__ void w8a8_store4(const W8A8Params& p, int m, int n, v
   }
 }
 
+// Split-K hand-off of a workgroup's INT32 tile [BM][BN] (row = token), 16 bytes per lane.
+// Partials of tile cidx live at p.partials + cidx * splits * BM * BN, split-major.
+template <int BM, int BN>
+__device__ __forceinline__ rsrc_t w8a8_partials_rsrc(const W8A8Params& p, int cidx) {
+  return make_rsrc(p.partials + (int64_t)cidx * p.splits * (BM * BN), (uint32_t)(p.splits * BM * BN * 4));
+}
+// Publish the quad of channels nl..nl+3 (tile-local) of token row ml (tile-local).
+template <int BM, int BN>
+__device__ __forceinline__ void w8a8_publish_quad(rsrc_t prs, int split, int ml, int nl, v4i v) {
+  publish16(prs, (uint32_t)(((split * BM + ml) * BN + nl) * 4), v);
+}
+// Called by every thread after its publishes: the last workgroup of the tile to arrive sums
+// the splits (all of a quad's loads in flight together) and applies the epilogue.
+template <int BM, int BN>
+__device__ __forceinline__ void w8a8_splitk_finish(const W8A8Params& p, rsrc_t prs, int cidx, int m0, int nbase,
+                                                   int M, int* s_last) {
+  if (!arrive_last(p.counters + cidx, p.splits, s_last)) return;
+  constexpr int QUADS = BM * BN / 4;
+  for (int q = threadIdx.x; q < QUADS; q += blockDim.x) {
+    const int ml = q / (BN / 4), nl = (q % (BN / 4)) * 4;
+    v4i s = {0, 0, 0, 0};
+    for (int sp0 = 0; sp0 < p.splits; sp0 += 4) {
+      v4i t[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        t[u] = collect16(prs, oob_unless(sp0 + u < p.splits, (uint32_t)((((sp0 + u) * BM + ml) * BN + nl) * 4)));
+      s += (t[0] + t[1]) + (t[2] + t[3]);
+    }
+    const int m = m0 + ml, n = nbase + nl;
+    if (m < M && n < p.N) w8a8_store4(p, m, n, s);
+  }
+}
+
 template <int MT, int RW, int VEC>
 __global__ __launch_bounds__(256) void w8a8_kernel(W8A8Params p) {
   constexpr int BM = MT * 16, BN = RW * 16, U = W8A8Unroll<MT, RW>::value;

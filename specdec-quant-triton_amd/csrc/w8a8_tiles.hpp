@@ -1,0 +1,57 @@
+// Tile table of the W8A8 streaming kernels (rk: M <= 16 per chunk, direct activation loads;
+// ws: LDS-staged activations), shared by the instantiation units and the C-ABI dispatcher.
+//
+// A channel width BLOCK_N maps to how the 4 waves of a workgroup split the work:
+//   16  -> all 4 waves on the same 16 channels, each a quarter of the K steps (KW = 4)
+//   32  -> 2 x 16 channels, K split 2 ways                                    (KW = 2)
+//   64  -> 4 x 16 channels, the waves walk the same K steps                   (KW = 1)
+//   128 -> 4 x 32 channels                                                     (KW = 1, RW = 2)
+// The ws kernel's activation ring holds 4 chunks up to 144 token rows and 2 beyond; a chunk
+// covers 256 bytes of K (S K steps of each of the KW waves).
+#pragma once
+#include "w8a8_rk.hpp"
+#include "w8a8_ws.hpp"
+
+namespace specq {
+
+constexpr int kW8A8MaxMt = 19;  // deepest token tile (304 rows)
+
+template <int BNSEL>  // 0: 16, 1: 32, 2: 64, 3: 128 channels
+struct W8A8BnSel {
+  static constexpr int KW = BNSEL == 0 ? 4 : (BNSEL == 1 ? 2 : 1);
+  static constexpr int RW = BNSEL == 3 ? 2 : 1;
+  static constexpr int S = 4 / KW;  // K steps per wave per 256-byte chunk
+};
+
+template <int MT, int BNSEL>
+struct W8A8WsPick {
+  using B = W8A8BnSel<BNSEL>;
+  static constexpr int NSLOT = (MT <= 9 && !(B::RW == 2 && MT >= 8)) ? 4 : 2;
+  using Cfg = W8A8WsCfg<MT, B::RW, B::KW, B::S, NSLOT, 4>;
+};
+
+template <int MT, int BNSEL, int WL>
+const void* w8a8_ws_pick() {
+  using P = W8A8WsPick<MT, BNSEL>;
+  using B = W8A8BnSel<BNSEL>;
+  return reinterpret_cast<const void*>(&w8a8_ws_kernel<MT, B::RW, B::KW, B::S, P::NSLOT, 4, WL>);
+}
+
+template <int BNSEL, int WL>
+const void* w8a8_rk_pick() {
+  using B = W8A8BnSel<BNSEL>;
+  return reinterpret_cast<const void*>(&w8a8_rk_kernel<1, B::RW, B::KW, 4, WL>);
+}
+
+// Defined in the instantiation units.
+const void* w8a8_ws_fn_n16_l0(int mt);
+const void* w8a8_ws_fn_n16_l1(int mt);
+const void* w8a8_ws_fn_n32_l0(int mt);
+const void* w8a8_ws_fn_n32_l1(int mt);
+const void* w8a8_ws_fn_n64_l0(int mt);
+const void* w8a8_ws_fn_n64_l1(int mt);
+const void* w8a8_ws_fn_n128_l0(int mt);
+const void* w8a8_ws_fn_n128_l1(int mt);
+const void* w8a8_rk_fn(int bnsel, int layout);
+
+}  // namespace specq

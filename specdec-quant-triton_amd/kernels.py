@@ -24,8 +24,8 @@ reference) restate the reference formulas in torch and run on any device.
 Differences a caller may notice:
   * BLOCK_K and num_stages are accepted and ignored (the MFMA K step and register
     pipelining are fixed per kernel).  BLOCK_M=None (or 0) picks the tile from the measured
-    M staircase.  W8A8 BLOCK_N is 16/32/64/128 channels per workgroup (larger values are taken
-    as 128); W4A16 BLOCK_N is 64 or 128.
+    M staircase.  W8A8 BLOCK_M is at most 304; BLOCK_N is 16/32/64/128 channels per
+    workgroup (larger values are taken as 128); W4A16 BLOCK_N is 64 or 128.
   * w8a8_matmul also accepts a PackedWeightInt8 (pack_weight_int8), the weight pre-packed
     once into MFMA fragments, with bit-identical results.
   * `ck` is a KernelInfo with n_regs / n_spills / metadata.shared like Triton's compiled
@@ -177,9 +177,10 @@ def _w8a8_block_n(block_n) -> int:
 class PackedWeightInt8:
     """An int8 weight [N, K] pre-packed once into MFMA fragments for w8a8_matmul.
 
-    Fragment (16-row tile t, 64-byte K step s) is 1 KB holding, for lane l and byte b,
-    w[16t + l%16][64s + 16*(l/16) + b] (zero-padded), so the GEMM streams it contiguously.
-    Results are bit-identical to passing the row-major weight.
+    Fragments are stored K-step-major: fragment (64-byte K step s, 16-row tile t) is the 1 KB
+    at (s * ceil(N/16) + t) KB holding, for lane l and byte b, w[16t + l%16][64s + 16*(l/16) + b]
+    (zero-padded), so every load is 1 KB contiguous and the workgroups running at one time
+    read one compact window.  Results are bit-identical to passing the row-major weight.
     """
 
     def __init__(self, w_q: torch.Tensor):

@@ -1,18 +1,19 @@
 """M-tile selection (the reference's BLOCK_M choice, bench_matmul.py:76-99, REPORT.md:81).
 
 The reference sweeps tile configs per M and reports that BLOCK_M should follow M.  Here a
-BLOCK_M of 0 hands the choice to the library, whose rule was fitted to measured sweeps on
-MI355X (W8A8: register-streaming kernel with the whole M-chunk in registers up to 32 rows,
-then the LDS-shared-activation kernel with 48-row tiles for narrow N and up to 144-row tiles
-for wide N; W4A16: one chunk of up to 256 rows for wide N, 48-row chunks for narrow N).
-STAIRCASE overrides it per (kind, N, K) with the best measured BLOCK_M for each M bucket.
+BLOCK_M of 0 hands the choice to the library, whose rule follows from measured sweeps on
+MI355X: W8A8 takes one chunk of token rows covering M (up to 304 rows), so every weight byte
+is read from HBM once, with the direct-activation streaming kernel for 16-row chunks and the
+LDS-staged-activation kernel above; W4A16 takes one chunk of up to 256 rows for wide N and
+48-row chunks for narrow N.  STAIRCASE overrides it per (kind, N, K) with the best measured
+BLOCK_M for each M bucket.
 """
 from __future__ import annotations
 
 # (kind, N, K) -> sorted list of (max_M, BLOCK_M); filled from measured sweeps.
 STAIRCASE: dict = {}
 
-_MAX_BM = {"w8a8": 320, "w4a16": 256}
+_MAX_BM = {"w8a8": 304, "w4a16": 256}
 
 
 def default_block_m(kind: str, m: int) -> int:

@@ -93,14 +93,14 @@ def test_w8a8_split_k_and_tiles_bit_identical(split_k):
 
 @pytest.mark.parametrize("bn_nw", [(16, 4), (32, 4), (32, 2), (64, 4), (64, 2), (128, 4)])
 def test_w8a8_every_tile_shape_and_block_m(bn_nw):
-    # Every channel-block shape of the aligned (LDS-DMA) path at every BLOCK_M bucket,
+    # Every channel-block shape of the aligned streaming paths at every BLOCK_M bucket,
     # including the deep tiles that change the K-chunk length.
     bn, nw = bn_nw
     note(f"w8a8 tile sweep BLOCK_N={bn} warps={nw}")
     a, w, sa, sw = gen.w8a8_inputs(300, 1000, 1536, seed=31)
     ref = O.w8a8(a.numpy(), sa.numpy(), w.numpy(), sw.numpy())
     a, w, sa, sw = (t.to(DEV) for t in (a, w, sa, sw))
-    for bm in (16, 32, 48, 80, 144, 192, 208, 304, 320):
+    for bm in (16, 32, 48, 80, 144, 192, 208, 288, 304):
         for M in sorted({1, min(bm, 300), min(bm + 5, 300), 300}):
             out, ck = K.w8a8_matmul(a[:M], sa[:M], w, sw, BLOCK_M=bm, BLOCK_N=bn, num_warps=nw)
             torch.cuda.synchronize()
@@ -122,8 +122,10 @@ def test_w8a8_packed_weight_bit_exact(shape):
             assert_bitexact_fp16(out, ref[:M], f"packed N={N} K={Kd} M={M} bn={bn} nw={nw} sk={sk}")
 
 
-@pytest.mark.parametrize("path", [1, 2, 3, 4])
+@pytest.mark.parametrize("path", [1, 2, 3])
 def test_w8a8_kernel_families_bit_identical(path):
+    # w8a8_path 1: direct-activation streaming kernel (16-row token tiles), 2: LDS-staged
+    # activations (deeper tiles), 3: byte-granular legacy kernel.  All sum the same INT32s.
     from specq import _lib
     note(f"w8a8 kernel family {path}")
     a, w, sa, sw = gen.w8a8_inputs(300, 1000, 1536, seed=51)
@@ -133,35 +135,32 @@ def test_w8a8_kernel_families_bit_identical(path):
     try:
         for M in (1, 17, 72, 300):
             for bm in (None, 16, 64):
-                out, ck = K.w8a8_matmul(a[:M], sa[:M], w, sw, BLOCK_M=bm, BLOCK_N=32, num_warps=4)
-                torch.cuda.synchronize()
-                assert_bitexact_fp16(out, ref[:M], f"path={path} M={M} BLOCK_M={bm} ({ck.name})")
+                for bn in (None, 16, 32, 64, 128):
+                    out, ck = K.w8a8_matmul(a[:M], sa[:M], w, sw, BLOCK_M=bm, BLOCK_N=bn, num_warps=4)
+                    torch.cuda.synchronize()
+                    assert_bitexact_fp16(out, ref[:M], f"path={path} M={M} BLOCK_M={bm} BLOCK_N={bn} ({ck.name})")
     finally:
         _lib.set_option("w8a8_path", 0)
 
 
 @pytest.mark.parametrize("layout", [0, 1])
-def test_w8a8_lds_shared_activation_family(layout):
-    # Streaming kernel with LDS-shared activations: every tile depth it is built for, both
-    # channel widths, K tails that are not whole 256-byte blocks, N tails, explicit split-K.
-    from specq import _lib
-    _lib.set_option("w8a8_path", 4)
-    try:
-        for N, Kd in ((1000, 1552), (4096, 4096)):
-            note(f"w8a8 stream2 layout={layout} N={N} K={Kd}")
-            a, w, sa, sw = gen.w8a8_inputs(300, N, Kd, seed=61 + N)
-            ref = O.w8a8(a.numpy(), sa.numpy(), w.numpy(), sw.numpy())
-            a, w, sa, sw = (t.to(DEV) for t in (a, w, sa, sw))
-            wt = K.pack_weight_int8(w) if layout == 1 else w
-            for bm in (None, 32, 80, 160, 256):
-                for M in (1, 17, 72, 130, 300):
-                    for bn, sk in ((None, 0), (64, 1), (128, 0), (64, 3)):
-                        out, ck = K.w8a8_matmul(a[:M], sa[:M], wt, sw, BLOCK_M=bm, BLOCK_N=bn, split_k=sk)
-                        torch.cuda.synchronize()
-                        assert_bitexact_fp16(out, ref[:M], f"stream2 N={N} K={Kd} M={M} BLOCK_M={bm} "
-                                                           f"BLOCK_N={bn} sk={sk} ({ck.name})")
-    finally:
-        _lib.set_option("w8a8_path", 0)
+def test_w8a8_streaming_tiles_and_layouts(layout):
+    # Streaming kernels (direct and LDS-staged activations): tile depths from 16 to 304 rows,
+    # every channel width, K tails that are not whole 256-byte chunks, N tails, explicit
+    # split-K, row-major and packed weights.
+    for N, Kd in ((1000, 1552), (4096, 4096)):
+        note(f"w8a8 streaming layout={layout} N={N} K={Kd}")
+        a, w, sa, sw = gen.w8a8_inputs(300, N, Kd, seed=61 + N)
+        ref = O.w8a8(a.numpy(), sa.numpy(), w.numpy(), sw.numpy())
+        a, w, sa, sw = (t.to(DEV) for t in (a, w, sa, sw))
+        wt = K.pack_weight_int8(w) if layout == 1 else w
+        for bm in (None, 16, 32, 80, 160, 256, 304):
+            for M in (1, 17, 72, 130, 300):
+                for bn, sk in ((None, 0), (16, 0), (32, 2), (64, 1), (128, 0), (64, 3), (16, 5)):
+                    out, ck = K.w8a8_matmul(a[:M], sa[:M], wt, sw, BLOCK_M=bm, BLOCK_N=bn, split_k=sk)
+                    torch.cuda.synchronize()
+                    assert_bitexact_fp16(out, ref[:M], f"streaming N={N} K={Kd} M={M} BLOCK_M={bm} "
+                                                       f"BLOCK_N={bn} sk={sk} ({ck.name})")
 
 
 def test_w8a8_plan_mode_sentinel_rows():
