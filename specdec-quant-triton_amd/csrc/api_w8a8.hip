@@ -99,7 +99,7 @@ int bn_of_sel(int sel) { return 16 << sel; }
 // Resolve the kernel and its tiles.  `vec` is the operand alignment (16 when unknown),
 // `layout` 0 = row-major weight, 1 = packed fragments.
 int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k,
-                int vec, W8A8Cfg* cfg) {
+                int vec, bool plan_mode, W8A8Cfg* cfg) {
   SPECQ_REQUIRE(m_grid >= 0 && N > 0 && K > 0, SPECQ_EINVAL, "w8a8: bad sizes M=%d N=%d K=%d", m_grid, N, K);
   SPECQ_REQUIRE(block_n == 0 || block_n == 16 || block_n == 32 || block_n == 64 || block_n == 128, SPECQ_ENOTSUP,
                 "w8a8: BLOCK_N=%d must be 16, 32, 64 or 128", block_n);
@@ -111,8 +111,11 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
     mt = block_m / 16;
   } else {
     // One chunk of token rows covering M (the weight is then read once), split evenly when
-    // M exceeds the deepest tile.
-    const int chunks = ceil_div(rows16, kW8A8MaxMt);
+    // M exceeds the deepest tile.  With a plan the grid covers the largest M while the
+    // active M is usually much smaller: chunks of at most 80 rows then let the chunks past
+    // the active M exit at once instead of running a full-depth tile.
+    const int cap = plan_mode ? 5 : kW8A8MaxMt;
+    const int chunks = ceil_div(rows16, cap);
     mt = ceil_div(rows16, chunks);
   }
   const int path = g_w8a8_path.load();
@@ -220,7 +223,7 @@ int run_w8a8(int layout, const int8_t* a, int64_t lda, const void* w, int64_t ld
                 "w8a8: packed weights need 16-byte aligned activations and K %% 16 == 0");
   SPECQ_REQUIRE(layout == 0 || (uintptr_t)w % 16 == 0, SPECQ_EINVAL, "w8a8: misaligned packed weight");
   W8A8Cfg cfg;
-  int rc = w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, vec, &cfg);
+  int rc = w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, vec, plan != nullptr, &cfg);
   if (rc) return rc;
   const size_t need = cfg.ws_partials + cfg.ws_counters;
   SPECQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), SPECQ_ENOSPC,
@@ -242,12 +245,14 @@ int run_w8a8(int layout, const int8_t* a, int64_t lda, const void* w, int64_t ld
 size_t workspace_size(int layout, int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k) {
   W8A8Cfg cfg;
   size_t best = 0;
-  // Size for every alignment class the call could resolve to.
+  // Size for every alignment class and mode (eager or plan) the call could resolve to.
   for (int vec : {16, 1}) {
     if (layout == 1 && vec != 16) continue;
-    if (w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, vec, &cfg) == SPECQ_OK) {
-      const size_t s = cfg.ws_partials + cfg.ws_counters;
-      if (s > best) best = s;
+    for (bool plan_mode : {false, true}) {
+      if (w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, vec, plan_mode, &cfg) == SPECQ_OK) {
+        const size_t s = cfg.ws_partials + cfg.ws_counters;
+        if (s > best) best = s;
+      }
     }
   }
   clear_error();
@@ -260,7 +265,7 @@ int w8a8_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, i
                specq_kernel_attrs* out) {
   W8A8Cfg cfg;
   SPECQ_REQUIRE(layout == 0 || layout == 1, SPECQ_EINVAL, "w8a8 attrs: layout %d", layout);
-  int rc = w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, 16, &cfg);
+  int rc = w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, 16, false, &cfg);
   if (rc) return rc;
   hipFuncAttributes fa;
   if (hipFuncGetAttributes(&fa, cfg.fn) != hipSuccess) return fail(SPECQ_EIO, "w8a8: hipFuncGetAttributes failed");

@@ -24,8 +24,10 @@ reference) restate the reference formulas in torch and run on any device.
 Differences a caller may notice:
   * BLOCK_K and num_stages are accepted and ignored (the MFMA K step and register
     pipelining are fixed per kernel).  BLOCK_M=None (or 0) picks the tile from the measured
-    M staircase.  W8A8 BLOCK_M is at most 304; BLOCK_N is 16/32/64/128 channels per
-    workgroup (larger values are taken as 128); W4A16 BLOCK_N is 64 or 128.
+    M staircase; BLOCK_N defaults to None (the channel width is then picked from N; the
+    reference's default is 64).  Every tile choice gives bit-identical results.  W8A8 BLOCK_M
+    is at most 304; BLOCK_N is 16/32/64/128 channels per workgroup (larger values are taken as
+    128); W4A16 BLOCK_N is 64 or 128.
   * w8a8_matmul also accepts a PackedWeightInt8 (pack_weight_int8), the weight pre-packed
     once into MFMA fragments, with bit-identical results.
   * `ck` is a KernelInfo with n_regs / n_spills / metadata.shared like Triton's compiled
@@ -202,7 +204,7 @@ def pack_weight_int8(w_q):
     return PackedWeightInt8(w_q)
 
 
-def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=64, BLOCK_K=128,
+def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK_K=128,
                 num_warps=4, num_stages=3, plan=None, grid_m_max=None, split_k=0, workspace=None):
     """C[M, N] = fp16((int32(a_q @ w_q.T) * sa[:, None]) * sw[None, :]).  Returns (out, ck).
 
@@ -298,7 +300,7 @@ def pack_int4_i32(q_unsigned):
     return word.to(torch.int32).contiguous()
 
 
-def w4a16_matmul(a, wp, sc, group=128, out=None, BLOCK_M=16, BLOCK_N=64, BLOCK_K=64,
+def w4a16_matmul(a, wp, sc, group=128, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK_K=64,
                  num_warps=4, num_stages=3, plan=None, grid_m_max=None, split_k=0, workspace=None):
     """C[M, N] = fp16(a @ dequant(wp, sc).T) (reference kernels.py:150-166).  Returns (out, ck).
 

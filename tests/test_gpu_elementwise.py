@@ -27,10 +27,13 @@ def test_quantize_act_int8_gpu_bit_exact(shape):
     assert bool((qz == 0).all()) and np.array_equal(sz.cpu().numpy(), np.full(3, np.float32(1e-8) / np.float32(127)))
 
 
-def test_silu_mul_and_fused_quant():
-    note("silu_mul + fused quant")
-    g = torch.randn(96, 14336, generator=torch.Generator().manual_seed(1)).half() * 4
-    u = torch.randn(96, 14336, generator=torch.Generator().manual_seed(2)).half()
+@pytest.mark.parametrize("shape", [(96, 14336), (7, 1001), (3, 40000), (5, 8)])
+def test_silu_mul_and_fused_quant(shape):
+    # Register-resident vector path (rows of 8-element multiples up to 32768) and the
+    # element-wise fallback (odd widths, wider rows).
+    note(f"silu_mul + fused quant {shape}")
+    g = torch.randn(*shape, generator=torch.Generator().manual_seed(1)).half() * 4
+    u = torch.randn(*shape, generator=torch.Generator().manual_seed(2)).half()
     gd, ud = g.to(DEV), u.to(DEV)
     h = K.silu_mul(gd, ud)
     q, s = K.silu_mul_quant_int8(gd, ud)
