@@ -269,12 +269,17 @@ int w8a8_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, i
   if (rc) return rc;
   hipFuncAttributes fa;
   if (hipFuncGetAttributes(&fa, cfg.fn) != hipSuccess) return fail(SPECQ_EIO, "w8a8: hipFuncGetAttributes failed");
-  if (cfg.family == kRk)
-    snprintf(out->name, sizeof(out->name), "specq::w8a8_rk_kernel<1,BN%d,%d>", cfg.bn, cfg.layout);
-  else if (cfg.family == kWs)
-    snprintf(out->name, sizeof(out->name), "specq::w8a8_ws_kernel<%d,BN%d,%d>", cfg.mt, cfg.bn, cfg.layout);
-  else
-    snprintf(out->name, sizeof(out->name), "specq::w8a8_kernel<%d,%d,%d>", cfg.mt, cfg.rw, cfg.vec);
+  // The name carries the template arguments exactly as profilers print the kernel symbol.
+  const int kw = cfg.bn == 16 ? 4 : (cfg.bn == 32 ? 2 : 1), rw = cfg.bn == 128 ? 2 : 1, s = 4 / kw;
+  if (cfg.family == kRk) {
+    snprintf(out->name, sizeof(out->name), "specq::w8a8_rk_kernel<1, %d, %d, 4, %d>", rw, kw, cfg.layout);
+  } else if (cfg.family == kWs) {
+    const int nslot = w8a8_ws_nslot(cfg.mt, rw);
+    snprintf(out->name, sizeof(out->name), "specq::w8a8_ws_kernel<%d, %d, %d, %d, %d, 4, %d>", cfg.mt, rw, kw, s,
+             nslot, cfg.layout);
+  } else {
+    snprintf(out->name, sizeof(out->name), "specq::w8a8_kernel<%d, %d, %d>", cfg.mt, cfg.rw, cfg.vec);
+  }
   out->num_regs = fa.numRegs;
   out->lds_bytes = (int)(fa.sharedSizeBytes + cfg.lds);
   out->scratch_bytes = (int)fa.localSizeBytes;

@@ -23,10 +23,13 @@ struct W8A8BnSel {
   static constexpr int S = 4 / KW;  // K steps per wave per 256-byte chunk
 };
 
+// Ring slots of the ws kernel's activation chunks for a token depth and channel width.
+constexpr int w8a8_ws_nslot(int mt, int rw) { return (mt <= 9 && !(rw == 2 && mt >= 8)) ? 4 : 2; }
+
 template <int MT, int BNSEL>
 struct W8A8WsPick {
   using B = W8A8BnSel<BNSEL>;
-  static constexpr int NSLOT = (MT <= 9 && !(B::RW == 2 && MT >= 8)) ? 4 : 2;
+  static constexpr int NSLOT = w8a8_ws_nslot(MT, B::RW);
   using Cfg = W8A8WsCfg<MT, B::RW, B::KW, B::S, NSLOT, 4>;
 };
 
