@@ -17,7 +17,8 @@ weights (the reference's w_q layout) is reported in `detail`.
   cpu_baseline the CPU oracle (oracle/oracle.py, numpy) on one layer's seven linears at the
                same M, timed on the host cores for a bounded ~10 s sample
   detail       the k=0 decode step (M=8) on the same weights and the verify/decode ratio
-               (target <= 1.1), W4A16 at M=72 and M=8, INT8 paged verification attention at
+               (target <= 1.1), W4A16 at M=72 and M=8 (load-time packed INT4, and the int32
+               packing as given at M=72), INT8 paged verification attention at
                B=8, k=8, and the plan-buffer graph replay of the config-4 stack
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-detail]
@@ -191,23 +192,28 @@ def bench_w8a8(args, K, torch):
 
 
 def bench_w4a16(args, K, torch):
-    """W4A16 over the same seven linears, int32-packed INT4 weights, M = 72 and 8."""
+    """W4A16 over the same seven linears, M = 72 and 8: INT4 weights (int32, 8 nibbles per word)
+    packed once at load into MFMA fragments (pack_weight_int4), and the int32 weights as given
+    for the verification step."""
     g = torch.Generator(device="cuda").manual_seed(3)
-    layers = []
+    layers, raw = [], []
     for _ in range(args.layers):
-        lw = {}
+        lw, lr = {}, {}
         for name, N, Kd in LINEARS:
             wp = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, Kd // 8), dtype=torch.int32, device="cuda", generator=g)
             sc = (torch.rand((N, Kd // 128), device="cuda", generator=g) * 0.018 + 0.002).half()
-            lw[name] = (wp, sc)
+            lw[name] = (K.pack_weight_int4(wp), sc)
+            lr[name] = (wp, sc)
         layers.append(lw)
+        raw.append(lr)
     x = torch.randn((300, 4096), device="cuda", generator=g).half()
     x_ff = torch.randn((300, 14336), device="cuda", generator=g).half()
     outs = {N: torch.empty((300, N), dtype=torch.float16, device="cuda") for N in {n for _, n, _ in LINEARS}}
     res = {}
-    for label, M in (("verify", args.B * (args.k + 1)), ("decode", args.B)):
+    for label, M, ls in (("verify", args.B * (args.k + 1), layers), ("decode", args.B, layers),
+                         ("verify_int32", args.B * (args.k + 1), raw)):
         def step():
-            for lw in layers:
+            for lw in ls:
                 for name, N, Kd in LINEARS:
                     K.w4a16_matmul(x[:M] if Kd == 4096 else x_ff[:M], *lw[name], out=outs[N][:M], BLOCK_M=None)
         step()
@@ -219,7 +225,7 @@ def bench_w4a16(args, K, torch):
         flops = args.layers * sum(2 * M * N * Kd for _, N, Kd in LINEARS)
         res[label] = dict(M=M, ms=ms, GBps=b / (ms * 1e-3) / 1e9, TFLOPs=flops / (ms * 1e-3) / 1e12)
         del graph
-    del layers
+    del layers, raw
     torch.cuda.empty_cache()
     return res
 
@@ -413,6 +419,7 @@ def main() -> int:
         w4 = bench_w4a16(args, K, torch)
         detail["w4a16_verify"] = {k: round(x, 4) for k, x in w4["verify"].items()}
         detail["w4a16_decode"] = {k: round(x, 4) for k, x in w4["decode"].items()}
+        detail["w4a16_verify_int32_weights"] = {k: round(x, 4) for k, x in w4["verify_int32"].items()}
         detail["w4a16_verify_over_decode"] = round(w4["verify"]["ms"] / w4["decode"]["ms"], 4)
         detail["w4a16_verify_over_w8a8_decode"] = round(w4["verify"]["ms"] / d["ms"], 4)
         detail["attention_B8_k8"] = {k: {kk: round(x, 2) for kk, x in r.items()}

@@ -97,7 +97,9 @@ int specq_w8a8_packed(const int8_t* a, int64_t lda, const void* w_packed,
  * streaming kernel (16-row token tiles), 2 = streaming with LDS-staged activations (tiles of
  * 32 rows or more; 16-row requests use family 1), 3 = byte-granular register kernel
  * (row-major weights only).  Every family computes the same INT32 sums, so results do not
- * change. */
+ * change.  "w4a16_path": W4A16 kernel family, 0 = automatic (LDS-staged activations), 1 =
+ * register-stream kernel for token tiles of up to 32 rows, 2 = LDS-staged activations.  Both sum in the
+ * same fp32 order, so results do not change either. */
 int specq_set_option(const char* name, int value);
 
 /* ---------------------------------------------------------------------------------------
@@ -109,11 +111,18 @@ int specq_set_option(const char* name, int value);
  *            layout 0 (reference, kernels.py:89-92, 143-145): uint8 [N, K/2]; byte j of a row
  *              holds k = j in its low nibble and k = j + K/2 in its high nibble.
  *            layout 1: int32 [N, K/8]; nibble i (bits 4i..4i+3) of word j holds k = 8j + i.
+ *            layout 2: the output of specq_w4a16_pack_weight (ldq is ignored).
  *   sc       fp16 [N, K/group] group scales, row stride ld_sc
- *   group    K group size: a multiple of 32 (layout 1) or 16 (layout 0) dividing K.
+ *   group    K group size: a power of two, a multiple of 32 (layouts 1, 2) or 16 (layout 0),
+ *            dividing K.  K must be a multiple of 128.
+ *   block_m  token rows per tile, a multiple of 16 up to 256 (0 = automatic);
+ *   block_n  64 or 128 channels per workgroup (0 = automatic); num_warps is ignored (4).
  *   Other arguments as specq_w8a8.  The fp32 accumulation order depends only on (N, K),
- *   block_n, num_warps and split_k, never on M, block_m or the plan, so plan-mode and
- *   eager results are bit-identical for equal tile arguments.
+ *   split_k (0 = automatic, chosen from N and K) and whether the layout is the reference one:
+ *   split s sums its contiguous range of 128-wide K blocks in order and the splits are added
+ *   in split order; a block is k in [128b, 128b + 128) for layouts 1 and 2 and the two runs
+ *   [64b, 64b + 64) and K/2 + [64b, 64b + 64) for layout 0.  It never depends on M, block_m,
+ *   block_n or the plan, so those give bit-identical results, and so do layouts 1 and 2.
  * ------------------------------------------------------------------------------------- */
 size_t specq_w4a16_workspace_size(int m_grid, int N, int K, int block_m, int block_n,
                                   int num_warps, int split_k);
@@ -122,6 +131,17 @@ int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t ldq, int wq_
                 int M, int N, int K, int group, int grid_m_max, const int32_t* plan,
                 int block_m, int block_n, int num_warps, int split_k,
                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* W4A16 weight packed once at load time into 1 KB MFMA fragments (wq_layout 2 above): fragment
+ * (b, t) of 128-wide K block b and 16-row tile t at (b * ceil(N/16) + t) KB; lane l's 16 bytes
+ * hold row 16t + l%16 at k = 128b + 32*(l/16) + 8u + j as word u, byte i = nibble(j = i) |
+ * nibble(j = i + 4) << 4 (rows past N hold nibble 8).  The source is layout 0 or 1 (row stride
+ * ldq in elements of its storage type); `packed` holds specq_w4a16_packed_bytes() bytes, and
+ * the scales stay as they are.  Results are bit-identical to layout 1 of the same weight.  No
+ * reference counterpart: the reference reads the row-major packing on every call. */
+size_t specq_w4a16_packed_bytes(int N, int K);
+int specq_w4a16_pack_weight(const void* wq, int64_t ldq, int wq_layout, int N, int K, void* packed,
+                            void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * INT8 paged-KV verification attention.

@@ -1,73 +1,146 @@
-// C ABI for the W4A16 GEMM: argument validation, tile / split-K selection and launch.
+// C ABI for the W4A16 GEMM: argument validation, split / tile / kernel-family selection,
+// launch, and the load-time weight packing.
+//
+// Kernel families (identical fp32 summation order, so every choice is bit-identical):
+//   WS  LDS-staged activations (w4a16_ws.hpp) for any token tile up to 256 rows (default).
+//   RK  register-stream kernel (w4a16_rk.hpp) for 16- and 32-row token tiles (w4a16_path 1).
+#include <atomic>
+
 #include "api_common.hpp"
-#include "w4a16.hpp"
+#include "w4a16_tiles.hpp"
 
 namespace specq {
 
-const void* w4a16_kernel_l0(int mt, int rw);
-const void* w4a16_kernel_l1(int mt, int rw);
+// Packs a W4A16 weight (layout 0 or 1, row stride ldq bytes) into 1 KB MFMA fragments:
+// fragment (b, t) of K block b and 16-row tile t at (b * ntiles + t) KB; lane l's 16 bytes hold
+// the nibbles of row 16t + l%16 for k = 128b + 32*(l/16) + 8u + j as word u, byte i =
+// nibble(j = i) | nibble(j = i + 4) << 4.  Rows past N hold nibble 8 (weight 0).
+__global__ __launch_bounds__(256) void w4a16_pack_kernel(const uint8_t* __restrict__ wq, int64_t ldq, int layout,
+                                                         int N, int K, uint8_t* __restrict__ out) {
+  const int ntiles = (N + 15) / 16;
+  const int nblocks = K / 128;
+  const int64_t frag = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // one wave per fragment
+  if (frag >= (int64_t)ntiles * nblocks) return;
+  const int b = (int)(frag / ntiles), t = (int)(frag % ntiles);
+  const int l = threadIdx.x & 63, r = l & 15, g = l >> 4;
+  const int row = 16 * t + r;
+  const uint8_t* src = wq + (int64_t)min(row, N - 1) * ldq;
+  auto nib = [&](int k) -> uint32_t {
+    if (row >= N) return 8u;
+    if (layout == 0) {
+      const int half = K / 2;
+      return k < half ? (src[k] & 15u) : (src[k - half] >> 4);
+    }
+    return (src[k >> 1] >> (4 * (k & 1))) & 15u;  // int32 words in k order = bytes in k order
+  };
+  int words[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int k0 = 128 * b + 32 * g + 8 * u;
+    uint32_t x = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x |= (nib(k0 + i) | (nib(k0 + i + 4) << 4)) << (8 * i);
+    words[u] = (int)x;
+  }
+  *reinterpret_cast<v4i*>(out + frag * 1024 + l * 16) = v4i{words[0], words[1], words[2], words[3]};
+}
+
+// Kernel family override (0 = automatic), set through specq_set_option("w4a16_path", v).
+std::atomic<int> g_w4a16_path{0};
 
 namespace {
 
-constexpr int kW4Waves = 4;
+enum W4Family { kW4Rk = 1, kW4Ws = 2 };
 
 struct W4Cfg {
-  int mt, rw, splits, bps, n_tiles, m_chunks, nblocks;
-  size_t lds, ws_partials, ws_counters;
+  int family, layout, mt, rw, splits, bps, n_tiles, m_chunks, units, grid, nblocks;
+  size_t ws_partials, ws_counters;
   const void* fn;
 };
 
-int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, int split_k, W4Cfg* cfg) {
-  SPECQ_REQUIRE(layout == 0 || layout == 1, SPECQ_EINVAL, "w4a16: unknown weight layout %d", layout);
+// Split count: a function of (N, K) only (or the caller's split_k), so the fp32 summation
+// order never depends on M, the token tile or the plan.  Wide N already fills the CUs with
+// 64-channel tiles; narrower N is split along K into about 256 workgroups, each at least 4
+// blocks (512 K) long.
+int w4_auto_splits(int N, int nblocks) {
+  const int tiles64 = ceil_div(N, 64);
+  if (tiles64 >= 192) return 1;
+  int splits = ceil_div(256, tiles64);
+  const int cap = nblocks / 4 > 0 ? nblocks / 4 : 1;
+  return splits < cap ? splits : cap;
+}
+
+int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, int split_k, bool plan_mode,
+              W4Cfg* cfg) {
+  SPECQ_REQUIRE(layout >= 0 && layout <= 2, SPECQ_EINVAL, "w4a16: unknown weight layout %d", layout);
   SPECQ_REQUIRE(m_grid >= 0 && N > 0 && K > 0, SPECQ_EINVAL, "w4a16: bad sizes M=%d N=%d K=%d", m_grid, N, K);
   SPECQ_REQUIRE(K % 128 == 0, SPECQ_ENOTSUP, "w4a16: K=%d must be a multiple of 128", K);
   const int rows16 = ceil_div(m_grid > 0 ? m_grid : 1, 16);
   int mt;
   if (block_m > 0) {
-    SPECQ_REQUIRE(block_m % 16 == 0 && block_m <= 256, SPECQ_ENOTSUP,
-                  "w4a16: BLOCK_M=%d must be a multiple of 16 and at most 256", block_m);
+    SPECQ_REQUIRE(block_m % 16 == 0 && block_m <= 16 * kW4MaxMt, SPECQ_ENOTSUP,
+                  "w4a16: BLOCK_M=%d must be a multiple of 16 and at most %d", block_m, 16 * kW4MaxMt);
     mt = block_m / 16;
   } else {
-    // Wide N: one M-chunk up to 256 rows (one weight pass); narrow N: 48-row chunks, so more
-    // workgroups share the activation traffic (measured on the Llama-3-8B linears).
-    const int cap = ceil_div(N, 64) >= 128 ? 16 : 3;
+    // One chunk of token rows covering M (the weight is read once), split evenly past the
+    // deepest tile.  With a plan the active M is usually far below the grid's: chunks of at
+    // most 80 rows let the chunks past the active M exit at once.
+    const int cap = plan_mode ? 5 : kW4MaxMt;
     const int chunks = ceil_div(rows16, cap);
     mt = ceil_div(rows16, chunks);
   }
-  // BLOCK_N is the channel width of the whole workgroup (4 waves): 64 or 128.
   int rw = 1;
   if (block_n > 0) {
     SPECQ_REQUIRE(block_n == 64 || block_n == 128, SPECQ_ENOTSUP, "w4a16: BLOCK_N=%d must be 64 or 128", block_n);
     rw = block_n / 64;
   }
-  cfg->mt = mt; cfg->rw = rw;
-  cfg->n_tiles = ceil_div(N, kW4Waves * rw * 16);
-  cfg->m_chunks = ceil_div(m_grid > 0 ? m_grid : 1, mt * 16);
+  // The LDS-staged kernel is the default at every depth (measured faster than the register
+  // stream even for 16-row tiles on the Llama-3-8B linears); the register stream stays
+  // selectable for tiles of up to 32 rows.
+  const int path = g_w4a16_path.load();
+  const int family = (path == kW4Rk && mt <= kW4RkMaxMt) ? kW4Rk : kW4Ws;
+
+  cfg->family = family; cfg->layout = layout; cfg->mt = mt; cfg->rw = rw;
   cfg->nblocks = K / 128;
-  int splits;
-  if (split_k > 0) {
-    splits = split_k;
-  } else {
-    // A function of (N, K, BLOCK_N) only, so the fp32 summation order never depends on M:
-    // about two workgroups per CU, each split long enough (>= 8 blocks) to fill its prefetch ring.
-    const int target = 2 * device_cus();
-    splits = cfg->n_tiles >= target ? 1 : ceil_div(target, cfg->n_tiles);
-    int max_splits = cfg->nblocks / 8;
-    if (max_splits < 1) max_splits = 1;
-    if (splits > max_splits) splits = max_splits;
-  }
+  cfg->n_tiles = ceil_div(N, 64 * rw);
+  cfg->m_chunks = ceil_div(m_grid > 0 ? m_grid : 1, mt * 16);
+  int splits = split_k > 0 ? split_k : w4_auto_splits(N, cfg->nblocks);
   if (splits > cfg->nblocks) splits = cfg->nblocks;
   cfg->bps = ceil_div(cfg->nblocks, splits);
   cfg->splits = ceil_div(cfg->nblocks, cfg->bps);
-  const int BM = mt * 16, BN = kW4Waves * rw * 16;
-  cfg->lds = 0;  // static LDS (activation ring slots)
+  cfg->units = cfg->n_tiles * cfg->splits;
+  cfg->grid = w4_grid(cfg->units, cfg->m_chunks);
+  const int BM = mt * 16, BN = 64 * rw;
   cfg->ws_partials = cfg->splits > 1 ? align_up((size_t)cfg->m_chunks * cfg->n_tiles * cfg->splits * BM * BN * 4, 256) : 0;
   cfg->ws_counters = cfg->splits > 1 ? kCounterBytes : 0;
   SPECQ_REQUIRE((int64_t)cfg->m_chunks * cfg->n_tiles <= kMaxCounters, SPECQ_ENOTSUP,
                 "w4a16: %d x %d tiles exceed the counter region", cfg->m_chunks, cfg->n_tiles);
-  cfg->fn = layout == 0 ? w4a16_kernel_l0(mt, rw) : w4a16_kernel_l1(mt, rw);
-  SPECQ_REQUIRE(cfg->fn != nullptr, SPECQ_ENOTSUP, "w4a16: kernel MT=%d RW=%d not built", mt, rw);
+  if (family == kW4Rk) {
+    cfg->fn = w4a16_rk_fn(mt, rw, layout);
+  } else {
+    switch (layout) {
+      case 0: cfg->fn = w4a16_ws_fn_l0(mt, rw); break;
+      case 1: cfg->fn = w4a16_ws_fn_l1(mt, rw); break;
+      default: cfg->fn = w4a16_ws_fn_l2(mt, rw); break;
+    }
+  }
+  SPECQ_REQUIRE(cfg->fn != nullptr, SPECQ_ENOTSUP, "w4a16: no kernel for BLOCK_M=%d BLOCK_N=%d", mt * 16, 64 * rw);
   return SPECQ_OK;
+}
+
+size_t w4_workspace(int m_grid, int N, int K, int block_m, int block_n, int split_k) {
+  // The partial-tile region does not depend on the weight layout or kernel family; take the
+  // larger of the eager and plan-mode token tilings.
+  size_t need = 0;
+  for (int plan_mode = 0; plan_mode < 2; ++plan_mode) {
+    W4Cfg cfg;
+    if (w4_config(1, m_grid, N, K, block_m, block_n, split_k, plan_mode != 0, &cfg) == SPECQ_OK) {
+      const size_t n = cfg.ws_partials + cfg.ws_counters;
+      need = n > need ? n : need;
+    }
+  }
+  clear_error();
+  return need;
 }
 
 }  // namespace
@@ -76,17 +149,25 @@ int w4a16_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, 
                 specq_kernel_attrs* out) {
   (void)num_warps;
   W4Cfg cfg;
-  int rc = w4_config(layout, m_grid, N, K, block_m, block_n, split_k, &cfg);
+  int rc = w4_config(layout, m_grid, N, K, block_m, block_n, split_k, false, &cfg);
   if (rc) return rc;
   hipFuncAttributes fa;
   if (hipFuncGetAttributes(&fa, cfg.fn) != hipSuccess) return fail(SPECQ_EIO, "w4a16: hipFuncGetAttributes failed");
-  snprintf(out->name, sizeof(out->name), "specq::w4a16_kernel<%d,%d,%d>", cfg.mt, cfg.rw, layout);
+  // The name carries the template arguments exactly as profilers print the kernel symbol.
+  if (cfg.family == kW4Rk)
+    snprintf(out->name, sizeof(out->name), "specq::w4a16_rk_kernel<%d, %d, %d>", cfg.mt, cfg.rw, layout);
+  else {
+    int s = 0, nslot = 0, nsw = 0;
+    w4a16_ws_shape(cfg.mt, cfg.rw, layout, &s, &nslot, &nsw);
+    snprintf(out->name, sizeof(out->name), "specq::w4a16_ws_kernel<%d, %d, %d, %d, %d, %d>", cfg.mt, cfg.rw, s,
+             nslot, nsw, layout);
+  }
   out->num_regs = fa.numRegs;
-  out->lds_bytes = (int)(fa.sharedSizeBytes + cfg.lds);
+  out->lds_bytes = (int)fa.sharedSizeBytes;
   out->scratch_bytes = (int)fa.localSizeBytes;
-  out->threads = kW4Waves * 64;
-  out->grid = cfg.m_chunks * cfg.n_tiles * cfg.splits;
-  out->block_m = cfg.mt * 16; out->block_n = kW4Waves * cfg.rw * 16; out->num_warps = kW4Waves;
+  out->threads = 256;
+  out->grid = cfg.grid;
+  out->block_m = cfg.mt * 16; out->block_n = 64 * cfg.rw; out->num_warps = 4;
   out->split_k = cfg.splits;
   return SPECQ_OK;
 }
@@ -98,11 +179,7 @@ using namespace specq;
 extern "C" size_t specq_w4a16_workspace_size(int m_grid, int N, int K, int block_m, int block_n, int num_warps,
                                              int split_k) {
   (void)num_warps;
-  W4Cfg cfg;
-  size_t need = 0;
-  if (w4_config(1, m_grid, N, K, block_m, block_n, split_k, &cfg) == SPECQ_OK) need = cfg.ws_partials + cfg.ws_counters;
-  clear_error();
-  return need;
+  return w4_workspace(m_grid, N, K, block_m, block_n, split_k);
 }
 
 extern "C" int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t ldq, int wq_layout, const void* sc,
@@ -113,40 +190,65 @@ extern "C" int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t l
   clear_error();
   SPECQ_REQUIRE(M >= 0 && N > 0 && K > 0, SPECQ_EINVAL, "w4a16: bad sizes M=%d N=%d K=%d", M, N, K);
   SPECQ_REQUIRE(a && wq && sc && c, SPECQ_EINVAL, "w4a16: null tensor pointer");
-  SPECQ_REQUIRE(wq_layout == 0 || wq_layout == 1, SPECQ_EINVAL, "w4a16: unknown weight layout %d", wq_layout);
+  SPECQ_REQUIRE(wq_layout >= 0 && wq_layout <= 2, SPECQ_EINVAL, "w4a16: unknown weight layout %d", wq_layout);
   SPECQ_REQUIRE(group > 0 && K % group == 0, SPECQ_EINVAL, "w4a16: group=%d must divide K=%d", group, K);
-  SPECQ_REQUIRE(group % (wq_layout == 1 ? 32 : 16) == 0 && (group & (group - 1)) == 0, SPECQ_ENOTSUP,
+  SPECQ_REQUIRE(group % (wq_layout == 0 ? 16 : 32) == 0 && (group & (group - 1)) == 0, SPECQ_ENOTSUP,
                 "w4a16: group=%d must be a power of two and a multiple of %d for layout %d", group,
-                wq_layout == 1 ? 32 : 16, wq_layout);
+                wq_layout == 0 ? 16 : 32, wq_layout);
   const int64_t row_bytes = wq_layout == 1 ? ldq * 4 : ldq;
-  SPECQ_REQUIRE(lda >= K && row_bytes >= K / 2 && ld_sc >= K / group && ldc >= N, SPECQ_EINVAL,
+  SPECQ_REQUIRE((wq_layout == 2 || row_bytes >= K / 2) && lda >= K && ld_sc >= K / group && ldc >= N, SPECQ_EINVAL,
                 "w4a16: row strides must cover a row");
   SPECQ_REQUIRE(grid_m_max == 0 || grid_m_max >= M, SPECQ_EINVAL, "w4a16: grid_m_max=%d < M=%d", grid_m_max, M);
   SPECQ_REQUIRE((uintptr_t)a % 16 == 0 && lda % 8 == 0, SPECQ_ENOTSUP,
                 "w4a16: activations need 16-byte aligned rows (lda %% 8 == 0)");
-  SPECQ_REQUIRE((uintptr_t)wq % 16 == 0 && row_bytes % 16 == 0, SPECQ_ENOTSUP,
+  SPECQ_REQUIRE((uintptr_t)wq % 16 == 0 && (wq_layout == 2 || row_bytes % 16 == 0), SPECQ_ENOTSUP,
                 "w4a16: packed weights need 16-byte aligned rows");
   SPECQ_REQUIRE((uintptr_t)sc % 2 == 0, SPECQ_EINVAL, "w4a16: misaligned scales");
   const int m_grid = grid_m_max > 0 ? grid_m_max : M;
   if (m_grid == 0) return SPECQ_OK;
   W4Cfg cfg;
-  int rc = w4_config(wq_layout, m_grid, N, K, block_m, block_n, split_k, &cfg);
+  int rc = w4_config(wq_layout, m_grid, N, K, block_m, block_n, split_k, plan != nullptr, &cfg);
   if (rc) return rc;
   const size_t need = cfg.ws_partials + cfg.ws_counters;
   SPECQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), SPECQ_ENOSPC,
                 "w4a16: workspace of %zu bytes required, %zu given", need, workspace ? workspace_bytes : 0);
-  rc = ensure_lds(cfg.fn, cfg.lds);
-  if (rc) return rc;
   W4A16Params p;
   p.A = (const _Float16*)a; p.lda = lda; p.Wq = (const uint8_t*)wq; p.ldq = row_bytes;
   p.sc = (const _Float16*)sc; p.ld_sc = ld_sc; p.C = (_Float16*)c; p.ldc = ldc; p.plan = plan;
-  p.M = M; p.N = N; p.K = K; p.group = group; p.m_grid = m_grid;
+  p.M = M; p.N = N; p.K = K; p.m_grid = m_grid;
   p.group_shift = __builtin_ctz((unsigned)group);
-  p.n_tiles = cfg.n_tiles; p.m_chunks = cfg.m_chunks; p.splits = cfg.splits; p.nblocks = cfg.nblocks;
-  p.blocks_per_split = cfg.bps;
+  p.n_tiles = cfg.n_tiles; p.m_chunks = cfg.m_chunks; p.splits = cfg.splits; p.units = cfg.units;
+  p.nblocks = cfg.nblocks; p.bps = cfg.bps; p.ntiles16 = ceil_div(N, 16);
   p.counters = need ? (int32_t*)workspace : nullptr;
   p.partials = need ? (float*)((char*)workspace + kCounterBytes) : nullptr;
   p.vec_store = ((uintptr_t)c % 8 == 0) && (ldc % 4 == 0);
-  const int grid = cfg.m_chunks * cfg.n_tiles * cfg.splits;
-  return launch(cfg.fn, grid, kW4Waves * 64, cfg.lds, (hipStream_t)stream, &p);
+  return launch(cfg.fn, cfg.grid, 256, 0, (hipStream_t)stream, &p);
+}
+
+extern "C" size_t specq_w4a16_packed_bytes(int N, int K) {
+  if (N <= 0 || K <= 0 || K % 128 != 0) return 0;
+  return (size_t)ceil_div(N, 16) * (K / 128) * 1024;
+}
+
+extern "C" int specq_w4a16_pack_weight(const void* wq, int64_t ldq, int wq_layout, int N, int K, void* packed,
+                                       void* stream) {
+  clear_error();
+  SPECQ_REQUIRE(wq && packed, SPECQ_EINVAL, "w4a16_pack_weight: null tensor pointer");
+  SPECQ_REQUIRE(wq_layout == 0 || wq_layout == 1, SPECQ_EINVAL, "w4a16_pack_weight: layout %d is not 0 or 1",
+                wq_layout);
+  SPECQ_REQUIRE(N > 0 && K > 0 && K % 128 == 0, SPECQ_ENOTSUP, "w4a16_pack_weight: K=%d must be a multiple of 128", K);
+  const int64_t row_bytes = wq_layout == 1 ? ldq * 4 : ldq;
+  SPECQ_REQUIRE(row_bytes >= K / 2, SPECQ_EINVAL, "w4a16_pack_weight: row stride %lld too small", (long long)ldq);
+  SPECQ_REQUIRE((uintptr_t)packed % 16 == 0, SPECQ_EINVAL, "w4a16_pack_weight: misaligned output");
+  const int64_t frags = (int64_t)ceil_div(N, 16) * (K / 128);
+  SPECQ_REQUIRE(ceil_div64(frags, 4) <= INT32_MAX, SPECQ_ENOTSUP, "w4a16_pack_weight: weight too large");
+  const uint8_t* w = (const uint8_t*)wq;
+  void* args[] = {(void*)&w, (void*)&row_bytes, (void*)&wq_layout, (void*)&N, (void*)&K, (void*)&packed};
+  hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&w4a16_pack_kernel),
+                                 dim3((unsigned)ceil_div64(frags, 4)), dim3(256), args, 0, (hipStream_t)stream);
+  if (e != hipSuccess) {
+    set_error("w4a16_pack_weight: hipLaunchKernel failed: %s", hipGetErrorString(e));
+    return SPECQ_EIO;
+  }
+  return SPECQ_OK;
 }

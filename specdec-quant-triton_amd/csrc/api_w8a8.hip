@@ -49,6 +49,7 @@ __global__ __launch_bounds__(256) void w8a8_pack_kernel(const int8_t* __restrict
 
 // Kernel family override (0 = automatic), set through specq_set_option("w8a8_path", v).
 std::atomic<int> g_w8a8_path{0};
+extern std::atomic<int> g_w4a16_path;  // api_w4a16.hip
 
 namespace {
 
@@ -350,6 +351,11 @@ extern "C" int specq_set_option(const char* name, int value) {
   if (strcmp(name, "w8a8_path") == 0) {
     SPECQ_REQUIRE(value >= 0 && value <= 3, SPECQ_EINVAL, "set_option: w8a8_path must be 0..3");
     g_w8a8_path.store(value);
+    return SPECQ_OK;
+  }
+  if (strcmp(name, "w4a16_path") == 0) {
+    SPECQ_REQUIRE(value >= 0 && value <= 2, SPECQ_EINVAL, "set_option: w4a16_path must be 0..2");
+    g_w4a16_path.store(value);
     return SPECQ_OK;
   }
   set_error("set_option: unknown option '%s'", name);

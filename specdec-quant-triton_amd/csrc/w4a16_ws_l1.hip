@@ -1,0 +1,45 @@
+// Instantiations of the LDS-staged-activation W4A16 kernel for the int32 layout (8 nibbles per word):
+// token tiles of 1 .. 16 x 16 rows, BLOCK_N = 64 (RW 1) and 128 (RW 2).
+#include "w4a16_tiles.hpp"
+
+namespace specq {
+
+const void* w4a16_ws_fn_l1(int mt, int rw) {
+  switch (mt * 4 + rw) {
+    case 5: return w4a16_ws_pick<1, 1, 1>();
+    case 6: return w4a16_ws_pick<1, 2, 1>();
+    case 9: return w4a16_ws_pick<2, 1, 1>();
+    case 10: return w4a16_ws_pick<2, 2, 1>();
+    case 13: return w4a16_ws_pick<3, 1, 1>();
+    case 14: return w4a16_ws_pick<3, 2, 1>();
+    case 17: return w4a16_ws_pick<4, 1, 1>();
+    case 18: return w4a16_ws_pick<4, 2, 1>();
+    case 21: return w4a16_ws_pick<5, 1, 1>();
+    case 22: return w4a16_ws_pick<5, 2, 1>();
+    case 25: return w4a16_ws_pick<6, 1, 1>();
+    case 26: return w4a16_ws_pick<6, 2, 1>();
+    case 29: return w4a16_ws_pick<7, 1, 1>();
+    case 30: return w4a16_ws_pick<7, 2, 1>();
+    case 33: return w4a16_ws_pick<8, 1, 1>();
+    case 34: return w4a16_ws_pick<8, 2, 1>();
+    case 37: return w4a16_ws_pick<9, 1, 1>();
+    case 38: return w4a16_ws_pick<9, 2, 1>();
+    case 41: return w4a16_ws_pick<10, 1, 1>();
+    case 42: return w4a16_ws_pick<10, 2, 1>();
+    case 45: return w4a16_ws_pick<11, 1, 1>();
+    case 46: return w4a16_ws_pick<11, 2, 1>();
+    case 49: return w4a16_ws_pick<12, 1, 1>();
+    case 50: return w4a16_ws_pick<12, 2, 1>();
+    case 53: return w4a16_ws_pick<13, 1, 1>();
+    case 54: return w4a16_ws_pick<13, 2, 1>();
+    case 57: return w4a16_ws_pick<14, 1, 1>();
+    case 58: return w4a16_ws_pick<14, 2, 1>();
+    case 61: return w4a16_ws_pick<15, 1, 1>();
+    case 62: return w4a16_ws_pick<15, 2, 1>();
+    case 65: return w4a16_ws_pick<16, 1, 1>();
+    case 66: return w4a16_ws_pick<16, 2, 1>();
+    default: return nullptr;
+  }
+}
+
+}  // namespace specq

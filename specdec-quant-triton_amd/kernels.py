@@ -32,7 +32,12 @@ Differences a caller may notice:
     once into MFMA fragments, with bit-identical results.
   * `ck` is a KernelInfo with n_regs / n_spills / metadata.shared like Triton's compiled
     kernel, plus the resolved tile configuration.
-  * w4a16_matmul also accepts the int32 "8 nibbles per word along K" packing.
+  * w4a16_matmul also accepts the int32 "8 nibbles per word along K" packing and a
+    PackedWeightInt4 (pack_weight_int4), bit-identical to the int32 packing; its fp32
+    summation order depends only on (N, K), split_k and whether the weight is the reference
+    uint8 packing (whose bytes pair k with k + K/2), so every W4A16 tile choice is
+    bit-identical too.
+    W4A16 BLOCK_M is at most 256.
 """
 from __future__ import annotations
 
@@ -55,7 +60,7 @@ __all__ = [
     "quantize_act_int8", "quantize_weight_int8", "quantize_weight_int4",
     "make_paged_kv", "paged_attention_ref",
     "silu_mul", "quantize_act_int8_gpu", "silu_mul_quant_int8",
-    "pack_int4_i32", "KernelInfo", "PackedWeightInt8", "pack_weight_int8",
+    "pack_int4_i32", "KernelInfo", "PackedWeightInt8", "pack_weight_int8", "PackedWeightInt4", "pack_weight_int4",
 ]
 
 
@@ -76,12 +81,18 @@ class KernelInfo:
 
     def __init__(self, kind: int, variant: int, m_grid: int, N: int, K: int, block_m: int, block_n: int,
                  num_warps: int, split_k: int):
+        # The kernel also depends on the library options (kernel-family overrides), so the
+        # cache key carries them and a first-time query happens now, under the options the
+        # call ran with.
         self._key = (kind, variant, m_grid, N, K, block_m, block_n, num_warps, split_k)
-        self._attrs = None
+        try:
+            self._attrs, self._err = _attrs_cached(self._key, _lib.options_key()), None
+        except RuntimeError as e:  # reported when the attributes are read
+            self._attrs, self._err = None, e
 
     def _get(self):
-        if self._attrs is None:
-            self._attrs = _attrs_cached(*self._key)
+        if self._err is not None:
+            raise self._err
         return self._attrs
 
     @property
@@ -113,10 +124,10 @@ class KernelInfo:
 _ATTRS: dict = {}
 
 
-def _attrs_cached(*key):
-    a = _ATTRS.get(key)
+def _attrs_cached(key, options):
+    a = _ATTRS.get((key, options))
     if a is None:
-        a = _ATTRS[key] = _lib.kernel_attrs(*key)
+        a = _ATTRS[(key, options)] = _lib.kernel_attrs(*key)
     return a
 
 
@@ -300,18 +311,57 @@ def pack_int4_i32(q_unsigned):
     return word.to(torch.int32).contiguous()
 
 
+class PackedWeightInt4:
+    """A W4A16 weight (uint8 [N, K/2] reference packing or int32 [N, K/8]) re-packed once into
+    MFMA fragments for w4a16_matmul.
+
+    Fragment (128-wide K block b, 16-row tile t) is the 1 KB at (b * ceil(N/16) + t) KB; lane
+    l's 16 bytes hold row 16t + l%16 at k = 128b + 32*(l/16) + 8u + j as word u, byte
+    i = nibble(j = i) | nibble(j = i + 4) << 4.  Every weight load is then 1 KB contiguous.  The
+    group scales are not repacked.  Results are bit-identical to passing the int32 packing of
+    the same weight (the reference uint8 packing sums K in another order, so it agrees to
+    fp32 rounding).
+    """
+
+    def __init__(self, wp: torch.Tensor):
+        _require_gpu(wp)
+        if wp.dim() != 2 or wp.dtype not in (torch.uint8, torch.int32):
+            raise RuntimeError("PackedWeightInt4 expects uint8 [N, K/2] or int32 [N, K/8] packed weights")
+        wp = _rowmajor(wp)
+        layout = 0 if wp.dtype == torch.uint8 else 1
+        self.N = wp.shape[0]
+        self.K = wp.shape[1] * (2 if layout == 0 else 8)
+        self.shape = (self.N, self.K)
+        self.device = wp.device
+        nbytes = _lib.lib().specq_w4a16_packed_bytes(self.N, self.K)
+        if nbytes == 0:
+            raise RuntimeError(f"PackedWeightInt4: K={self.K} must be a multiple of 128")
+        self.data = torch.empty(nbytes, dtype=torch.uint8, device=wp.device)
+        _lib.call("specq_w4a16_pack_weight", wp.data_ptr(), wp.stride(0), layout, self.N, self.K,
+                  self.data.data_ptr(), _stream_ptr(wp))
+
+
+def pack_weight_int4(wp):
+    """Pack a W4A16 weight for w4a16_matmul (see PackedWeightInt4)."""
+    return PackedWeightInt4(wp)
+
+
 def w4a16_matmul(a, wp, sc, group=128, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK_K=64,
                  num_warps=4, num_stages=3, plan=None, grid_m_max=None, split_k=0, workspace=None):
     """C[M, N] = fp16(a @ dequant(wp, sc).T) (reference kernels.py:150-166).  Returns (out, ck).
 
-    a fp16 [M, K].  wp is uint8 [N, K/2] (reference packing) or int32 [N, K/8] (8 nibbles per
-    word along K).  sc fp16 [N, K/group].
+    a fp16 [M, K].  wp is uint8 [N, K/2] (reference packing), int32 [N, K/8] (8 nibbles per
+    word along K) or a PackedWeightInt4.  sc fp16 [N, K/group].
     """
-    _require_gpu(a, wp, sc)
+    _require_gpu(a, sc)
     assert BLOCK_K <= group and group % BLOCK_K == 0
     M, K = a.shape
     N = wp.shape[0]
-    if wp.dtype == torch.uint8:
+    if isinstance(wp, PackedWeightInt4):
+        layout = 2
+        if wp.K != K:
+            raise RuntimeError(f"w4a16_matmul: packed weight K={wp.K} does not match K={K}")
+    elif wp.dtype == torch.uint8:
         layout = 0
         if wp.shape[1] * 2 != K:
             raise RuntimeError(f"w4a16_matmul: packed uint8 weights {tuple(wp.shape)} do not match K={K}")
@@ -320,10 +370,16 @@ def w4a16_matmul(a, wp, sc, group=128, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK
         if wp.shape[1] * 8 != K:
             raise RuntimeError(f"w4a16_matmul: packed int32 weights {tuple(wp.shape)} do not match K={K}")
     else:
-        raise RuntimeError("w4a16_matmul: wp must be uint8 [N, K/2] or int32 [N, K/8]")
+        raise RuntimeError("w4a16_matmul: wp must be uint8 [N, K/2], int32 [N, K/8] or a PackedWeightInt4")
     if a.dtype != torch.float16 or sc.dtype != torch.float16:
         raise RuntimeError("w4a16_matmul expects fp16 activations and fp16 scales")
-    a, wp, sc = _rowmajor(a), _rowmajor(wp), _rowmajor(sc)
+    a, sc = _rowmajor(a), _rowmajor(sc)
+    if layout == 2:
+        w_ptr, w_ld = wp.data.data_ptr(), 0
+    else:
+        _require_gpu(wp)
+        wp = _rowmajor(wp)
+        w_ptr, w_ld = wp.data_ptr(), wp.stride(0)
     if a.data_ptr() % 16 or a.stride(0) % 8:
         a = a.contiguous() if a.data_ptr() % 16 == 0 else a.clone()
     if out is None:
@@ -336,7 +392,7 @@ def w4a16_matmul(a, wp, sc, group=128, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK
     ws = workspace or _ws.shared(a.device)
     need = _lib.lib().specq_w4a16_workspace_size(m_grid, N, K, bm, bn, 4, split_k)
     wptr, wbytes = ws.ensure(need)
-    _lib.call("specq_w4a16", a.data_ptr(), a.stride(0), wp.data_ptr(), wp.stride(0), layout,
+    _lib.call("specq_w4a16", a.data_ptr(), a.stride(0), w_ptr, w_ld, layout,
               sc.data_ptr(), sc.stride(0), out.data_ptr(), out.stride(0),
               M, N, K, int(group), int(grid_m_max or 0), _plan_ptr(plan), bm, bn, 4, split_k,
               wptr, wbytes, _stream_ptr(a))

@@ -46,6 +46,8 @@ SIGNATURES = {
                                    _c_int, _c_int, _c_int, _c_int, _c_vp, _c_size, _c_vp]),
     "specq_set_option": (_c_int, [ctypes.c_char_p, _c_int]),
     "specq_w4a16_workspace_size": (_c_size, [_c_int] * 7),
+    "specq_w4a16_packed_bytes": (_c_size, [_c_int, _c_int]),
+    "specq_w4a16_pack_weight": (_c_int, [_c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp, _c_vp]),
     "specq_w4a16": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_vp, _c_i64, _c_vp, _c_i64,
                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp,
                              _c_int, _c_int, _c_int, _c_int, _c_vp, _c_size, _c_vp]),
@@ -101,8 +103,17 @@ def call(name: str, *args) -> int:
     return rc
 
 
+_OPTIONS: dict = {}
+
+
 def set_option(name: str, value: int) -> None:
     call("specq_set_option", name.encode(), int(value))
+    _OPTIONS[name] = int(value)
+
+
+def options_key() -> tuple:
+    """The library options set through set_option (they can change which kernel a call runs)."""
+    return tuple(sorted(_OPTIONS.items()))
 
 
 def kernel_attrs(kind: int, variant: int, m_grid: int, N: int, K: int, block_m: int, block_n: int,

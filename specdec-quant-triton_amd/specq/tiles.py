@@ -4,9 +4,10 @@ The reference sweeps tile configs per M and reports that BLOCK_M should follow M
 BLOCK_M of 0 hands the choice to the library, whose rule follows from measured sweeps on
 MI355X: W8A8 takes one chunk of token rows covering M (up to 304 rows), so every weight byte
 is read from HBM once, with the direct-activation streaming kernel for 16-row chunks and the
-LDS-staged-activation kernel above; W4A16 takes one chunk of up to 256 rows for wide N and
-48-row chunks for narrow N.  STAIRCASE overrides it per (kind, N, K) with the best measured
-BLOCK_M for each M bucket.
+LDS-staged-activation kernel above; W4A16 likewise takes one chunk of up to 256 rows (the
+register-stream kernel for 16 rows, LDS-staged activations above).  With a plan both cap the
+chunk at 80 rows so chunks past the active M exit early.  STAIRCASE overrides it per
+(kind, N, K) with the best measured BLOCK_M for each M bucket.
 """
 from __future__ import annotations
 

@@ -121,3 +121,94 @@ def test_w4a16_plan_mode_bit_identical_to_eager():
     e128, _ = K.w4a16_matmul(a[:100], wi, sc, BLOCK_M=128)
     torch.cuda.synchronize()
     assert torch.equal(e16, e128)
+
+
+def _pack(wp):
+    out = K.pack_weight_int4(wp)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("shape", [(1000, 1024), (4096, 4096), (1024, 4096), (4096, 14336), (17, 256), (1, 128)])
+def test_w4a16_layouts_families_tiles_bit_identical(shape):
+    """Every kernel family (w4a16_path 1: register stream, 2: LDS-staged), BLOCK_M and
+    BLOCK_N gives the same bits, and so do the layouts that walk K in the same order (int32
+    and packed, whichever layout it was packed from); the reference uint8 layout pairs k with
+    k + K/2 in each byte, so its blocks cover other k and it has its own order.  Every result
+    meets the tolerance against the oracle."""
+    from specq import _lib
+    N, Kd = shape
+    note(f"w4a16 layouts/families/tiles N={N} K={Kd}")
+    qu, sc = gen.int4_weights(N, Kd, 128, seed=40 + N)
+    a = gen.fp16_acts(300, Kd, seed=41 + Kd)
+    ref = O.w4a16(a.numpy(), qu.numpy(), sc.numpy(), 128)
+    wu, wi = gen.pack_u8_reference(qu).to(DEV), gen.pack_i32(qu).to(DEV)
+    a, sc = a.to(DEV), sc.to(DEV)
+    weights = {"u8": ("u8", wu), "i32": ("k", wi), "packed(u8)": ("k", _pack(wu)), "packed(i32)": ("k", _pack(wi))}
+    try:
+        for M in (1, 5, 16, 17, 32, 72, 100, 300):
+            base = {}
+            for path in (0, 1, 2):
+                _lib.set_option("w4a16_path", path)
+                for wname, (order, wp) in weights.items():
+                    for bm in (None, 16, 32, 80, 256):
+                        for bn in (None, 128):
+                            out, ck = K.w4a16_matmul(a[:M], wp, sc, BLOCK_M=bm, BLOCK_N=bn)
+                            torch.cuda.synchronize()
+                            what = f"M={M} path={path} {wname} BLOCK_M={bm} BLOCK_N={bn} ({ck.name})"
+                            if order not in base:
+                                base[order] = out
+                                check_tol(out, ref[:M], what)
+                            else:
+                                assert torch.equal(out, base[order]), what
+    finally:
+        _lib.set_option("w4a16_path", 0)
+
+
+@pytest.mark.parametrize("split_k", [1, 2, 3, 5, 8])
+def test_w4a16_explicit_split_k(split_k):
+    N, Kd = 1024, 4096
+    note(f"w4a16 split_k={split_k}")
+    qu, sc = gen.int4_weights(N, Kd, 128, seed=55)
+    a = gen.fp16_acts(80, Kd, seed=56)
+    ref = O.w4a16(a.numpy(), qu.numpy(), sc.numpy(), 128)
+    wi, a, sc = gen.pack_i32(qu).to(DEV), a.to(DEV), sc.to(DEV)
+    for M in (1, 8, 80):
+        outs = [K.w4a16_matmul(a[:M], wi, sc, BLOCK_M=bm, split_k=split_k)[0] for bm in (16, 80)]
+        torch.cuda.synchronize()
+        check_tol(outs[0], ref[:M], f"split_k={split_k} M={M}")
+        assert torch.equal(outs[0], outs[1])
+
+
+def test_w4a16_packed_plan_mode_graph_replays():
+    """Plan-mode W4A16 on the packed layout inside a captured graph: every replay matches the
+    eager call bit for bit and rows >= M stay untouched."""
+    note("w4a16 packed plan graph")
+    N, Kd, MMAX = 4096, 4096, 288
+    qu, sc = gen.int4_weights(N, Kd, 128, seed=61)
+    wpk = _pack(gen.pack_i32(qu).to(DEV))
+    sc = sc.to(DEV)
+    a = gen.fp16_acts(MMAX, Kd, seed=62).to(DEV)
+    plan = torch.zeros(8, dtype=torch.int32, device=DEV)
+    out = torch.full((MMAX, N), 7.0, dtype=torch.float16, device=DEV)
+    plan[0] = MMAX
+    K.w4a16_matmul(a, wpk, sc, out=out, plan=plan, grid_m_max=MMAX, BLOCK_M=None)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g):
+            K.w4a16_matmul(a, wpk, sc, out=out, plan=plan, grid_m_max=MMAX, BLOCK_M=None)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for M in (72, 1, 288, 9, 150, 72):
+        out.fill_(7.0)
+        plan[0] = M
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        eager, _ = K.w4a16_matmul(a[:M], wpk, sc, BLOCK_M=None)
+        torch.cuda.synchronize()
+        assert torch.equal(out[:M], eager), f"replay M={M}"
+        assert bool((out[M:] == 7.0).all()), f"replay M={M} wrote rows >= M"

@@ -108,7 +108,8 @@ def test_workspace_sizes(built_lib):
 def test_kernel_attrs_resources_file(built_lib):
     res = os.path.join(os.path.dirname(built_lib), "libspecq.resources.txt")
     txt = open(res).read()
-    assert "w8a8_kernel" in txt and "w4a16_kernel" in txt and "paged_attn_kernel" in txt
+    for name in ("w8a8_ws_kernel", "w8a8_rk_kernel", "w4a16_ws_kernel", "w4a16_rk_kernel", "paged_attn_kernel"):
+        assert name in txt, name
 
 
 # ---------------------------------------------------------------- host helpers vs oracle
