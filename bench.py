@@ -253,8 +253,9 @@ def bench_attention(args, K, torch):
 
 
 def bench_plan_graph(args, K, torch):
-    """Config 4: one plan-buffer graph of a 4-layer INT8 stack (d_model 4096) captured at B=32,
-    k=8 (M=288), replayed over a seeded (B, k) trace; eager per-step time for comparison."""
+    """Config 4: one plan-buffer graph of a 4-layer INT8 stack (d_model 4096, weights packed at
+    load) captured at B=32, k=8 (M=288), replayed over a seeded (B, k) trace; eager per-step
+    time for comparison."""
     import random
 
     from specq import gen
@@ -267,8 +268,8 @@ def bench_plan_graph(args, K, torch):
     M_MAX = B_MAX * QL_MAX
     gg = torch.Generator(device="cuda").manual_seed(9)
 
-    def w(N, Kd):
-        return (torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=gg),
+    def w(N, Kd):  # packed at load, as in the headline step
+        return (K.pack_weight_int8(torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=gg)),
                 torch.rand((N,), device="cuda", generator=gg) * 0.009 + 0.001)
     layers = []
     for i in range(L):

@@ -197,7 +197,8 @@ int specq_silu_mul_quant_int8(const void* gate, int64_t ld_gate, const void* up,
  * Resource usage of the kernel a call with these arguments would launch (the reference's
  * compiled-kernel metadata ck.n_regs / ck.n_spills / ck.metadata.shared, regs.py:29-32).
  * kind: 0 = W8A8 (weight layout in `variant`: 0 row-major, 1 packed), 1 = W4A16 (layout in
- * `variant`), 2 = paged attention (D in `variant`).
+ * `variant`), 2 = paged attention (D in `variant`).  For the GEMMs, `variant` | 16 describes a
+ * call made with a plan (m_grid is then grid_m_max).
  * ------------------------------------------------------------------------------------- */
 typedef struct specq_kernel_attrs {
   char name[160];          /* kernel symbol */

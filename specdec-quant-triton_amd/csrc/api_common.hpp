@@ -26,6 +26,9 @@ inline int fail(int code, const char* what) {
     }                                  \
   } while (0)
 
+// Flag in the `variant` of a GEMM resource query: the call ran with a plan (tile rules differ).
+constexpr int kAttrsPlan = 16;
+
 // Every workspace starts with a fixed counter region (zero between calls), then scratch.
 constexpr size_t kCounterBytes = 256 * 1024;
 constexpr int64_t kMaxCounters = kCounterBytes / 4;

@@ -109,7 +109,7 @@ int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, in
   cfg->bps = ceil_div(cfg->nblocks, splits);
   cfg->splits = ceil_div(cfg->nblocks, cfg->bps);
   cfg->units = cfg->n_tiles * cfg->splits;
-  cfg->grid = w4_grid(cfg->units, cfg->m_chunks);
+  cfg->grid = chunked_grid(cfg->units, cfg->m_chunks);
   const int BM = mt * 16, BN = 64 * rw;
   cfg->ws_partials = cfg->splits > 1 ? align_up((size_t)cfg->m_chunks * cfg->n_tiles * cfg->splits * BM * BN * 4, 256) : 0;
   cfg->ws_counters = cfg->splits > 1 ? kCounterBytes : 0;
@@ -149,7 +149,9 @@ int w4a16_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, 
                 specq_kernel_attrs* out) {
   (void)num_warps;
   W4Cfg cfg;
-  int rc = w4_config(layout, m_grid, N, K, block_m, block_n, split_k, false, &cfg);
+  const bool plan_mode = (layout & kAttrsPlan) != 0;
+  layout &= ~kAttrsPlan;
+  int rc = w4_config(layout, m_grid, N, K, block_m, block_n, split_k, plan_mode, &cfg);
   if (rc) return rc;
   hipFuncAttributes fa;
   if (hipFuncGetAttributes(&fa, cfg.fn) != hipSuccess) return fail(SPECQ_EIO, "w4a16: hipFuncGetAttributes failed");

@@ -239,7 +239,7 @@ int run_w8a8(int layout, const int8_t* a, int64_t lda, const void* w, int64_t ld
   p.counters = need ? reinterpret_cast<int32_t*>(workspace) : nullptr;
   p.partials = need ? reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + kCounterBytes) : nullptr;
   p.vec_store = ((uintptr_t)c % 8 == 0) && (ldc % 4 == 0) && ((uintptr_t)sw % 16 == 0);
-  const int grid = cfg.m_chunks * cfg.n_tiles * cfg.splits;
+  const int grid = chunked_grid(cfg.n_tiles * cfg.splits, cfg.m_chunks);
   return launch(cfg.fn, grid, cfg.nw * 64, cfg.lds, reinterpret_cast<hipStream_t>(stream), &p);
 }
 
@@ -265,8 +265,10 @@ size_t workspace_size(int layout, int m_grid, int N, int K, int block_m, int blo
 int w8a8_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k,
                specq_kernel_attrs* out) {
   W8A8Cfg cfg;
+  const bool plan_mode = (layout & kAttrsPlan) != 0;
+  layout &= ~kAttrsPlan;
   SPECQ_REQUIRE(layout == 0 || layout == 1, SPECQ_EINVAL, "w8a8 attrs: layout %d", layout);
-  int rc = w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, 16, false, &cfg);
+  int rc = w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, 16, plan_mode, &cfg);
   if (rc) return rc;
   hipFuncAttributes fa;
   if (hipFuncGetAttributes(&fa, cfg.fn) != hipSuccess) return fail(SPECQ_EIO, "w8a8: hipFuncGetAttributes failed");
@@ -285,7 +287,7 @@ int w8a8_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, i
   out->lds_bytes = (int)(fa.sharedSizeBytes + cfg.lds);
   out->scratch_bytes = (int)fa.localSizeBytes;
   out->threads = cfg.nw * 64;
-  out->grid = cfg.m_chunks * cfg.n_tiles * cfg.splits;
+  out->grid = chunked_grid(cfg.n_tiles * cfg.splits, cfg.m_chunks);
   out->block_m = cfg.mt * 16; out->block_n = cfg.bn; out->num_warps = cfg.nw; out->split_k = cfg.splits;
   return SPECQ_OK;
 }

@@ -221,6 +221,18 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// Workgroup id -> (M-chunk mc, work unit): chunk-major, id = mc * units + unit.  In plan mode
+// the grid covers the largest M while the active M usually fills only the first chunks; the
+// workgroups of those chunks then come first in dispatch order, and the trailing ones (which
+// only read the plan and exit) do not hold up the dispatch of active ones behind them.
+__device__ __forceinline__ bool chunked_unit(int m_chunks, int units, int& mc, int& unit) {
+  const int id = blockIdx.x;
+  mc = id / units;
+  unit = id - mc * units;
+  return mc < m_chunks;
+}
+__host__ __device__ inline int chunked_grid(int units, int m_chunks) { return units * m_chunks; }
+
 __device__ __forceinline__ void wait_all_memory() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);

@@ -168,26 +168,13 @@ __device__ __forceinline__ void w4_store4(const W4A16Params& p, int m, int n, v4
   }
 }
 
-// Workgroup -> (M-chunk, channel tile, split).  With several M-chunks, the chunks of one
-// (tile, split) unit get block ids 8 apart, i.e. the same XCD (ids are dealt round-robin over
-// the 8 XCDs), at about the same time: the chunks after the first find the weight in that
-// XCD's L2.  Returns false for padding workgroups.
+// Workgroup -> (M-chunk, channel tile, split); false for padding workgroups (chunked_unit).
 __device__ __forceinline__ bool w4_decode_id(const W4A16Params& p, int& mc, int& tile, int& split) {
-  int id = blockIdx.x, unit;
-  if (p.m_chunks == 1) {
-    mc = 0; unit = id;
-  } else {
-    const int lo = id & 7, hi = id >> 3;
-    mc = hi % p.m_chunks;
-    unit = (hi / p.m_chunks) * 8 + lo;
-  }
-  if (unit >= p.units) return false;
+  int unit;
+  if (!chunked_unit(p.m_chunks, p.units, mc, unit)) return false;
   split = unit % p.splits;
   tile = unit / p.splits;
   return true;
-}
-__host__ __device__ inline int w4_grid(int units, int m_chunks) {
-  return m_chunks == 1 ? units : ((units + 7) / 8) * 8 * m_chunks;
 }
 
 // Split-K hand-off of a workgroup's fp32 tile [BM][BN] (row = token), 16 bytes per lane.

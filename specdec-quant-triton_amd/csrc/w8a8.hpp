@@ -119,10 +119,10 @@ __global__ __launch_bounds__(256) void w8a8_kernel(W8A8Params p) {
   extern __shared__ int32_t smem[];
 
   const int nw = blockDim.x / kWave;
-  int id = blockIdx.x;
-  const int mc = id % p.m_chunks; id /= p.m_chunks;
-  const int split = id % p.splits;
-  const int tile = id / p.splits;
+  int mc, unit;
+  if (!chunked_unit(p.m_chunks, p.n_tiles * p.splits, mc, unit)) return;
+  const int split = unit % p.splits;
+  const int tile = unit / p.splits;
 
   int M = p.M;
   if (p.plan != nullptr) M = min(max(p.plan[0], 0), p.m_grid);

@@ -53,10 +53,10 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
   constexpr int CW = C::CW, BM = C::BM, BNW = C::BNW, BN = C::BN, NS = C::NS, D = C::D, PER = C::PER;
   extern __shared__ __attribute__((aligned(16))) int32_t smem_rk[];
 
-  int id = blockIdx.x;
-  const int mc = id % p.m_chunks; id /= p.m_chunks;
-  const int split = id % p.splits;
-  const int tile = id / p.splits;
+  int mc, unit;
+  if (!chunked_unit(p.m_chunks, p.n_tiles * p.splits, mc, unit)) return;
+  const int split = unit % p.splits;
+  const int tile = unit / p.splits;
 
   int M = p.M;
   if (p.plan != nullptr) M = min(max(p.plan[0], 0), p.m_grid);

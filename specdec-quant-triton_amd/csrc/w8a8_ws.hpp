@@ -71,10 +71,10 @@ __global__ __launch_bounds__(NW * 64) void w8a8_ws_kernel(W8A8Params p) {
     else return lds_s5;
   };
 
-  int id = blockIdx.x;
-  const int mc = id % p.m_chunks; id /= p.m_chunks;
-  const int split = id % p.splits;
-  const int tile = id / p.splits;
+  int mc, unit;
+  if (!chunked_unit(p.m_chunks, p.n_tiles * p.splits, mc, unit)) return;
+  const int split = unit % p.splits;
+  const int tile = unit / p.splits;
 
   int M = p.M;
   if (p.plan != nullptr) M = min(max(p.plan[0], 0), p.m_grid);

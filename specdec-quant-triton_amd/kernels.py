@@ -262,7 +262,7 @@ def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK_K=12
                   M, N, K, int(grid_m_max or 0), _plan_ptr(plan), bm, bn, nw, split_k,
                   wptr, wbytes, _stream_ptr(a_q))
     _w8a8_kernel._note(a_q.device.index or 0, (bm, bn, nw))
-    return out, KernelInfo(0, 1 if packed else 0, m_grid, N, K, bm, bn, nw, split_k)
+    return out, KernelInfo(0, (1 if packed else 0) | (16 if plan is not None else 0), m_grid, N, K, bm, bn, nw, split_k)
 
 
 def quantize_act_int8(x):
@@ -397,7 +397,7 @@ def w4a16_matmul(a, wp, sc, group=128, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK
               M, N, K, int(group), int(grid_m_max or 0), _plan_ptr(plan), bm, bn, 4, split_k,
               wptr, wbytes, _stream_ptr(a))
     _w4a16_kernel._note(a.device.index or 0, (bm, bn, layout))
-    return out, KernelInfo(1, layout, m_grid, N, K, bm, bn, 4, split_k)
+    return out, KernelInfo(1, layout | (16 if plan is not None else 0), m_grid, N, K, bm, bn, 4, split_k)
 
 
 # ----------------------------------------------------------------------------------------
