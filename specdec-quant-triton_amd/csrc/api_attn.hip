@@ -27,10 +27,17 @@ const void* attn_fn(int D, int rb, int fp32) {
   return nullptr;
 }
 
+// 512-token sub-splits per split: 1 until the block table holds more than kAttnMergeMax of them.
+int split_sub_for(int max_pages, int PAGE) {
+  const int64_t subs = ((int64_t)max_pages * PAGE + kAttnSplitTokens - 1) / kAttnSplitTokens;
+  return subs <= kAttnMergeMax ? 1 : (int)((subs + kAttnMergeMax - 1) / kAttnMergeMax);
+}
+
 int n_splits_for(int max_pages, int PAGE) {
   const int64_t tokens = (int64_t)max_pages * PAGE;
-  return (int)((tokens + kAttnSplitTokens - 1) / kAttnSplitTokens) > 0
-             ? (int)((tokens + kAttnSplitTokens - 1) / kAttnSplitTokens) : 1;
+  const int64_t per = (int64_t)kAttnSplitTokens * split_sub_for(max_pages, PAGE);
+  const int ns = (int)((tokens + per - 1) / per);
+  return ns > 0 ? ns : 1;
 }
 
 }  // namespace
@@ -124,6 +131,7 @@ extern "C" int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64
   p.out = (_Float16*)out; p.s_ob = s_ob; p.s_ot = s_ot; p.s_oh = s_oh;
   p.plan = plan; p.B_grid = B_grid; p.n_seqs = plan ? B_grid : n_seqs; p.q_len = plan ? ql_grid : q_len;
   p.ql_grid = ql_grid; p.G = G; p.QPP = QPP; p.n_qc = n_qc; p.H_KV = H_KV; p.PAGE = PAGE; p.n_splits = ns;
+  p.split_sub = split_sub_for(max_pages, PAGE);
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   p.counters = need ? (int32_t*)workspace : nullptr;
   p.part = need ? (float*)((char*)workspace + kCounterBytes) : nullptr;

@@ -8,23 +8,30 @@
 // K/V are int8 [pages, PAGE, H_KV, D] reached through a block table; scales are fp16 or fp32.
 //
 // MI355X schedule:
-//  * One workgroup = (KV split of 512 tokens, KV head, query chunk of QPP tokens, sequence).
+//  * One workgroup = (KV split, KV head, query chunk of QPP tokens, sequence).  A split is 512
+//    tokens, or a multiple of 512 for block tables longer than 64 x 512 tokens.
 //    The QPP * G query rows sharing the KV head are packed into RB 16-row blocks, so a fused
 //    verification program reads each K/V byte once for all (k+1) * G rows.
-//  * S^T = K . Q^T on v_mfma_f32_16x16x32_f16 with K as the A-operand: each lane loads 32
-//    contiguous int8 bytes of one token row straight from HBM (block-table indirection per
-//    16-token page) and converts them to fp16 in registers.  The result lands with the query
-//    row in lane % 16, which is exactly the B-operand layout of the next product, so P never
-//    moves between lanes.
+//  * The four waves take interleaved 32-token chunks of the split (chunk c of the split goes
+//    to wave c % 4) and stream them through a two-deep register pipeline: the K rows, V rows
+//    and scales of the wave's next chunk are in flight while the current one is multiplied.
+//    Every lane loads 16-byte pieces: a K row is 4 lanes x 32 B, a V row 8 lanes x 16 B, one
+//    lane per token for each scale, all through the block table (one 16-token page sub-tile
+//    per page lookup).  Loads are never branched around: tokens past the program's last
+//    visible key read a valid dummy address (finite int8 whose P is 0).
+//  * S^T = K . Q^T on v_mfma_f32_16x16x32_f16 with K as the A-operand (int8 converted to fp16
+//    in registers by exponent injection).  The result lands with the query row in lane % 16,
+//    which is exactly the B-operand layout of the next product, so P never moves between
+//    lanes.  The scales of the chunk pass through a small wave-private LDS staging area so a
+//    lane reads the 4 consecutive tokens it needs with one 16-byte LDS read.
 //  * O^T = V^T . P^T with V^T as the A-operand.  V rows are transposed through a wave-private
 //    LDS tile (4x4 byte transposes with v_perm, dword writes, two dword reads per operand).
 //    The O accumulator then also has the query row in lane % 16, so the online-softmax
 //    rescale is lane local.
-//  * The four waves of a workgroup take interleaved 32-token chunks of its split and merge
-//    in a fixed order through LDS; splits merge in split order through the workspace (last
-//    workgroup to arrive).  The split boundaries are fixed token positions, so a row's result
-//    is bit-identical whether it is computed by a QPP=1 or a fused program, eagerly or from
-//    a plan-mode graph.
+//  * The waves merge in a fixed order through LDS; splits merge in split order through the
+//    workspace (16-byte hand-offs, last workgroup to arrive).  The split boundaries and the
+//    chunk-to-wave assignment are fixed token positions, so a row's result is bit-identical
+//    whether it is computed by a QPP=1 or a fused program, eagerly or from a plan-mode graph.
 //  * Plan mode reads (n_seqs, q_len) from plan[0..1]; programs for inactive sequences or
 //    query slots return before any load or store.
 #pragma once
@@ -43,6 +50,7 @@ struct AttnParams {
   int B_grid, n_seqs, q_len, ql_grid;
   int G, QPP, n_qc, H_KV, PAGE;
   int n_splits;        // splits the grid covers per program
+  int split_sub;       // 512-token sub-splits per split (longer contexts keep n_splits <= 64)
   float scale_log2;    // sm_scale * log2(e)
   float* part;         // [progs][n_splits][rows][D] unnormalised O, then [progs][n_splits][rows][2] (m, l)
   int32_t* counters;   // [progs]
@@ -52,6 +60,7 @@ constexpr int kAttnSplitTokens = 512;  // tokens per workgroup (KV split)
 constexpr int kAttnChunk = 32;         // tokens per wave iteration
 constexpr int kAttnWaves = 4;
 constexpr int kAttnVtPitch = 36;       // bytes per d-row of the transposed V tile (32 tokens + pad)
+constexpr int kAttnMergeMax = 64;      // most splits one program merges (fits the o_lds tile for D >= 64)
 
 template <typename ST>
 __device__ __forceinline__ float load_scale(const void* base, int64_t idx) {
@@ -75,11 +84,17 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
   constexpr int NU = D / 32;          // MFMA K-steps over the head dimension
   constexpr int ND = D / 16;          // 16-wide d blocks of the output
   constexpr int DS = D / 4;           // head-dim bytes a lane holds per token (K) or row (Q)
+  constexpr int DB = D / 8;           // V bytes per lane per token
   constexpr int ROWS = RB * 16;
-  constexpr int CHUNKS = kAttnSplitTokens / kAttnChunk;
+  constexpr int IT = kAttnSplitTokens / kAttnChunk / kAttnWaves;  // chunks per wave
+  constexpr int KV4 = D / 64;         // 16-byte K pieces per lane per 16-token sub-tile
+  constexpr int VW = D / 32;          // dwords per lane per V row piece
   __shared__ __attribute__((aligned(16))) uint8_t vt_lds[kAttnWaves][D * kAttnVtPitch];
+  __shared__ __attribute__((aligned(16))) float sc_lds[kAttnWaves][64];
   __shared__ float ml_lds[kAttnWaves][2][ROWS];
   __shared__ __attribute__((aligned(16))) float o_lds[ROWS][D + 4];
+  // Q fragments in MFMA B-operand order: [rb][u][lane] of 16 bytes (zero for padding rows).
+  __shared__ __attribute__((aligned(16))) v8h q_lds[RB][NU][64];
   __shared__ int s_last;
 
   const int split = blockIdx.x;
@@ -97,29 +112,23 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
   const int L = uniform(min(p.ctx_len[b], p.max_pages * p.PAGE));
   const int kv_end = L - q_len + min(qc * p.QPP + p.QPP, q_len);
   // Split 0 always runs, so rows with no visible key still get their zero output.
-  if (split > 0 && split * kAttnSplitTokens >= kv_end) return;
-  const int n_active = kv_end > kAttnSplitTokens ? (kv_end + kAttnSplitTokens - 1) / kAttnSplitTokens : 1;
+  const int split_tokens = kAttnSplitTokens * p.split_sub;
+  if (split > 0 && split * split_tokens >= kv_end) return;
+  const int n_active = kv_end > split_tokens ? (kv_end + split_tokens - 1) / split_tokens : 1;
 
   const int lane = lane_id(), w = wave_id(), g = lane >> 4, r = lane & 15;
   const int G = p.G;
 
-  // Query rows held by this lane (one per row block): row = rb*16 + r.
+  // Query rows held by this lane (one per row block): row = rb*16 + r.  Their B-operand
+  // fragments go to LDS once (each wave writes its share of the row blocks) and are read back
+  // per MFMA, which leaves registers for a three-chunk load pipeline.
   int qpos[RB];
-  bool rvalid[RB];
-  v8h qf[RB][NU];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int row = rb * 16 + r;
     const int qi = qc * p.QPP + row / G;
-    const int head = kvh * G + row % G;
-    rvalid[rb] = (row < p.QPP * G) && (qi < q_len);
-    qpos[rb] = rvalid[rb] ? (L - q_len + qi) : -1;
-    const _Float16* qrow = p.q + (int64_t)b * p.s_qb + (int64_t)qi * p.s_qt + (int64_t)head * p.s_qh + DS * g;
-#pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      if (rvalid[rb]) qf[rb][u] = *reinterpret_cast<const v8h*>(qrow + 8 * u);
-      else qf[rb][u] = v8h{0, 0, 0, 0, 0, 0, 0, 0};
-    }
+    const bool valid = (row < p.QPP * G) && (qi < q_len);
+    qpos[rb] = valid ? (L - q_len + qi) : -1;
   }
 
   float m_run[RB], l_run[RB];
@@ -133,93 +142,134 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
   }
 
   uint8_t* vt = vt_lds[w];
+  float* scw = sc_lds[w];
   const int64_t kv_head_off = (int64_t)kvh * p.s_kh;
   const int64_t sc_head_off = (int64_t)kvh * p.s_sh;
   const int32_t* bt_row = p.bt + (int64_t)b * p.s_bt;
+  const int PAGE = p.PAGE;
 
-  for (int it = 0; it < CHUNKS / kAttnWaves; ++it) {
-    const int t0 = split * kAttnSplitTokens + (it * kAttnWaves + w) * kAttnChunk;
-    if (t0 >= kv_end) break;  // wave-uniform; later chunks of this wave are further out
-
-    // ---- K tile: two 16-token sub-tiles, lane (tt, g) loads bytes [32g, 32g+32) of token tt.
-    v8h kf[2][NU];
-    float ksc[2][4], vsc[2][4];
-    uint32_t vraw[4][4];
+  // ---- Chunk loads.  Chunk `it` of this wave starts at token t0(it); its two 16-token
+  // sub-tiles each lie in one page.  Masked tokens (at or past kv_end) read the first bytes of
+  // the cache instead: their int8 K/V are finite, their scores are masked to -inf and their P
+  // is 0, so they add nothing; their scales are zeroed.
+  int sub_base = split * split_tokens;  // first token of the current 512-token sub-split
+  auto chunk_t0 = [&](int it) { return sub_base + (it * kAttnWaves + w) * kAttnChunk; };
+  // Register double buffer of the raw chunk bytes: K pieces, V pieces, one scale per lane
+  // (lane l < 32: ks of token l; lane >= 32: vs of token l - 32).
+  constexpr int NB = 2;  // chunks in the register pipeline
+  v4i kbuf[NB][2][KV4];
+  uint32_t vbuf[NB][4][VW];
+  float sbuf[NB];
+  // Pages of the wave's 2 * IT sub-tiles in the current 512-token sub-split, looked up together
+  // at its start (one block-table round trip instead of one per chunk).
+  int pages[IT][2];
+  auto lookup_pages = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int it = 0; it < IT; ++it)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int ts = chunk_t0(it) + 16 * j;
+        pages[it][j] = ts < kv_end ? bt_row[ts / PAGE] : 0;
+      }
+  };
+  auto load_chunk = [&](auto bic, auto itc) __attribute__((always_inline)) {
+    constexpr int bi = decltype(bic)::value;
+    constexpr int it = decltype(itc)::value;
+    const int t0 = chunk_t0(it);
+    int64_t pbase[2];  // element offset of (page, token 0 of the sub-tile, this KV head) in the cache
+    int64_t sbase[2];  // element offset of the sub-tile's first scale
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int ts = t0 + 16 * j;
-      if (ts < kv_end) {
-        const int page = bt_row[ts / p.PAGE];
-        const int off0 = ts % p.PAGE;
-        const int8_t* krow = p.kc + (int64_t)page * p.s_kp + (int64_t)(off0 + r) * p.s_ko + kv_head_off + DS * g;
-        const v4i k0 = *reinterpret_cast<const v4i*>(krow);
-        kf[j][0] = i8x8_to_h8((uint32_t)k0.x, (uint32_t)k0.y);
-        kf[j][1] = i8x8_to_h8((uint32_t)k0.z, (uint32_t)k0.w);
-        if constexpr (NU == 4) {
-          const v4i k1 = *reinterpret_cast<const v4i*>(krow + 16);
-          kf[j][2] = i8x8_to_h8((uint32_t)k1.x, (uint32_t)k1.y);
-          kf[j][3] = i8x8_to_h8((uint32_t)k1.z, (uint32_t)k1.w);
-        }
-        const int64_t sbase = (int64_t)page * p.s_sp + sc_head_off;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int64_t si = sbase + (int64_t)(off0 + 4 * g + i) * p.s_so;
-          ksc[j][i] = load_scale<ST>(p.ks, si);
-          vsc[j][i] = load_scale<ST>(p.vs, si);
-        }
-      } else {
-#pragma unroll
-        for (int u = 0; u < NU; ++u) kf[j][u] = v8h{0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) { ksc[j][i] = 0.f; vsc[j][i] = 0.f; }
-      }
+      pbase[j] = (int64_t)pages[it][j] * p.s_kp + (int64_t)(ts % PAGE) * p.s_ko + kv_head_off;
+      sbase[j] = (int64_t)pages[it][j] * p.s_sp + (int64_t)(ts % PAGE) * p.s_so + sc_head_off;
     }
-    // ---- V tile: lane (tq = lane/8, dq = lane%8) loads 4 tokens x (D/8) bytes.
+    // K: lane (r, g) holds bytes [DS*g, DS*g + DS) of token 16j + r.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const bool ok = t0 + 16 * j + r < kv_end;
+      const int8_t* src = p.kc + (ok ? pbase[j] + (int64_t)r * p.s_ko + DS * g : 0);
+#pragma unroll
+      for (int h = 0; h < KV4; ++h) kbuf[bi][j][h] = *reinterpret_cast<const v4i*>(src + 16 * h);
+    }
+    // V: lane (tq = lane / 8, dq = lane % 8) holds DB bytes at d = DB*dq of tokens 4tq .. 4tq+3.
     {
-      const int tq = lane >> 3, dq = lane & 7;
-      const int ts = t0 + 4 * tq;
-      const int j = tq >> 2;  // sub-tile
-      const bool ok = (t0 + 16 * j) < kv_end;
-      const int page = ok ? bt_row[(t0 + 16 * j) / p.PAGE] : 0;
-      const int off = (t0 + 16 * j) % p.PAGE + (ts - t0 - 16 * j);
-      constexpr int DB = D / 8;  // bytes per lane per token: 16 (D=128) or 8 (D=64)
-      const int8_t* vrow = p.vc + (int64_t)page * p.s_kp + (int64_t)off * p.s_ko + kv_head_off + DB * dq;
+      const int tq = lane >> 3, dq = lane & 7, j = tq >> 2;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if constexpr (DB == 16) {
-          v4i v = ok ? *reinterpret_cast<const v4i*>(vrow + (int64_t)i * p.s_ko) : v4i{0, 0, 0, 0};
-          vraw[i][0] = v.x; vraw[i][1] = v.y; vraw[i][2] = v.z; vraw[i][3] = v.w;
+        const int tl = 4 * (tq & 3) + i;  // token within sub-tile j
+        const bool ok = t0 + 16 * j + tl < kv_end;
+        const int8_t* src = p.vc + (ok ? pbase[j] + (int64_t)tl * p.s_ko + DB * dq : 0);
+        if constexpr (VW == 4) {
+          const v4i x = *reinterpret_cast<const v4i*>(src);
+          vbuf[bi][i][0] = (uint32_t)x.x; vbuf[bi][i][1] = (uint32_t)x.y;
+          vbuf[bi][i][2] = (uint32_t)x.z; vbuf[bi][i][3] = (uint32_t)x.w;
         } else {
-          v2i v = ok ? *reinterpret_cast<const v2i*>(vrow + (int64_t)i * p.s_ko) : v2i{0, 0};
-          vraw[i][0] = v.x; vraw[i][1] = v.y; vraw[i][2] = 0; vraw[i][3] = 0;
+          const v2i x = *reinterpret_cast<const v2i*>(src);
+          vbuf[bi][i][0] = (uint32_t)x.x; vbuf[bi][i][1] = (uint32_t)x.y;
         }
       }
-      // transpose and store: Vt[d][token] for d in [DB*dq, DB*dq + DB), tokens 4tq..4tq+3
+    }
+    // Scales: lane l holds ks (l < 32) or vs (l >= 32) of token l % 32.
+    {
+      const int tl = lane & 31, j = tl >> 4;
+      const bool ok = t0 + tl < kv_end;
+      const int64_t si = ok ? sbase[j] + (int64_t)(tl & 15) * p.s_so : 0;
+      const float x = load_scale<ST>(lane < 32 ? p.ks : p.vs, si);
+      sbuf[bi] = ok ? x : 0.f;
+    }
+  };
+
+  // ---- One chunk: stage V^T and the scales in LDS, S^T, online softmax, O^T += V^T . P^T.
+  auto compute_chunk = [&](auto bic, int it) __attribute__((always_inline)) {
+    constexpr int bi = decltype(bic)::value;
+    const int t0 = chunk_t0(it);
+    // Stage: Vt[d][token] for d in [DB*dq, DB*dq + DB), tokens 4tq..4tq+3; the 64 scales.
+    {
+      const int tq = lane >> 3, dq = lane & 7;
 #pragma unroll
-      for (int c = 0; c < DB / 4; ++c) {
-        uint32_t x[4] = {vraw[0][c], vraw[1][c], vraw[2][c], vraw[3][c]};
+      for (int cc = 0; cc < DB / 4; ++cc) {
+        uint32_t x[4] = {vbuf[bi][0][cc], vbuf[bi][1][cc], vbuf[bi][2][cc], vbuf[bi][3][cc]};
         uint32_t y[4];
         transpose4x4(x, y);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          *reinterpret_cast<uint32_t*>(vt + (DB * dq + 4 * c + e) * kAttnVtPitch + 4 * tq) = y[e];
+          *reinterpret_cast<uint32_t*>(vt + (DB * dq + 4 * cc + e) * kAttnVtPitch + 4 * tq) = y[e];
       }
+      scw[lane] = sbuf[bi];
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // Scales of the lane's tokens 16j + 4g + i: ks at [0, 32), vs at [32, 64).
+    v4f ksc[2], vsc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      ksc[j] = *reinterpret_cast<const v4f*>(scw + 16 * j + 4 * g);
+      vsc[j] = *reinterpret_cast<const v4f*>(scw + 32 + 16 * j + 4 * g);
+    }
+    // K fragment u of sub-tile j (8 int8 -> fp16), converted where it is used.
+    auto kfrag = [&](int j, int u) __attribute__((always_inline)) {
+      const v4i& x = kbuf[bi][j][u >> 1];
+      return (u & 1) ? i8x8_to_h8((uint32_t)x.z, (uint32_t)x.w) : i8x8_to_h8((uint32_t)x.x, (uint32_t)x.y);
+    };
 
-    // ---- S^T = K . Q^T, online softmax, P^T operand.
+    // Every row of the program sees every token of the chunk: no causal mask needed.
+    const bool full = t0 + kAttnChunk - 1 <= L - q_len + qc * p.QPP;
     v8h pf[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       float s[2][4];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        v4f c = {0.f, 0.f, 0.f, 0.f};
+        v4f cs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int u = 0; u < NU; ++u) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[j][u], qf[rb][u], c, 0, 0, 0);
+        for (int u = 0; u < NU; ++u) cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfrag(j, u), q_lds[rb][u][lane], cs, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int t = t0 + 16 * j + 4 * g + i;
-          s[j][i] = (t <= qpos[rb]) ? c[i] * (ksc[j][i] * p.scale_log2) : -INFINITY;
+          const float v = cs[i] * (ksc[j][i] * p.scale_log2);
+          s[j][i] = (full || t <= qpos[rb]) ? v : -INFINITY;
         }
       }
       float cmax = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
@@ -239,15 +289,18 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
           pf[rb][4 * j + i] = (_Float16)(pv * vsc[j][i]);
         }
       l_run[rb] = l_run[rb] * alpha + psum;
+      // alpha is exactly 1 for every row whose running max did not grow, so the O rescale is
+      // skipped (bit-identically) unless some row of the wave's block grew, which after the
+      // first chunks is rare; the accumulators then stay in the MFMA's registers.
+      const bool grew = m_new > m_run[rb];
       m_run[rb] = m_new;
+      if (__builtin_amdgcn_ballot_w64(grew) != 0) {
 #pragma unroll
-      for (int db = 0; db < ND; ++db) acc[rb][db] *= alpha;
+        for (int db = 0; db < ND; ++db) acc[rb][db] *= alpha;
+      }
     }
 
-    // ---- O^T += V^T . P^T  (A-operand: lane (d, g) holds tokens {4g..4g+3, 16+4g..16+4g+3} of d)
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // O^T += V^T . P^T  (A-operand: lane (d, g) holds tokens {4g..4g+3, 16+4g..16+4g+3} of d)
 #pragma unroll
     for (int db = 0; db < ND; ++db) {
       const uint8_t* vrow = vt + (db * 16 + r) * kAttnVtPitch;
@@ -261,6 +314,58 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  // Chunk it + 1 is in flight while chunk it is multiplied; the first sub-split's
+  // page lookups and first loads are issued before the Q fragments are staged, so those
+  // memory round trips overlap.
+  // Q fragments: thread t stages fragments t, t + 256, ... of [rb][u][lane].
+  constexpr int QF = (RB * NU * 64 + 255) / 256;
+  auto q_frag_valid = [&](int f) {
+    const int row = (f / (NU * 64)) * 16 + (f % 64 & 15);
+    return f < RB * NU * 64 && (row < p.QPP * G) && (qc * p.QPP + row / G < q_len);
+  };
+  auto q_frag_src = [&](int f) -> const _Float16* {  // a valid fragment's 8 halves
+    const int rb = f / (NU * 64), u = (f / 64) % NU, ln = f % 64;
+    const int row = rb * 16 + (ln & 15);
+    const int qi = qc * p.QPP + row / G;
+    const int head = kvh * G + row % G;
+    return p.q + (int64_t)b * p.s_qb + (int64_t)qi * p.s_qt + (int64_t)head * p.s_qh + DS * (ln >> 4) + 8 * u;
+  };
+  bool staged = false;
+  for (int sub = 0; sub < p.split_sub && sub_base < kv_end; ++sub, sub_base += kAttnSplitTokens) {
+    lookup_pages();
+    v8h qtmp[QF];
+    if (!staged) {
+#pragma unroll
+      for (int i = 0; i < QF; ++i) {
+        const int f = threadIdx.x + 256 * i;
+        const bool ok = q_frag_valid(f);
+        const v8h x = *reinterpret_cast<const v8h*>(ok ? q_frag_src(f) : p.q);
+        qtmp[i] = ok ? x : v8h{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+    static_for<0, NB - 1>([&](auto ic) __attribute__((always_inline)) {
+      constexpr int i = decltype(ic)::value;
+      if constexpr (i < IT) load_chunk(std::integral_constant<int, i>{}, std::integral_constant<int, i>{});
+    });
+    if (!staged) {
+      // The Q fragments go to LDS while the first chunks stay in flight (the barrier waits
+      // for LDS only).
+#pragma unroll
+      for (int i = 0; i < QF; ++i) {
+        const int f = threadIdx.x + 256 * i;
+        if (f < RB * NU * 64) (&q_lds[0][0][0])[f] = qtmp[i];
+      }
+      wg_barrier_lds();
+      staged = true;
+    }
+    static_for<0, IT>([&](auto itc) __attribute__((always_inline)) {
+      constexpr int it = decltype(itc)::value;
+      if constexpr (it + NB - 1 < IT)
+        load_chunk(std::integral_constant<int, (it + NB - 1) % NB>{}, std::integral_constant<int, it + NB - 1>{});
+      if (chunk_t0(it) < kv_end) compute_chunk(std::integral_constant<int, it % NB>{}, it);
+    });
   }
 
   // ---- Merge the four waves in a fixed order.
@@ -290,13 +395,11 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int db = 0; db < ND; ++db)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float* dst = &o_lds[rb * 16 + r][db * 16 + 4 * g + i];
-            const float v = acc[rb][db][i] * wscale[rb];
-            *dst = (ww == 0) ? v : (*dst + v);
-          }
+        for (int db = 0; db < ND; ++db) {
+          v4f* dst = reinterpret_cast<v4f*>(&o_lds[rb * 16 + r][db * 16 + 4 * g]);
+          const v4f v = acc[rb][db] * wscale[rb];
+          *dst = (ww == 0) ? v : (*dst + v);
+        }
     }
     __syncthreads();
   }
@@ -331,13 +434,16 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
     return;
   }
 
-  // ---- Cross-split merge: publish this split, the last to arrive combines in split order.
+  // ---- Cross-split merge: publish this split (16 bytes per lane), the last to arrive combines
+  // the splits in split order.
   const int64_t prog_base = (int64_t)prog * p.n_splits;
-  float* opart = p.part;
-  float* mlpart = p.part + (int64_t)gridDim.y * gridDim.z * p.n_splits * ROWS * D;
-  for (int e = threadIdx.x; e < ROWS * D; e += blockDim.x) {
-    const int row = e / D, d = e % D;
-    publish(opart + ((prog_base + split) * ROWS + row) * D + d, o_lds[row][d]);
+  const int64_t n_o = (int64_t)gridDim.y * gridDim.z * p.n_splits * ROWS * D;  // floats of the O region
+  const rsrc_t ors = make_rsrc(p.part + prog_base * ROWS * D, (uint32_t)(p.n_splits * ROWS * D * 4));
+  float* mlpart = p.part + n_o;
+  for (int e = threadIdx.x; e < ROWS * D / 4; e += blockDim.x) {
+    const int row = e / (D / 4), d = (e % (D / 4)) * 4;
+    const v4f v = *reinterpret_cast<const v4f*>(&o_lds[row][d]);
+    publish16(ors, (uint32_t)(((split * ROWS + row) * D + d) * 4), __builtin_bit_cast(v4i, v));
   }
   if (threadIdx.x < ROWS) {
     float* mlp = mlpart + ((prog_base + split) * ROWS + threadIdx.x) * 2;
@@ -345,33 +451,88 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
     publish(mlp + 1, ml_lds[0][1][threadIdx.x]);
   }
   if (!arrive_last(p.counters + prog, n_active, &s_last)) return;
-  for (int e = threadIdx.x; e < ROWS * DCH; e += blockDim.x) {
-    const int row = e / DCH, d0 = (e % DCH) * 8;
-    const int qi = qc * p.QPP + row / G;
-    if (!(row < p.QPP * G && qi < q_len)) continue;
-    const int head = kvh * G + row % G;
-    float mx = -INFINITY;
-    for (int s = 0; s < n_active; ++s) mx = fmaxf(mx, collect(mlpart + ((prog_base + s) * ROWS + row) * 2));
-    const float ms = (mx == -INFINITY) ? 0.f : mx;
-    float o[8];
-    float l = 0.f;
-    for (int s = 0; s < n_active; ++s) {
-      const float* mlp = mlpart + ((prog_base + s) * ROWS + row) * 2;
-      const float ws = fast_exp2(collect(mlp) - ms);
-      const float ls = ws * collect(mlp + 1);
-      l = (s == 0) ? ls : l + ls;
-      const float* op = opart + ((prog_base + s) * ROWS + row) * D + d0;
+  // Row weights of the splits, exp2(m_s - max) / l (l summed in split order), kept in the
+  // o_lds tile (already published).  Up to 16 splits the (m, l) pairs are loaded once, all in
+  // flight together; more splits take a second pass.
+  constexpr int kMergeBatch = 16;
+  if (threadIdx.x < ROWS) {
+    const int row = threadIdx.x;
+    float* wt = &o_lds[row][0];
+    auto ml_at = [&](int sp) { return mlpart + ((prog_base + (sp < n_active ? sp : 0)) * ROWS + row) * 2; };
+    float mv[kMergeBatch], lv[kMergeBatch];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float v = ws * collect(op + i);
-        o[i] = (s == 0) ? v : o[i] + v;
+    for (int u = 0; u < kMergeBatch; ++u) {
+      mv[u] = collect(ml_at(u));
+      lv[u] = collect(ml_at(u) + 1);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u)
+      if (u < n_active) mx = fmaxf(mx, mv[u]);
+    for (int sp = kMergeBatch; sp < n_active; ++sp) mx = fmaxf(mx, collect(ml_at(sp)));
+    const float mxs = (mx == -INFINITY) ? 0.f : mx;
+    float l = 0.f;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u)
+      if (u < n_active) {
+        const float wgt = fast_exp2(mv[u] - mxs);
+        wt[u] = wgt;
+        const float lw = wgt * lv[u];
+        l = (u == 0) ? lw : l + lw;
       }
+    for (int sp = kMergeBatch; sp < n_active; ++sp) {
+      const float wgt = fast_exp2(collect(ml_at(sp)) - mxs);
+      wt[sp] = wgt;
+      l += wgt * collect(ml_at(sp) + 1);
     }
     const float inv = (l == 0.f) ? 0.f : 1.f / l;
-    v8h out;
+    for (int sp = 0; sp < n_active; ++sp) wt[sp] *= inv;
+  }
+  __syncthreads();
+  // O rows: sum over splits in split order of weight * partial O.  Thread t owns the 4-column
+  // items t, t + 256, ...; all of its items' loads of 4 splits are in flight together.
+  constexpr int QPR = D / 4;                       // 4-column items per row
+  constexpr int ITEMS = (ROWS * QPR + 255) / 256;  // items per thread
+  constexpr int SB = 8;                            // splits per batch
+  v4f o[ITEMS];
+  uint32_t ioff[ITEMS];
+  bool ivalid[ITEMS];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) out[i] = (_Float16)(o[i] * inv);
-    *reinterpret_cast<v8h*>(p.out + (int64_t)b * p.s_ob + (int64_t)qi * p.s_ot + (int64_t)head * p.s_oh + d0) = out;
+  for (int it = 0; it < ITEMS; ++it) {
+    const int e = threadIdx.x + 256 * it;
+    const int row = e / QPR, d0 = (e % QPR) * 4;
+    const int qi = qc * p.QPP + row / G;
+    ivalid[it] = e < ROWS * QPR && row < p.QPP * G && qi < q_len;
+    ioff[it] = (uint32_t)((row * D + d0) * 4);
+    o[it] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int s0 = 0; s0 < n_active; s0 += SB) {
+    v4i t[SB][ITEMS];
+#pragma unroll
+    for (int u = 0; u < SB; ++u)
+#pragma unroll
+      for (int it = 0; it < ITEMS; ++it)
+        t[u][it] = collect16(ors, oob_unless(ivalid[it] && s0 + u < n_active,
+                                             (uint32_t)((s0 + u) * ROWS * D * 4) + ioff[it]));
+#pragma unroll
+    for (int u = 0; u < SB; ++u)
+#pragma unroll
+      for (int it = 0; it < ITEMS; ++it)
+        if (ivalid[it] && s0 + u < n_active) {
+          const int e = threadIdx.x + 256 * it;
+          o[it] += o_lds[e / QPR][s0 + u] * __builtin_bit_cast(v4f, t[u][it]);
+        }
+  }
+  typedef _Float16 v4h_t __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    if (!ivalid[it]) continue;
+    const int e = threadIdx.x + 256 * it;
+    const int row = e / QPR, d0 = (e % QPR) * 4;
+    const int qi = qc * p.QPP + row / G;
+    const int head = kvh * G + row % G;
+    *reinterpret_cast<v4h_t*>(p.out + (int64_t)b * p.s_ob + (int64_t)qi * p.s_ot + (int64_t)head * p.s_oh + d0) =
+        v4h_t{(_Float16)o[it].x, (_Float16)o[it].y, (_Float16)o[it].z, (_Float16)o[it].w};
   }
 }
 
