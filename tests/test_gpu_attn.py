@@ -105,3 +105,23 @@ def test_attention_head_dim_64_and_no_visible_key():
     torch.cuda.synchronize()
     check(out, ref, 4, "D=64")
     assert bool((out[1, :2] == 0).all())
+
+
+def test_attention_long_context_sub_splits():
+    """A block table beyond 64 x 512 tokens makes each workgroup cover several 512-token
+    sub-splits; results stay within tolerance and QPP=1 still equals the fused program."""
+    B, k = 2, 3
+    ql = k + 1
+    ctx = [33000 + ql, 20000 + ql]   # the block table spans ~33K tokens for both sequences
+    kc, vc, ks, vs, bt, cl = gen.paged_kv(B, ctx, H_KV, D, seed=71)
+    q = gen.queries(B, ql, H, D, seed=72)
+    ref = O.paged_attention(*cpu(q, kc, vc, ks, vs, bt, cl), ql)
+    kc, vc, ks, vs, bt, cl, q = (t.to(DEV) for t in (kc, vc, ks, vs, bt, cl, q))
+    note(f"attn long context ctx={ctx} max_pages={bt.shape[1]}")
+    outs = {}
+    for QPP in (1, ql):
+        out, _ = K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=QPP)
+        torch.cuda.synchronize()
+        check(out, ref, ql, f"long ctx QPP={QPP}")
+        outs[QPP] = out
+    assert torch.equal(outs[1], outs[ql]), "QPP=1 and fused results differ"
