@@ -96,6 +96,9 @@ const void* ws_fn(int bnsel, int layout, int mt) {
 }
 
 int bn_of_sel(int sel) { return 16 << sel; }
+int kw_of_sel(int sel) { return sel == 0 ? 4 : (sel == 1 ? 2 : 1); }  // waves splitting K
+static_assert(W8A8BnSel<0>::KW == 4 && W8A8BnSel<1>::KW == 2 && W8A8BnSel<2>::KW == 1 && W8A8BnSel<3>::KW == 1,
+              "kw_of_sel mirrors the tile table");
 
 // Resolve the kernel and its tiles.  `vec` is the operand alignment (16 when unknown),
 // `layout` 0 = row-major weight, 1 = packed fragments.
@@ -168,7 +171,7 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   cfg->m_chunks = ceil_div(m_grid > 0 ? m_grid : 1, mt * 16);
   const int BM = mt * 16, BN = cfg->bn;
   if (family == kRk) {
-    cfg->lds = bnsel <= 1 ? (size_t)BM * BN * 4 : 0;  // cross-wave reduction slice
+    cfg->lds = (size_t)(kw_of_sel(bnsel) - 1) * BM * BN * 4;  // one reduction slice per non-owner wave
   } else if (family == kWs) {
     cfg->lds = 0;  // static LDS
   } else {

@@ -183,6 +183,15 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // to be turned into a branch around the load, which costs a vmcnt(0) at the join.
 __device__ __forceinline__ uint32_t oob_unless(bool ok, uint32_t off) { return off | ((uint32_t)(!ok) << 31); }
 
+// Returns x unchanged while hiding from the compiler how it was computed.  Used on an fp32
+// product that is then cast to fp16: the compiler otherwise folds fptrunc(a * b) into one
+// v_fma_mix, which rounds the exact product to fp16 once instead of rounding to fp32 first
+// (the two differ when the fp32 product lands on an fp16 rounding midpoint).
+__device__ __forceinline__ float f32_opaque(float x) {
+  asm("" : "+v"(x));
+  return x;
+}
+
 // 16-byte LDS DMA (buffer_load_dwordx4 ... lds): lane l's 16 bytes from voff land at
 // lds_frag + 16*l (lds_frag must be wave-uniform); out-of-range lanes write zeros.
 __device__ __forceinline__ void dma16(rsrc_t rs, uint8_t* lds_frag, uint32_t voff) {

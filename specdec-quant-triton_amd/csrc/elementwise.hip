@@ -25,6 +25,8 @@ struct EltParams {
 };
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+// silu(gate) * up is rounded to fp32 and then cast to fp16 (f32_opaque keeps the multiply and
+// the cast from being fused into one v_fma_mix with a single rounding).
 
 template <int MODE>  // 0 = silu_mul, 1 = quantize, 2 = silu_mul + quantize
 __global__ __launch_bounds__(256) void elt_kernel(EltParams p) {
@@ -38,7 +40,7 @@ __global__ __launch_bounds__(256) void elt_kernel(EltParams p) {
 
   auto value = [&](int k) -> _Float16 {
     if constexpr (MODE == 1) return xr[k];
-    else return (_Float16)(silu_f((float)xr[k]) * (float)ur[k]);
+    else return (_Float16)f32_opaque(silu_f((float)xr[k]) * (float)ur[k]);
   };
 
   if constexpr (MODE == 0) {
@@ -91,7 +93,7 @@ __global__ __launch_bounds__(256) void elt_vec_kernel(EltParams p) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if constexpr (MODE == 1) val[i][j] = xv[i][j];
-      else val[i][j] = (_Float16)(silu_f((float)xv[i][j]) * (float)uv[i][j]);
+      else val[i][j] = (_Float16)f32_opaque(silu_f((float)xv[i][j]) * (float)uv[i][j]);
     }
   if constexpr (MODE == 0) {
     v8h* hr = reinterpret_cast<v8h*>(p.h + (int64_t)m * p.ldh);

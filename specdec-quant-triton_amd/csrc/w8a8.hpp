@@ -60,24 +60,67 @@ __device__ __forceinline__ void w8a8_mma_step(const v4i (&wf)[RW], const v4i (&a
       acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[i], af[j], acc[i][j], 0, 0, 0);
 }
 
-// Epilogue for 4 consecutive output channels of one token row.
-__device__ __forceinline__ void w8a8_store4(const W8A8Params& p, int m, int n, v4i s) {
-  const float a = p.sa[m];
+// Epilogue for 4 consecutive output channels of one token row, with the token scale `a` and
+// the channel scales `w` already in registers (entries past N are not stored).
+__device__ __forceinline__ void w8a8_store4s(const W8A8Params& p, int m, int n, v4i s, float a, const float (&w)[4]) {
   __half* dst = p.C + (int64_t)m * p.ldc + n;
-  float v[4] = {(float)s.x, (float)s.y, (float)s.z, (float)s.w};
+  // Each value is rounded to fp32 and then to fp16, as in the reference (f32_opaque keeps the
+  // compiler from fusing the last multiply into the fp16 conversion).
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = f32_opaque(((float)s[i] * a) * w[i]);
   if (p.vec_store && n + 3 < p.N) {
-    v4f w = *reinterpret_cast<const v4f*>(p.sw + n);
-    _Float16 h0 = (_Float16)((v[0] * a) * w.x), h1 = (_Float16)((v[1] * a) * w.y);
-    _Float16 h2 = (_Float16)((v[2] * a) * w.z), h3 = (_Float16)((v[3] * a) * w.w);
     typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-    v4h o = {h0, h1, h2, h3};
+    const v4h o = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
     *reinterpret_cast<v4h*>(dst) = o;
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (n + i < p.N) dst[i] = __float2half_rn((v[i] * a) * p.sw[n + i]);
+      if (n + i < p.N) dst[i] = __float2half_rn(v[i]);
   }
 }
+
+// Epilogue for 4 consecutive output channels of one token row (scales read here).
+__device__ __forceinline__ void w8a8_store4(const W8A8Params& p, int m, int n, v4i s) {
+  float w[4];
+  if (n + 3 < p.N) {
+    const v4f q = *reinterpret_cast<const v4f*>(p.sw + n);
+    w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = n + i < p.N ? p.sw[n + i] : 0.f;
+  }
+  w8a8_store4s(p, m, n, s, p.sa[m], w);
+}
+
+// The epilogue scales of one lane's outputs, fetched before the main loop so that the
+// epilogue of a weight-streaming kernel does not begin with one more memory round trip:
+// sa of token rows m0 + 16u + r (u < MT) and sw of channels n0 + 16t + 4g .. + 3 (t < RW),
+// lane = 16g + r.  Entries past M or N, and every entry of lanes with `use` false, are
+// range-checked buffer reads that return zero without touching memory; the loads carry no
+// control flow, so they do not disturb the compile-time wait counts that follow.
+template <int MT, int RW>
+struct W8A8EpiScales {
+  float a[MT];
+  float w[RW][4];
+  __device__ __forceinline__ void load(const W8A8Params& p, int M, int m0, int n0, bool use) {
+    const int lane = lane_id(), g = lane >> 4, r = lane & 15;
+    const rsrc_t ars = make_rsrc(p.sa, (uint32_t)max(M, 0) * 4u);
+    const rsrc_t wrs = make_rsrc(p.sw, (uint32_t)p.N * 4u);
+#pragma unroll
+    for (int u = 0; u < MT; ++u) {
+      const int m = m0 + 16 * u + r;
+      a[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ars, oob_unless(use & (m < M), (uint32_t)m * 4u), 0, 0));
+    }
+#pragma unroll
+    for (int t = 0; t < RW; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = n0 + 16 * t + 4 * g + i;
+        w[t][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wrs, oob_unless(use & (n < p.N), (uint32_t)n * 4u), 0, 0));
+      }
+  }
+};
 
 // Split-K hand-off of a workgroup's INT32 tile [BM][BN] (row = token), 16 bytes per lane.
 // Partials of tile cidx live at p.partials + cidx * splits * BM * BN, split-major.

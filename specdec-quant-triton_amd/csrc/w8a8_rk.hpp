@@ -44,7 +44,7 @@ struct W8A8RkCfg {
   static constexpr int NS0 = NS_REG < NS_CNT ? NS_REG : NS_CNT;
   static constexpr int NS = NS0 > 8 ? 8 : (NS0 < 2 ? 2 : NS0);
   static constexpr int D = NS - 1;                      // steps in flight
-  static constexpr int RED_BYTES = KW > 1 ? BM * BN * 4 : 0;  // one reduction slice
+  static constexpr int RED_BYTES = (KW - 1) * BM * BN * 4;     // one slice per non-owner wave
 };
 
 template <int MT, int RW, int KW, int NW, int LAYOUT>
@@ -118,6 +118,10 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
       slot[RW + j] = __builtin_amdgcn_raw_buffer_load_b128(asrc, oob_unless(live & (arow[j] != kOOB), arow[j] + (uint32_t)k0), 0, 0);
   };
 
+  const bool owner = kw == 0;
+  W8A8EpiScales<MT, RW> es;
+  es.load(p, M, m0, n0, owner & (p.splits == 1));
+
   v4i acc[RW][MT];
 #pragma unroll
   for (int t = 0; t < RW; ++t)
@@ -152,27 +156,26 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
   }
   wait_vmcnt<0>();
 
-  // Reduce the KW waves of each channel group through LDS, one slice per round; every wave
-  // stays to the end so the workgroup barriers see all of them.
-  const bool owner = kw == 0;
+  // Reduce the KW waves of each channel group through LDS in one round: each non-owner wave
+  // writes its slice, then the owner adds them.
   if constexpr (KW > 1) {
-    for (int q = 1; q < KW; ++q) {
-      if (kw == q) {
+    constexpr int SLICE = BM * BN;  // int32 per slice
+    if (kw > 0) {
+#pragma unroll
+      for (int a = 0; a < RW; ++a)
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+          *reinterpret_cast<v4i*>(smem_rk + (kw - 1) * SLICE + ((j * 16 + r) * BN + cw * BNW + a * 16 + 4 * g)) = acc[a][j];
+    }
+    __syncthreads();
+    if (owner) {
+#pragma unroll
+      for (int q = 0; q < KW - 1; ++q)
 #pragma unroll
         for (int a = 0; a < RW; ++a)
 #pragma unroll
           for (int j = 0; j < MT; ++j)
-            *reinterpret_cast<v4i*>(smem_rk + ((j * 16 + r) * BN + cw * BNW + a * 16 + 4 * g)) = acc[a][j];
-      }
-      __syncthreads();
-      if (owner) {
-#pragma unroll
-        for (int a = 0; a < RW; ++a)
-#pragma unroll
-          for (int j = 0; j < MT; ++j)
-            acc[a][j] += *reinterpret_cast<const v4i*>(smem_rk + ((j * 16 + r) * BN + cw * BNW + a * 16 + 4 * g));
-      }
-      __syncthreads();
+            acc[a][j] += *reinterpret_cast<const v4i*>(smem_rk + q * SLICE + ((j * 16 + r) * BN + cw * BNW + a * 16 + 4 * g));
     }
   }
 
@@ -184,7 +187,7 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
           const int m = m0 + j * 16 + r, n = n0 + a * 16 + 4 * g;
-          if (m < M && n < p.N) w8a8_store4(p, m, n, acc[a][j]);
+          if (m < M && n < p.N) w8a8_store4s(p, m, n, acc[a][j], es.a[j], es.w[a]);
         }
     }
     return;

@@ -152,6 +152,10 @@ __global__ __launch_bounds__(NW * 64) void w8a8_ws_kernel(W8A8Params p) {
     }
   };
 
+  const bool owner = kw == 0;
+  W8A8EpiScales<MT, RW> es;
+  es.load(p, M, m0, n0, owner & (p.splits == 1));
+
   v4i acc[RW][MT];
 #pragma unroll
   for (int t = 0; t < RW; ++t)
@@ -223,28 +227,40 @@ __global__ __launch_bounds__(NW * 64) void w8a8_ws_kernel(W8A8Params p) {
   wait_vmcnt<0>();
   wg_barrier_lds();  // every wave is done with the activation slots
 
-  // Reduce the KW waves of each channel group through LDS, one slice per round.
-  const bool owner = kw == 0;
+  // Reduce the KW waves of each channel group through LDS: every non-owner wave writes its
+  // slice into its own activation slot (up to NSLOT slices per round), then the owner adds
+  // them, so KW = 4 takes one round and two barriers.
   if constexpr (KW > 1) {
-    int32_t* red = reinterpret_cast<int32_t*>(lds_s0);  // one slice fits a slot
-    for (int q = 1; q < KW; ++q) {
-      if (kw == q) {
+    constexpr int PR = KW - 1 < NSLOT ? KW - 1 : NSLOT;  // slices per round
+    static_for<0, (KW - 1 + PR - 1) / PR>([&](auto rc) {
+      constexpr int q0 = 1 + decltype(rc)::value * PR;
+      static_for<0, PR>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        if (q0 + j < KW && kw == q0 + j) {
+          int32_t* red = reinterpret_cast<int32_t*>(slot_ptr(jc));
 #pragma unroll
-        for (int a = 0; a < RW; ++a)
+          for (int a = 0; a < RW; ++a)
 #pragma unroll
-          for (int u = 0; u < MT; ++u)
-            *reinterpret_cast<v4i*>(red + (u * 16 + r) * BN + cw * BNW + a * 16 + 4 * g) = acc[a][u];
-      }
+            for (int u = 0; u < MT; ++u)
+              *reinterpret_cast<v4i*>(red + (u * 16 + r) * BN + cw * BNW + a * 16 + 4 * g) = acc[a][u];
+        }
+      });
       wg_barrier_lds();
       if (owner) {
+        static_for<0, PR>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          if constexpr (q0 + j < KW) {
+            const int32_t* red = reinterpret_cast<const int32_t*>(slot_ptr(jc));
 #pragma unroll
-        for (int a = 0; a < RW; ++a)
+            for (int a = 0; a < RW; ++a)
 #pragma unroll
-          for (int u = 0; u < MT; ++u)
-            acc[a][u] += *reinterpret_cast<const v4i*>(red + (u * 16 + r) * BN + cw * BNW + a * 16 + 4 * g);
+              for (int u = 0; u < MT; ++u)
+                acc[a][u] += *reinterpret_cast<const v4i*>(red + (u * 16 + r) * BN + cw * BNW + a * 16 + 4 * g);
+          }
+        });
       }
-      wg_barrier_lds();
-    }
+      if constexpr (q0 + PR < KW) wg_barrier_lds();  // the next round reuses the slots
+    });
   }
 
   const int cidx = mc * p.n_tiles + tile;
@@ -255,7 +271,7 @@ __global__ __launch_bounds__(NW * 64) void w8a8_ws_kernel(W8A8Params p) {
 #pragma unroll
         for (int u = 0; u < MT; ++u) {
           const int m = m0 + u * 16 + r, n = n0 + a * 16 + 4 * g;
-          if (m < M && n < p.N) w8a8_store4(p, m, n, acc[a][u]);
+          if (m < M && n < p.N) w8a8_store4s(p, m, n, acc[a][u], es.a[u], es.w[a]);
         }
     }
     return;

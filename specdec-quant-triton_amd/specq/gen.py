@@ -60,6 +60,43 @@ def w8a8_acts(M: int, K: int, seed: int = 0, device="cpu"):
     return a.to(device), sa.to(device)
 
 
+def w8a8_epilogue_midpoints(M: int, N: int, seed: int = 0):
+    """W8A8 inputs on which rounding order shows: for every channel n, the output of token row
+    n % M is a case where fp16(fp32(fp32(acc * sa) * sw)) (the reference order, two
+    roundings) differs from the product acc * sa * sw rounded to fp16 once.
+
+    K = 64, W is all ones and row m of A sums to a chosen acc_m, so acc[m, n] = acc_m; the
+    channel scales are drawn from U[0.001, 0.01] and kept where the two orders disagree.
+    Returns (a int8 [M, 64], w int8 [N, 64], sa fp32 [M], sw fp32 [N], hit bool [M, N])."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    K = 64
+    acc = rng.integers(64, 127 * K + 1, size=M) * rng.choice(np.array([-1, 1]), size=M)
+    base = np.floor_divide(acc, K)  # in [-127, 127]; entries are base or base + 1 <= 127
+    rem = acc - base * K
+    a = np.repeat(base[:, None], K, axis=1)
+    a += (np.arange(K)[None, :] < rem[:, None])
+    sa = rng.uniform(0.005, 0.02, size=M).astype(np.float32)
+    sw = np.empty(N, dtype=np.float32)
+    for m in range(M):
+        cols = np.arange(m, N, M)
+        p1 = np.float32(acc[m]) * sa[m]
+        found = np.empty(0, dtype=np.float32)
+        while found.size < cols.size:
+            cand = rng.uniform(0.001, 0.01, size=1 << 18).astype(np.float32)
+            twice = (p1 * cand).astype(np.float16)
+            once = (np.float64(p1) * cand.astype(np.float64)).astype(np.float16)
+            found = np.concatenate([found, cand[twice != once]])
+        sw[cols] = found[:cols.size]
+    w = np.ones((N, K), dtype=np.int8)
+    p1 = acc.astype(np.float32)[:, None] * sa[:, None]
+    twice = (p1 * sw[None, :]).astype(np.float16)
+    once = (p1.astype(np.float64) * sw[None, :].astype(np.float64)).astype(np.float16)
+    return (torch.from_numpy(a.astype(np.int8)), torch.from_numpy(w), torch.from_numpy(sa),
+            torch.from_numpy(sw), torch.from_numpy(twice != once))
+
+
 def int4_weights(N: int, K: int, group: int = 128, seed: int = 0, device="cpu"):
     """(q unsigned nibbles uint8 [N,K] in 0..15, scales fp16 [N, K/group])."""
     g = _gen(seed)

@@ -91,6 +91,25 @@ def test_w8a8_split_k_and_tiles_bit_identical(split_k):
         assert_bitexact_fp16(out, ref, f"split_k={split_k} BLOCK_N={bn} warps={nw}")
 
 
+def test_w8a8_epilogue_fp32_rounding_order():
+    # Every channel has an output whose fp32 product sits on an fp16 rounding midpoint, so an
+    # epilogue that rounds the product to fp16 once (fused multiply-convert) fails here.  N is
+    # ragged, so the 4-channel vector stores and the per-channel edge stores are both covered.
+    N = 1003
+    note(f"w8a8 epilogue rounding order M=96 N={N} K=64")
+    a, w, sa, sw, hit = gen.w8a8_epilogue_midpoints(96, N, seed=7)
+    assert bool(hit.any(dim=0).all())
+    ref = O.w8a8(a.numpy(), sa.numpy(), w.numpy(), sw.numpy())
+    a, w, sa, sw = (t.to(DEV) for t in (a, w, sa, sw))
+    wp = K.pack_weight_int8(w)
+    for M in (16, 96):
+        for wt, bm, bn, nw, sk in ((w, None, None, 4, 0), (w, 16, 16, 4, 0), (w, 80, 64, 4, 0), (w, 96, 32, 4, 3),
+                                   (wp, None, None, 4, 0), (wp, 96, 128, 4, 0), (wp, 16, 16, 4, 2)):
+            out, ck = K.w8a8_matmul(a[:M], sa[:M], wt, sw, BLOCK_M=bm, BLOCK_N=bn, num_warps=nw, split_k=sk)
+            torch.cuda.synchronize()
+            assert_bitexact_fp16(out, ref[:M], f"M={M} BLOCK_M={bm} BLOCK_N={bn} sk={sk} ({ck.name})")
+
+
 @pytest.mark.parametrize("bn_nw", [(16, 4), (32, 4), (32, 2), (64, 4), (64, 2), (128, 4)])
 def test_w8a8_every_tile_shape_and_block_m(bn_nw):
     # Every channel-block shape of the aligned streaming paths at every BLOCK_M bucket,

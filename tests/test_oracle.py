@@ -71,6 +71,21 @@ def test_w8a8_epilogue_matches_torch_reference_order():
     assert not np.array_equal(other.view(np.uint16), ref.view(np.uint16))
 
 
+def test_w8a8_epilogue_rounds_through_fp32():
+    # Cases where the fp32 product lands on an fp16 rounding midpoint: the reference order
+    # rounds to fp32 and then to fp16; a single rounding of the exact product (what a fused
+    # multiply-convert does) differs on every marked element.
+    from specq import gen
+    a, w, sa, sw, hit = (t.numpy() for t in gen.w8a8_epilogue_midpoints(16, 160, seed=3))
+    assert hit.any(axis=0).all()
+    acc = O.w8a8_int32(a, w)
+    ref = ((torch.from_numpy(acc).float() * torch.from_numpy(sa)[:, None]) * torch.from_numpy(sw)[None, :]).half().numpy()
+    got = O.w8a8(a, sa, w, sw)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+    once = ((acc.astype(np.float32) * sa[:, None]).astype(np.float64) * sw[None, :].astype(np.float64)).astype(np.float16)
+    assert (got.view(np.uint16) != once.view(np.uint16))[hit].all()
+
+
 def test_w8a8_kat_single_term():
     a = np.zeros((1, 64), np.int8); a[0, 5] = 100
     w = np.zeros((2, 64), np.int8); w[1, 5] = -3
