@@ -1,21 +1,23 @@
 """Benchmark of the quantized verification path on one MI355X (prints one JSON line).
 
-Workload: W8A8 GEMMs over the seven Llama-3-8B-shaped linears
-(q, o 4096x4096; k, v 1024x4096; gate, up 14336x4096; down 4096x14336) at the verification
-batch M = B*(k+1) = 8*9 = 72.  One step is the linears of one verification forward: 32 layers
-x 7 GEMMs = 224 launches streaming 6.98 GB of distinct INT8 weights (far beyond the 256 MiB
-Infinity Cache, so every step reads its weights from HBM).  The step is captured once into a
-hipGraph (torch.cuda.graph over the C-ABI launches) and replayed; inputs are resident in HBM
-before the timed region starts.  Weights are packed once, at load time, into the kernel's
-MFMA-fragment layout (pack_weight_int8; bit-identical results); the same step on row-major
-weights (the reference's w_q layout) is reported in `detail`.
+Workload: W8A8 GEMMs over the reference's per-layer Llama-3-8B linears (bench_matmul.py:16:
+qkv 6144x4096, o 4096x4096, gate_up 28672x4096, down 4096x14336; the config-1 shapes fused as
+the reference benchmarks them) at the verification batch M = B*(k+1) = 8*9 = 72.  One step is
+the linears of one verification forward: 32 layers x 4 GEMMs = 128 launches streaming 6.98 GB
+of distinct INT8 weights (far beyond the 256 MiB Infinity Cache, so every step reads its
+weights from HBM).  The step is captured once into a hipGraph (torch.cuda.graph over the
+C-ABI launches) and replayed; inputs are resident in HBM before the timed region starts.
+Weights are packed once, at load time, into the kernel's MFMA-fragment layout
+(pack_weight_int8; bit-identical results); the same step on row-major weights (the
+reference's w_q layout) and on the seven unfused config-1 linears (q, k, v, o, gate, up, down)
+are reported in `detail`.
 
   value        algorithmic HBM bytes of a step / step time, in GB/s (whole job, one GPU)
-  roofline     the dominant kernel (the gate/up GEMM, 54% of the bytes): algorithmic bytes per
+  roofline     the dominant kernel (the gate_up GEMM, 54% of the bytes): algorithmic bytes per
                launch / its mean launch duration, measured with HIP events around a graph of
                back-to-back launches on the stream the kernels run on, against 8 TB/s
-  cpu_baseline the CPU oracle (oracle/oracle.py, numpy) on one layer's seven linears at the
-               same M, timed on the host cores for a bounded ~10 s sample
+  cpu_baseline the CPU oracle (oracle/oracle.py, numpy) on one layer's linears at the same M,
+               timed on the host cores for a bounded ~10 s sample
   detail       the k=0 decode step (M=8) on the same weights and the verify/decode ratio
                (target <= 1.1), W4A16 at M=72 and M=8 (load-time packed INT4, and the int32
                packing as given at M=72), INT8 paged verification attention at
@@ -40,8 +42,11 @@ for _p in (ROOT, PKG):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
-LINEARS = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
-           ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+# One layer's linears as the reference benchmarks them (bench_matmul.py:16), and unfused.
+LINEARS = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
+SPLIT_LINEARS = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+                 ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+DOMINANT = ("gate_up", 28672, 4096)
 METRIC = "GEMM µs & HBM GB/s vs M=B·(k+1); INT8 verify-attn µs at k=8; graph replay µs"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -101,16 +106,16 @@ def time_replays(g, steps: int, warmup: int) -> float:
     return e0.elapsed_time(e1) / steps
 
 
-def make_weights(K, L: int, seed: int = 0, packed: bool = True):
-    """L layers of the seven linears: int8 weights (packed MFMA fragments, or row-major) and
-    fp32 per-channel scales, on the GPU."""
+def make_weights(K, L: int, seed: int = 0, packed: bool = True, linears=LINEARS):
+    """L layers of the linears: int8 weights (packed MFMA fragments, or row-major) and fp32
+    per-channel scales, on the GPU."""
     import torch
 
     g = torch.Generator(device="cuda").manual_seed(seed)
     layers = []
     for _ in range(L):
         lw = {}
-        for name, N, Kd in LINEARS:
+        for name, N, Kd in linears:
             w = torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=g)
             sw = torch.rand((N,), device="cuda", generator=g) * 0.009 + 0.001
             lw[name] = (K.pack_weight_int8(w) if packed else w, sw)
@@ -120,12 +125,12 @@ def make_weights(K, L: int, seed: int = 0, packed: bool = True):
     return layers
 
 
-def w8a8_step_fn(K, layers, acts, M, outs):
+def w8a8_step_fn(K, layers, acts, M, outs, linears=LINEARS):
     a, sa, a_ff = acts[0][:M], acts[1][:M], acts[2][:M]
 
     def step():
         for lw in layers:
-            for name, N, Kd in LINEARS:
+            for name, N, Kd in linears:
                 w, sw = lw[name]
                 K.w8a8_matmul(a if Kd == a.shape[1] else a_ff, sa, w, sw, out=outs[N][:M], BLOCK_M=None)
     return step
@@ -142,7 +147,8 @@ def bench_w8a8(args, K, torch):
     a_ff = torch.randint(-127, 128, (M_max, 14336), dtype=torch.int8, device="cuda", generator=g)
     sa = torch.rand((M_max,), device="cuda", generator=g) * 0.015 + 0.005
     acts = (a, sa, a_ff)
-    outs = {N: torch.empty((M_max, N), dtype=torch.float16, device="cuda") for N in {n for _, n, _ in LINEARS}}
+    outs = {N: torch.empty((M_max, N), dtype=torch.float16, device="cuda")
+            for N in {n for _, n, _ in LINEARS + SPLIT_LINEARS}}
     res = {}
     for label, M in (("verify", args.B * (args.k + 1)), ("decode", args.B)):
         step = w8a8_step_fn(K, layers, acts, M, outs)
@@ -155,23 +161,22 @@ def bench_w8a8(args, K, torch):
         res[label] = dict(M=M, ms=ms, bytes=bytes_step, GBps=bytes_step / (ms * 1e-3) / 1e9)
         del graph
 
-    # Dominant kernel (gate/up shape): a graph of back-to-back launches over every layer's
-    # gate and up weights, timed with events on the stream the launches run on.
+    # Dominant kernel (gate_up shape): a graph of back-to-back launches over every layer's
+    # gate_up weights, timed with events on the stream the launches run on.
     M = res["verify"]["M"]
-    N, Kd = 14336, 4096
+    dname, N, Kd = DOMINANT
     outg = outs[N][:M]
 
     def dom():
         for lw in layers:
-            for name in ("gate", "up"):
-                K.w8a8_matmul(a[:M], sa[:M], *lw[name], out=outg, BLOCK_M=None)
+            K.w8a8_matmul(a[:M], sa[:M], *lw[dname], out=outg, BLOCK_M=None)
     dom()
     torch.cuda.synchronize()
     gdom = capture(dom)
-    launches = 2 * args.layers
-    ms = time_replays(gdom, max(5, args.steps // 2), 2)
+    launches = args.layers
+    ms = time_replays(gdom, max(5, args.steps), 2)
     us_launch = ms * 1e3 / launches
-    _, ck = K.w8a8_matmul(a[:M], sa[:M], *layers[0]["gate"], out=outg, BLOCK_M=None)
+    _, ck = K.w8a8_matmul(a[:M], sa[:M], *layers[0][dname], out=outg, BLOCK_M=None)
     dom_bytes = w8a8_bytes(M, N, Kd)
     res["dominant"] = dict(kernel=ck.name, M=M, N=N, K=Kd, us=us_launch, bytes=dom_bytes,
                            GBps=dom_bytes / (us_launch * 1e-6) / 1e9, config=ck.config)
@@ -188,11 +193,24 @@ def bench_w8a8(args, K, torch):
     res["verify_rowmajor"] = dict(M=M, ms=ms, GBps=res["verify"]["bytes"] / (ms * 1e-3) / 1e9)
     del graph, layers
     torch.cuda.empty_cache()
+    # The seven unfused config-1 linears (packed weights), verification and decode.
+    layers = make_weights(K, args.layers, seed=1, packed=True, linears=SPLIT_LINEARS)
+    for label, M in (("verify_split", args.B * (args.k + 1)), ("decode_split", args.B)):
+        step = w8a8_step_fn(K, layers, acts, M, outs, linears=SPLIT_LINEARS)
+        step()
+        torch.cuda.synchronize()
+        graph = capture(step)
+        ms = time_replays(graph, args.steps, args.warmup)
+        b = args.layers * sum(w8a8_bytes(M, N, Kd) for _, N, Kd in SPLIT_LINEARS)
+        res[label] = dict(M=M, ms=ms, GBps=b / (ms * 1e-3) / 1e9)
+        del graph
+    del layers
+    torch.cuda.empty_cache()
     return res
 
 
 def bench_w4a16(args, K, torch):
-    """W4A16 over the same seven linears, M = 72 and 8: INT4 weights (int32, 8 nibbles per word)
+    """W4A16 over the same per-layer linears, M = 72 and 8: INT4 weights (int32, 8 nibbles per word)
     packed once at load into MFMA fragments (pack_weight_int4), and the int32 weights as given
     for the verification step."""
     g = torch.Generator(device="cuda").manual_seed(3)
@@ -339,7 +357,7 @@ def bench_plan_graph(args, K, torch):
 
 
 def cpu_baseline(args, M: int, seconds: float):
-    """The CPU oracle (numpy) on one layer's seven linears at M, repeated for about `seconds`."""
+    """The CPU oracle (numpy) on one layer's linears at M, repeated for about `seconds`."""
     import numpy as np
 
     from oracle import oracle as O
@@ -364,7 +382,7 @@ def cpu_baseline(args, M: int, seconds: float):
         if el >= seconds or reps >= 50:
             break
     return dict(value=round(reps * b_layer / el / 1e9, 3), unit="GB/s", cores=int(cores), kind="port",
-                sample=f"oracle.w8a8 (numpy) on one layer's 7 Llama-3-8B linears at M={M}, {reps} reps "
+                sample=f"oracle.w8a8 (numpy) on one layer's Llama-3-8B linears (qkv, o, gate_up, down) at M={M}, {reps} reps "
                        f"in {el:.1f} s ({reps * b_layer / 1e9:.2f} GB of weights)")
 
 
@@ -415,6 +433,9 @@ def main() -> int:
               "w8a8_verify_rowmajor_weights": dict(M=vr["M"], ms=round(vr["ms"], 4), GBps=round(vr["GBps"], 1)),
               "w8a8_decode": dict(M=d["M"], ms=round(d["ms"], 4), GBps=round(d["GBps"], 1)),
               "w8a8_verify_over_decode": round(v["ms"] / d["ms"], 4),
+              "w8a8_verify_7_linears": {k: round(x, 4) for k, x in w["verify_split"].items()},
+              "w8a8_decode_7_linears": {k: round(x, 4) for k, x in w["decode_split"].items()},
+              "w8a8_verify_over_decode_7_linears": round(w["verify_split"]["ms"] / w["decode_split"]["ms"], 4),
               "dominant_kernel": dict(name=dom["kernel"], us=round(dom["us"], 3), **dom["config"])}
     if not args.no_detail:
         w4 = bench_w4a16(args, K, torch)
@@ -445,8 +466,8 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic",
-        "config": {"workload": f"W8A8 verification linears of Llama-3-8B: {args.layers} layers x 7 "
-                               f"(q,k,v,o,gate,up,down), M=B*(k+1)={M} (B={args.B}, k={args.k}), "
+        "config": {"workload": f"W8A8 verification linears of Llama-3-8B: {args.layers} layers x 4 "
+                               f"(qkv, o, gate_up, down as in bench_matmul.py), M=B*(k+1)={M} (B={args.B}, k={args.k}), "
                                f"weights packed at load, one hipGraph replay per step",
                    "M": M, "layers": args.layers, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -97,6 +97,37 @@ const void* ws_fn(int bnsel, int layout, int mt) {
 
 int bn_of_sel(int sel) { return 16 << sel; }
 int kw_of_sel(int sel) { return sel == 0 ? 4 : (sel == 1 ? 2 : 1); }  // waves splitting K
+
+// Channel block and split count of the LDS-staged kernel from a cost model fitted to measured
+// latencies of the Llama-3-8B linears (qkv, o, gate_up, down, gate, k/v at M = 24..288; mean
+// regret 0.6%, worst 5.5% against the best measured tile): a workgroup streams
+// (BN + rows) * K / splits bytes at ~50 GB/s per CU, all weights cross HBM at ~7 TB/s, and a
+// split costs ~2 us plus writing and reading its INT32 partial tiles at ~2 TB/s.  Shapes that
+// need more workgroups than CUs are left out (one workgroup per CU streams best).
+// `bnsel_fixed` >= 0 keeps the caller's BLOCK_N; `splits_fixed` > 0 keeps its split count.
+void ws_auto_tiles(int rows, int m_chunks, int N, int K, int bnsel_fixed, int splits_fixed, int* bnsel, int* splits) {
+  const int cus = device_cus();
+  const int mpad = ceil_div(rows, 16) * 16;
+  double best_t = 0;
+  int best_sel = -1, best_s = 1;
+  for (int pass = 0; pass < 2 && best_sel < 0; ++pass) {  // pass 1 only if nothing fits the CUs
+    for (int sel = 0; sel < 4; ++sel) {
+      if (bnsel_fixed >= 0 && sel != bnsel_fixed) continue;
+      const int bn = bn_of_sel(sel);
+      const int cand[3] = {splits_fixed > 0 ? splits_fixed : 1, 2, 4};
+      for (int ci = 0; ci < (splits_fixed > 0 ? 1 : 3); ++ci) {
+        const int s = cand[ci];
+        if (pass == 0 && (int64_t)ceil_div(N, bn) * s * m_chunks > cus) continue;
+        double t = std::max((double)(bn + rows) * K / s / 50e3, (double)N * K / 7e6);
+        if (s > 1) t += 2.0 + (double)s * mpad * N * 8 / 2e6;
+        if (pass == 1) t *= (double)ceil_div(ceil_div(N, bn) * s * m_chunks, cus);  // rounds of workgroups
+        if (best_sel < 0 || t < best_t) { best_t = t; best_sel = sel; best_s = s; }
+      }
+    }
+  }
+  *bnsel = best_sel;
+  *splits = best_s;
+}
 static_assert(W8A8BnSel<0>::KW == 4 && W8A8BnSel<1>::KW == 2 && W8A8BnSel<2>::KW == 1 && W8A8BnSel<3>::KW == 1,
               "kw_of_sel mirrors the tile table");
 
@@ -130,16 +161,25 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   else if (path == kWs && mt >= 2) family = kWs;
   else family = mt == 1 ? kRk : kWs;
 
-  int nw = 4, rw = 1, bnsel = 2;
+  int nw = 4, rw = 1, bnsel = 2, ws_splits = 1;
   const void* fn = nullptr;
   if (family == kRk || family == kWs) {
-    if (block_n > 0) {
-      bnsel = block_n == 16 ? 0 : (block_n == 32 ? 1 : (block_n == 64 ? 2 : 3));
+    const int want = block_n > 0 ? (block_n == 16 ? 0 : (block_n == 32 ? 1 : (block_n == 64 ? 2 : 3))) : -1;
+    if (family == kWs) {
+      // With a plan the grid is sized for the largest M, but usually one M-chunk is active.
+      const int rows = std::min(std::max(m_grid, 1), mt * 16);
+      const int chunks = plan_mode ? 1 : ceil_div(std::max(m_grid, 1), mt * 16);
+      ws_auto_tiles(rows, chunks, N, K, want, split_k, &bnsel, &ws_splits);
+    } else if (want >= 0) {
+      bnsel = want;
     } else {
-      // Measured on the Llama-3-8B linears: wide N fills the CUs with 64-channel tiles whose 4
-      // waves share each activation fragment; narrower N gets 16-channel tiles (4 times the
-      // workgroups) whose waves split K.
-      bnsel = ceil_div(N, 64) >= 192 ? 2 : 0;
+      // Measured on the Llama-3-8B linears at M = 1..16: the narrowest channel block whose
+      // workgroups fit the CUs in one round streams best (16 channels for o/down/k/v, 32 for
+      // qkv, 64 for gate, 128 for the fused gate_up), without splitting K.
+      const int chunks = ceil_div(std::max(m_grid, 1), 16);
+      bnsel = 3;
+      for (int sel = 0; sel < 3; ++sel)
+        if ((int64_t)ceil_div(N, bn_of_sel(sel)) * chunks <= device_cus()) { bnsel = sel; break; }
     }
     if (family == kRk) {
       if (mt > 1) {
@@ -188,9 +228,8 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
     splits = 4 * base >= 3 * target ? 1 : ceil_div(target, base);
     const int max_splits = std::max(1, ksteps / (2 * nw));
     splits = std::min(splits, max_splits);
-  } else if (family == kWs && bnsel == 0 && cfg->n_tiles * cfg->m_chunks < 128) {
-    // Few 16-channel tiles (e.g. the 1024-wide k/v projections): split K up to 4 ways.
-    splits = std::min(4, std::max(1, 256 / (cfg->n_tiles * cfg->m_chunks)));
+  } else if (family == kWs) {
+    splits = ws_splits;
   } else {
     splits = 1;
   }
@@ -280,7 +319,7 @@ int w8a8_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, i
   if (cfg.family == kRk) {
     snprintf(out->name, sizeof(out->name), "specq::w8a8_rk_kernel<1, %d, %d, 4, %d>", rw, kw, cfg.layout);
   } else if (cfg.family == kWs) {
-    const int nslot = w8a8_ws_nslot(cfg.mt, rw);
+    const int nslot = w8a8_ws_nslot(cfg.mt, kw);
     snprintf(out->name, sizeof(out->name), "specq::w8a8_ws_kernel<%d, %d, %d, %d, %d, 4, %d>", cfg.mt, rw, kw, s,
              nslot, cfg.layout);
   } else {

@@ -134,24 +134,54 @@ __device__ __forceinline__ void w8a8_publish_quad(rsrc_t prs, int split, int ml,
   publish16(prs, (uint32_t)(((split * BM + ml) * BN + nl) * 4), v);
 }
 // Called by every thread after its publishes: the last workgroup of the tile to arrive sums
-// the splits (all of a quad's loads in flight together) and applies the epilogue.
-template <int BM, int BN>
+// the splits and applies the epilogue.  Thread t owns quads t, t + NT, ...; the scales and
+// the partials of up to QG quads x SB splits are loaded together, so the sum costs one
+// memory round trip per group instead of one per quad (INT32 sums are order independent).
+template <int BM, int BN, int NT>
 __device__ __forceinline__ void w8a8_splitk_finish(const W8A8Params& p, rsrc_t prs, int cidx, int m0, int nbase,
                                                    int M, int* s_last) {
   if (!arrive_last(p.counters + cidx, p.splits, s_last)) return;
   constexpr int QUADS = BM * BN / 4;
-  for (int q = threadIdx.x; q < QUADS; q += blockDim.x) {
-    const int ml = q / (BN / 4), nl = (q % (BN / 4)) * 4;
-    v4i s = {0, 0, 0, 0};
-    for (int sp0 = 0; sp0 < p.splits; sp0 += 4) {
-      v4i t[4];
+  constexpr int QPT = (QUADS + NT - 1) / NT;                   // quads per thread
+  constexpr int QG = QPT < 4 ? QPT : 4;                        // quads summed together
+  constexpr int SB = 16 / QG > 8 ? 8 : 16 / QG;                // splits loaded together
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        t[u] = collect16(prs, oob_unless(sp0 + u < p.splits, (uint32_t)((((sp0 + u) * BM + ml) * BN + nl) * 4)));
-      s += (t[0] + t[1]) + (t[2] + t[3]);
+  for (int g0 = 0; g0 < QPT; g0 += QG) {
+    int ml[QG], nl[QG];
+    bool ok[QG];
+    float a[QG], w[QG][4];
+#pragma unroll
+    for (int i = 0; i < QG; ++i) {
+      const int q = (int)threadIdx.x + (g0 + i) * NT;
+      ml[i] = q / (BN / 4);
+      nl[i] = (q % (BN / 4)) * 4;
+      const int m = m0 + ml[i], n = nbase + nl[i];
+      ok[i] = (g0 + i < QPT) & (q < QUADS) & (m < M) & (n < p.N);
+      // Indices clamped into range (the values of lanes that do not store are unused), so
+      // the loads need no branch and no extra buffer descriptors.
+      a[i] = p.sa[ok[i] ? m : m0];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) w[i][c] = p.sw[min(ok[i] ? n + c : nbase, p.N - 1)];
     }
-    const int m = m0 + ml, n = nbase + nl;
-    if (m < M && n < p.N) w8a8_store4(p, m, n, s);
+    v4i s[QG];
+#pragma unroll
+    for (int i = 0; i < QG; ++i) s[i] = v4i{0, 0, 0, 0};
+    for (int sp0 = 0; sp0 < p.splits; sp0 += SB) {
+      v4i t[QG][SB];
+#pragma unroll
+      for (int i = 0; i < QG; ++i)
+#pragma unroll
+        for (int u = 0; u < SB; ++u)
+          t[i][u] = collect16(prs, oob_unless(ok[i] & (sp0 + u < p.splits),
+                                              (uint32_t)((((sp0 + u) * BM + ml[i]) * BN + nl[i]) * 4)));
+#pragma unroll
+      for (int i = 0; i < QG; ++i)
+#pragma unroll
+        for (int u = 0; u < SB; ++u) s[i] += t[i][u];
+    }
+#pragma unroll
+    for (int i = 0; i < QG; ++i)
+      if (ok[i]) w8a8_store4s(p, m0 + ml[i], nbase + nl[i], s[i], a[i], w[i]);
   }
 }
 

@@ -201,7 +201,7 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
         w8a8_publish_quad<BM, BN>(prs, split, j * 16 + r, cw * BNW + a * 16 + 4 * g, acc[a][j]);
   }
   __shared__ int s_last_rk;
-  w8a8_splitk_finish<BM, BN>(p, prs, cidx, m0, tile * BN, M, &s_last_rk);
+  w8a8_splitk_finish<BM, BN, NW * 64>(p, prs, cidx, m0, tile * BN, M, &s_last_rk);
 }
 
 }  // namespace specq

@@ -6,8 +6,10 @@
 //   32  -> 2 x 16 channels, K split 2 ways                                    (KW = 2)
 //   64  -> 4 x 16 channels, the waves walk the same K steps                   (KW = 1)
 //   128 -> 4 x 32 channels                                                     (KW = 1, RW = 2)
-// The ws kernel's activation ring holds 4 chunks up to 144 token rows and 2 beyond; a chunk
-// covers 256 bytes of K (S K steps of each of the KW waves).
+// A chunk of the ws kernel's activation ring covers 256 bytes of K (S K steps of each of the KW
+// waves).  The ring holds 2 chunks, or 4 for the K-splitting tiles (16 and 32 channels) up to
+// 96 token rows: measured on the Llama-3-8B linears, deeper rings only add queueing once a
+// chunk carries 4 K steps per wave or the token tile is deep.
 #pragma once
 #include "w8a8_rk.hpp"
 #include "w8a8_ws.hpp"
@@ -23,13 +25,13 @@ struct W8A8BnSel {
   static constexpr int S = 4 / KW;  // K steps per wave per 256-byte chunk
 };
 
-// Ring slots of the ws kernel's activation chunks for a token depth and channel width.
-constexpr int w8a8_ws_nslot(int mt, int rw) { return (mt <= 9 && !(rw == 2 && mt >= 8)) ? 4 : 2; }
+// Ring slots of the ws kernel's activation chunks for a token depth and channel-block shape.
+constexpr int w8a8_ws_nslot(int mt, int kw) { return (kw >= 2 && mt <= 6) ? 4 : 2; }
 
 template <int MT, int BNSEL>
 struct W8A8WsPick {
   using B = W8A8BnSel<BNSEL>;
-  static constexpr int NSLOT = w8a8_ws_nslot(MT, B::RW);
+  static constexpr int NSLOT = w8a8_ws_nslot(MT, B::KW);
   using Cfg = W8A8WsCfg<MT, B::RW, B::KW, B::S, NSLOT, 4>;
 };
 

@@ -285,7 +285,7 @@ __global__ __launch_bounds__(NW * 64) void w8a8_ws_kernel(W8A8Params p) {
         w8a8_publish_quad<BM, BN>(prs, split, u * 16 + r, cw * BNW + a * 16 + 4 * g, acc[a][u]);
   }
   __shared__ int s_last_ws;
-  w8a8_splitk_finish<BM, BN>(p, prs, cidx, m0, tile * BN, M, &s_last_ws);
+  w8a8_splitk_finish<BM, BN, NW * 64>(p, prs, cidx, m0, tile * BN, M, &s_last_ws);
 }
 
 }  // namespace specq

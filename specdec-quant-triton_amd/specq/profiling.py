@@ -2,8 +2,8 @@
 
 Subcommands (run from the repository root):
 
-  probe   the workload of the `--pmc` passes: the dominant W8A8 kernel (gate/up shape,
-          N=14336, K=4096, packed weights) at M, launched once per layer over `--layers`
+  probe   the workload of the `--pmc` passes: the dominant W8A8 kernel (fused gate_up shape,
+          N=28672, K=4096, packed weights) at M, launched once per layer over `--layers`
           layers so every launch reads its weight from HBM, then a plain elementwise copy
           (torch.neg on int32, reads and writes `--copy-mib` MiB) as the calibration kernel.
   stats   a markdown table of a `--kernel-trace` run: dispatches grouped by kernel and grid,
@@ -42,7 +42,7 @@ def probe(args) -> int:
 
     torch.cuda.set_device(0)
     g = torch.Generator(device="cuda").manual_seed(1)
-    N, Kd, M = 14336, 4096, args.M
+    N, Kd, M = 28672, 4096, args.M
     layers = []
     for _ in range(args.layers):
         w = torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=g)
