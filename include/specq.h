@@ -62,7 +62,8 @@ const char* specq_last_error(void);
  *   plan     NULL, or device int32*: plan[0] = active M (kernels.py:35-38)
  *   block_m  token rows per workgroup: a multiple of 16, at most 304 (the reference's
  *            BLOCK_M; 16/32/64/128 are its values); 0 = one chunk covering M.
- *   block_n  output channels per workgroup: 16, 32, 64 or 128; 0 = auto.  (BLOCK_N)
+ *   block_n  output channels per workgroup: 16, 32, 64 or 128; 0 = auto (chosen with split_k
+ *            from M, N and K by a cost model fitted to measured latencies).  (BLOCK_N)
  *   num_warps  waves per workgroup of the byte-granular fallback kernel (unaligned operands):
  *            1, 2 or 4 (8 is taken as 4); 0 = 4.  The streaming kernels always run 4 waves.
  *   split_k  workgroups splitting K; 0 = auto.  The INT32 result does not depend on it.

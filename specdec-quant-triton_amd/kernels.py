@@ -24,8 +24,9 @@ reference) restate the reference formulas in torch and run on any device.
 Differences a caller may notice:
   * BLOCK_K and num_stages are accepted and ignored (the MFMA K step and register
     pipelining are fixed per kernel).  BLOCK_M=None (or 0) picks the tile from the measured
-    M staircase; BLOCK_N defaults to None (the channel width is then picked from N; the
-    reference's default is 64).  Every tile choice gives bit-identical results.  W8A8 BLOCK_M
+    M staircase; BLOCK_N defaults to None (the channel width and split-K are then picked
+    from M, N and K by a cost model fitted to measured latencies; the reference's default
+    is 64).  Every tile choice gives bit-identical results.  W8A8 BLOCK_M
     is at most 304; BLOCK_N is 16/32/64/128 channels per workgroup (larger values are taken as
     128); W4A16 BLOCK_N is 64 or 128.
   * w8a8_matmul also accepts a PackedWeightInt8 (pack_weight_int8), the weight pre-packed
