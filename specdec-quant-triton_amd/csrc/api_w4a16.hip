@@ -62,12 +62,17 @@ struct W4Cfg {
 // order never depends on M, the token tile or the plan.  Wide N already fills the CUs with
 // 64-channel tiles; narrower N is split along K into about 256 workgroups, each at least 4
 // blocks (512 K) long.
+// Split count of the K range, a function of (N, K) only so that the fp32 summation order (and
+// with it every result) is the same for every M, tile and plan mode.  Measured on the
+// Llama-3-8B linears (qkv, o, gate_up, down, gate, k/v at M = 8..288): the most splits, a
+// power of two, that keep the 64-channel tiles x splits within one workgroup per CU and at
+// least 8 K blocks (1024 of K) per split; two rounds of workgroups or shorter splits lose.
 int w4_auto_splits(int N, int nblocks) {
   const int tiles64 = ceil_div(N, 64);
-  if (tiles64 >= 192) return 1;
-  int splits = ceil_div(256, tiles64);
-  const int cap = nblocks / 4 > 0 ? nblocks / 4 : 1;
-  return splits < cap ? splits : cap;
+  const int cus = device_cus();
+  int splits = 1;
+  while (tiles64 * splits * 2 <= cus && nblocks / (splits * 2) >= 8) splits *= 2;
+  return splits;
 }
 
 int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, int split_k, bool plan_mode,
@@ -93,6 +98,8 @@ int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, in
   if (block_n > 0) {
     SPECQ_REQUIRE(block_n == 64 || block_n == 128, SPECQ_ENOTSUP, "w4a16: BLOCK_N=%d must be 64 or 128", block_n);
     rw = block_n / 64;
+  } else if (ceil_div(N, 64) > device_cus()) {
+    rw = 2;  // 128-channel blocks keep wide N (the fused gate_up) to one workgroup per CU
   }
   // The LDS-staged kernel is the default at every depth (measured faster than the register
   // stream even for 16-row tiles on the Llama-3-8B linears); the register stream stays
