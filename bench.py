@@ -20,8 +20,10 @@ are reported in `detail`.
                timed on the host cores for a bounded ~10 s sample
   detail       the k=0 decode step (M=8) on the same weights and the verify/decode ratio
                (target <= 1.1), W4A16 at M=72 and M=8 (load-time packed INT4, and the int32
-               packing as given at M=72), INT8 paged verification attention at
-               B=8, k=8, and the plan-buffer graph replay of the config-4 stack
+               packing as given at M=72), W4A8 at M=72 and M=8 (packed INT4 weights on the
+               INT8 MFMA path), INT8 paged verification attention at B=8, k=8, the paged
+               KV-cache append of the k+1 new tokens, and the plan-buffer graph replay of the
+               config-4 stack
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-detail]
 """
@@ -68,6 +70,11 @@ def attn_bytes(B: int, L: int, q_len: int, H: int, H_KV: int, D: int, scale_byte
     """K/V int8 + their scales for every context token, q in + out (fp16), block table, lengths."""
     return (B * L * H_KV * (2 * D + 2 * scale_bytes) + 4 * B * q_len * H * D
             + 4 * B * ((L + page - 1) // page) + 4 * B)
+
+
+def kv_append_bytes(B: int, q_len: int, H_KV: int, D: int, scale_bytes: int) -> int:
+    """New K and V rows read (fp16), int8 rows and scales written, block-table entry and length read."""
+    return B * q_len * H_KV * 2 * (2 * D + D + scale_bytes) + 4 * B * q_len + 4 * B
 
 
 # ------------------------------------------------------------------------------------------
@@ -248,6 +255,48 @@ def bench_w4a16(args, K, torch):
     return res
 
 
+def w4a8_bytes(M: int, N: int, K: int) -> int:
+    """Algorithmic HBM bytes of one W4A8 call: packed INT4 W, A, sa, sw read once, C written once."""
+    return N * K // 2 + M * K + 4 * M + 4 * N + 2 * M * N
+
+
+def bench_w4a8(args, K, torch):
+    """W4A8 (INT4 weights on the INT8 MFMA path, per-channel scale) over the same per-layer
+    linears, M = 72 and 8, weights packed once at load (pack_weight_w4a8)."""
+    g = torch.Generator(device="cuda").manual_seed(4)
+    layers = []
+    for _ in range(args.layers):
+        lw = {}
+        for name, N, Kd in LINEARS:
+            wp = torch.randint(0, 256, (N, Kd // 2), dtype=torch.uint8, device="cuda", generator=g)
+            sw = torch.rand((N,), device="cuda", generator=g) * 0.009 + 0.001
+            lw[name] = (K.pack_weight_w4a8(wp), sw)
+            del wp
+        layers.append(lw)
+    a = torch.randint(-127, 128, (300, 4096), dtype=torch.int8, device="cuda", generator=g)
+    a_ff = torch.randint(-127, 128, (300, 14336), dtype=torch.int8, device="cuda", generator=g)
+    sa = torch.rand((300,), device="cuda", generator=g) * 0.015 + 0.005
+    outs = {N: torch.empty((300, N), dtype=torch.float16, device="cuda") for N in {n for _, n, _ in LINEARS}}
+    res = {}
+    for label, M in (("verify", args.B * (args.k + 1)), ("decode", args.B)):
+        def step():
+            for lw in layers:
+                for name, N, Kd in LINEARS:
+                    K.w4a8_matmul(a[:M] if Kd == 4096 else a_ff[:M], sa[:M], *lw[name], out=outs[N][:M],
+                                  BLOCK_M=None)
+        step()
+        torch.cuda.synchronize()
+        graph = capture(step)
+        log(f"w4a8 {label} M={M}")
+        ms = time_replays(graph, args.steps, args.warmup)
+        b = args.layers * sum(w4a8_bytes(M, N, Kd) for _, N, Kd in LINEARS)
+        res[label] = dict(M=M, ms=ms, GBps=b / (ms * 1e-3) / 1e9)
+        del graph
+    del layers
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_attention(args, K, torch):
     """INT8 paged verification attention (config 3): B=8, k=8, context 4096, fused vs QPP=1."""
     from specq import gen
@@ -267,6 +316,18 @@ def bench_attention(args, K, torch):
             ms = do_bench(fn, warmup=5, rep=20)
             res[f"ctx{ctx}_{name}"] = dict(us=ms * 1e3, GBps=b / (ms * 1e-3) / 1e9)
         log(f"attention ctx={ctx}: fused {res[f'ctx{ctx}_fused']['us']:.1f} us")
+    # The step before attention: the k+1 new tokens' K/V quantised into the cache pages.
+    for B in (args.B, 32):
+        L = 4096 + ql
+        kc, vc, ks, vs, bt, cl = (t.cuda() for t in gen.paged_kv(B, [L] * B, H_KV, D, seed=7))
+        g = torch.Generator().manual_seed(8)
+        kn = torch.randn((B, ql, H_KV, D), generator=g).half().cuda()
+        vn = torch.randn((B, ql, H_KV, D), generator=g).half().cuda()
+        fn = lambda: K.paged_kv_append(kn, vn, kc, vc, ks, vs, bt, cl, ql)  # noqa: E731
+        ms = do_bench(fn, warmup=5, rep=50)
+        b = kv_append_bytes(B, ql, H_KV, D, 4)
+        res[f"kv_append_B{B}"] = dict(us=ms * 1e3, GBps=b / (ms * 1e-3) / 1e9)
+    log(f"kv append B={args.B}: {res[f'kv_append_B{args.B}']['us']:.1f} us")
     return res
 
 
@@ -444,8 +505,15 @@ def main() -> int:
         detail["w4a16_verify_int32_weights"] = {k: round(x, 4) for k, x in w4["verify_int32"].items()}
         detail["w4a16_verify_over_decode"] = round(w4["verify"]["ms"] / w4["decode"]["ms"], 4)
         detail["w4a16_verify_over_w8a8_decode"] = round(w4["verify"]["ms"] / d["ms"], 4)
+        w48 = bench_w4a8(args, K, torch)
+        detail["w4a8_verify"] = {k: round(x, 4) for k, x in w48["verify"].items()}
+        detail["w4a8_decode"] = {k: round(x, 4) for k, x in w48["decode"].items()}
+        detail["w4a8_verify_over_decode"] = round(w48["verify"]["ms"] / w48["decode"]["ms"], 4)
+        attn = bench_attention(args, K, torch)
         detail["attention_B8_k8"] = {k: {kk: round(x, 2) for kk, x in r.items()}
-                                     for k, r in bench_attention(args, K, torch).items()}
+                                     for k, r in attn.items() if not k.startswith("kv_append")}
+        detail["kv_append_k8"] = {k: {kk: round(x, 2) for kk, x in r.items()}
+                                  for k, r in attn.items() if k.startswith("kv_append")}
         detail["plan_graph_4layer"] = {k: round(x, 4) for k, x in bench_plan_graph(args, K, torch).items()}
 
     cpu = None

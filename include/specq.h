@@ -94,6 +94,33 @@ int specq_w8a8_packed(const int8_t* a, int64_t lda, const void* w_packed,
                       int block_m, int block_n, int num_warps, int split_k,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * W4A8 GEMM: C[m, n] = fp16( (float(sum_k A[m,k] * q[n,k]) * sa[m]) * sw[n] ) with q the
+ * signed INT4 weight in [-8, 7] and a per-channel fp32 scale sw, so the INT4 weights run on
+ * the INT8 MFMA path and their scale moves to the W8A8 epilogue (the reference's
+ * recommendation for INT4, REPORT.md:156; it has no W4A8 kernel).  The INT32 sums are exact,
+ * so results are bit-identical to specq_w8a8 on the unpacked weight q.
+ *   The weight is packed once at load from the reference INT4 packing (wq_layout 0: uint8
+ *   [N, K/2], byte j of a row holding k = j in its low and k = j + K/2 in its high nibble,
+ *   kernels.py:143-145; or wq_layout 1: int32 [N, K/8], nibble i of word j holding k = 8j + i;
+ *   nibbles carry offset 8) into 512-byte fragments stored K-step-major: fragment (s, t) of
+ *   64-wide K step s and 16-row tile t at (s * ceil(N/16) + t) * 512; lane l's dword d, byte i
+ *   holds the two's-complement nibbles of w[16t + l%16][64s + 16*(l/16) + 8d + i] (low) and
+ *   [... + 8d + 4 + i] (high), zero-padded.  specq_w4a8_packed_bytes() bytes.
+ *   Activations as specq_w8a8_packed (16-byte aligned rows, K % 16 == 0); K <= 131072.
+ *   Tiles, plan mode and workspace as specq_w8a8_packed.
+ * ------------------------------------------------------------------------------------- */
+size_t specq_w4a8_packed_bytes(int N, int K);
+int specq_w4a8_pack_weight(const void* wq, int64_t ldq, int wq_layout, int N, int K, void* packed,
+                           void* stream);
+size_t specq_w4a8_packed_workspace_size(int m_grid, int N, int K, int block_m, int block_n,
+                                        int num_warps, int split_k);
+int specq_w4a8_packed(const int8_t* a, int64_t lda, const void* w_packed,
+                      const float* sa, const float* sw, void* c, int64_t ldc,
+                      int M, int N, int K, int grid_m_max, const int32_t* plan,
+                      int block_m, int block_n, int num_warps, int split_k,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
 /* Tuning options.  "w8a8_path": W8A8 kernel family, 0 = automatic, 1 = direct-activation
  * streaming kernel (16-row token tiles), 2 = streaming with LDS-staged activations (tiles of
  * 32 rows or more; 16-row requests use family 1), 3 = byte-granular register kernel
@@ -175,6 +202,30 @@ int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64_t s_qh,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Paged INT8 KV-cache append: quantises the q_len new tokens' K and V into the cache pages
+ * that specq_paged_attn reads.  Token i of sequence b lands at position
+ * pos = ctx_len[b] - q_len + i (ctx_len already counts the new tokens), page
+ * block_tbl[b, pos / PAGE], slot pos % PAGE.  Each (token, KV head) row is quantised as the
+ * reference builds its cache (make_paged_kv's q8, kernels.py:280-284):
+ * s = max(amax |x|, 1e-8) / 127 in fp32, q = clamp(rne(x / s), -127, 127), s stored as fp16
+ * (RNE) or fp32.  Replaces the host-side q8 of make_paged_kv (kernels.py:265-286) with the
+ * on-device step that runs before attention in a serving loop.
+ *   k_new, v_new  fp16 [B_grid, ql_grid, H_KV, D], shared strides s_nb, s_nt, s_nh
+ *                 (rows 16-byte aligned)
+ *   kc, vc, ks, vs, block_tbl, ctx_len  as specq_paged_attn (cache rows 8-byte aligned);
+ *                 n_pages = pages in the pool (rows naming a page outside [0, n_pages), or a
+ *                 position outside [0, max_pages * PAGE), are skipped)
+ *   plan     NULL, or device int32*: plan[0] = n_seqs, plan[1] = q_len (as specq_paged_attn)
+ *   D must be 64, 128 or 256.  Slots of inactive sequences and tokens are never written.
+ * ------------------------------------------------------------------------------------- */
+int specq_kv_append_int8(const void* k_new, const void* v_new, int64_t s_nb, int64_t s_nt, int64_t s_nh,
+                         int8_t* kc, int8_t* vc, int64_t s_kp, int64_t s_ko, int64_t s_kh,
+                         void* ks, void* vs, int64_t s_sp, int64_t s_so, int64_t s_sh, int scale_fp32,
+                         const int32_t* block_tbl, int64_t s_bt, int max_pages, int n_pages,
+                         const int32_t* ctx_len, int B_grid, int n_seqs, int q_len, int ql_grid,
+                         int H_KV, int D, int PAGE, const int32_t* plan, void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * Elementwise steps around the GEMMs of a verification layer.
  * specq_silu_mul: h[m, n] = fp16( silu(float(gate[m,n])) * float(up[m,n]) ), m < M.
  *   No reference counterpart (the reference's graph stack has no MLP activation,
@@ -197,7 +248,8 @@ int specq_silu_mul_quant_int8(const void* gate, int64_t ld_gate, const void* up,
 /* ---------------------------------------------------------------------------------------
  * Resource usage of the kernel a call with these arguments would launch (the reference's
  * compiled-kernel metadata ck.n_regs / ck.n_spills / ck.metadata.shared, regs.py:29-32).
- * kind: 0 = W8A8 (weight layout in `variant`: 0 row-major, 1 packed), 1 = W4A16 (layout in
+ * kind: 0 = W8A8 (weight layout in `variant`: 0 row-major, 1 packed, 2 the packed INT4 weight
+ * of W4A8), 1 = W4A16 (layout in
  * `variant`), 2 = paged attention (D in `variant`).  For the GEMMs, `variant` | 16 describes a
  * call made with a plan (m_grid is then grid_m_max).
  * ------------------------------------------------------------------------------------- */

@@ -27,6 +27,8 @@ __all__ = [
     "dequant_int4", "w4a16",
     "paged_attention",
     "silu_mul", "silu_mul_quant_int8",
+    "paged_kv_append",
+    "quantize_weight_int4_channel", "w4a8",
 ]
 
 
@@ -206,3 +208,58 @@ def silu_mul(gate, up) -> np.ndarray:
 def silu_mul_quant_int8(h_fp16) -> tuple:
     """Quantisation of an fp16 activation row block (kernels.py:58-62 applied to h)."""
     return quantize_rows_int8(np.asarray(h_fp16, np.float16))
+
+
+# ------------------------------------------------------------------------------------------
+# Paged INT8 KV-cache append (kernels.py:265-286: the q8 of make_paged_kv, applied to the
+# new tokens and scattered through the block table)
+# ------------------------------------------------------------------------------------------
+def paged_kv_append(k_new, v_new, kc, vc, ks, vs, block_tbl, ctx_len, q_len: int, n_seqs=None) -> tuple:
+    """Copies of (kc, vc, ks, vs) with the q_len new tokens of each sequence written in.
+
+    Token i of sequence b goes to position pos = ctx_len[b] - q_len + i (ctx_len counts the
+    new tokens, kernels.py:173), page block_tbl[b, pos // PAGE], slot pos % PAGE.  Each
+    (token, head) row of D values is quantised as q8 does (kernels.py:280-283):
+    s = max(amax |x|, 1e-8) / 127 in fp32, q = clamp(rne(x / s), -127, 127), and s is stored
+    in the scale tensor's dtype (fp16 as kernels.py:283 returns it, or fp32).  Rows whose
+    position or page falls outside the cache are skipped.
+    """
+    kc, vc = np.array(kc, dtype=np.int8), np.array(vc, dtype=np.int8)
+    ks, vs = np.array(ks), np.array(vs)
+    bt = np.asarray(block_tbl, dtype=np.int64)
+    cl = np.asarray(ctx_len, dtype=np.int64)
+    B = bt.shape[0] if n_seqs is None else int(n_seqs)
+    PAGE, max_pages, n_pages = kc.shape[1], bt.shape[1], kc.shape[0]
+    for src, cache, scales in ((k_new, kc, ks), (v_new, vc, vs)):
+        x = np.asarray(src, dtype=np.float16)
+        for b in range(B):
+            for i in range(q_len):
+                pos = int(cl[b]) - q_len + i
+                if pos < 0 or pos // PAGE >= max_pages:
+                    continue
+                page = int(bt[b, pos // PAGE])
+                if page < 0 or page >= n_pages:
+                    continue
+                q, s = quantize_rows_int8(x[b, i])          # rows = heads, [H_KV, D]
+                cache[page, pos % PAGE] = q
+                scales[page, pos % PAGE] = s.astype(scales.dtype)
+    return kc, vc, ks, vs
+
+
+# ------------------------------------------------------------------------------------------
+# W4A8: INT4 weights with a per-channel scale on the W8A8 arithmetic (the INT4 packing of
+# kernels.py:138-147 at one group per row; the epilogue of kernels.py:51-55)
+# ------------------------------------------------------------------------------------------
+def quantize_weight_int4_channel(w) -> tuple:
+    """(unsigned nibbles [N, K], scale fp32 [N]): sc = max(amax_row, 1e-8) / 7 in fp32,
+    q = clamp(rne(w / sc), -8, 7) + 8 -- kernels.py:140-142 with the group spanning the row."""
+    w = np.asarray(w).astype(np.float32)
+    sc = (np.maximum(np.abs(w).max(-1), np.float32(1e-8)) / np.float32(7.0)).astype(np.float32)
+    q = np.clip(np.rint(w / sc[:, None]), -8, 7).astype(np.int16) + 8
+    return q.astype(np.uint8), sc
+
+
+def w4a8(a, sa, qu, sw) -> np.ndarray:
+    """fp16((fp32(sum_k a[m,k] * (q[n,k] - 8)) * sa[m]) * sw[n]): W8A8 on the unpacked INT4 weight."""
+    q = (np.asarray(qu, dtype=np.int16) - 8).astype(np.int8)
+    return w8a8(a, sa, q, sw)

@@ -6,7 +6,9 @@
 //   WS      weight streaming with LDS-staged activations (w8a8_ws.hpp) for deeper token tiles.
 //   LEGACY  register-pipelined kernel with 16/8/4/1-byte loads (w8a8.hpp): any alignment.
 // RK and WS read the row-major weight or the packed K-step-major fragments and need 16-byte
-// aligned activation rows.
+// aligned activation rows.  Weight layout 2 is the packed INT4 weight of W4A8 (INT4 weights on
+// the INT8 MFMA path with a per-channel scale in the epilogue), served by the RK and WS
+// families with the same tiles.
 #include <algorithm>
 #include <atomic>
 
@@ -47,6 +49,43 @@ __global__ __launch_bounds__(256) void w8a8_pack_kernel(const int8_t* __restrict
   *reinterpret_cast<v4i*>(out + frag * 1024 + l * 16) = v4i{w4[0], w4[1], w4[2], w4[3]};
 }
 
+// Packs an INT4 weight (reference uint8 layout 0 or int32 layout 1, nibbles with offset 8) into
+// the W4A8 fragments: fragment (s, t) of 64-wide K step s and 16-row tile t is the 512 bytes at
+// (s * ntiles + t) * 512; lane l's dword d, byte i holds the two's-complement nibbles of
+// w[16t + l%16][64s + 16*(l/16) + 8d + i] (low) and [... + 8d + 4 + i] (high), zero past N or K.
+__global__ __launch_bounds__(256) void w4a8_pack_kernel(const uint8_t* __restrict__ q, int64_t ldq, int layout, int N,
+                                                        int K, int8_t* __restrict__ out) {
+  const int ksteps = (K + 63) / 64;
+  const int ntiles = (N + 15) / 16;
+  const int64_t frag = blockIdx.x * 4 + (threadIdx.x >> 6);  // one wave per fragment
+  if (frag >= (int64_t)ntiles * ksteps) return;
+  const int s = (int)(frag / ntiles), t = (int)(frag % ntiles);
+  const int l = threadIdx.x & 63;
+  const int row = 16 * t + (l & 15), k0 = 64 * s + 16 * (l >> 4);
+  auto nib = [&](int k) -> uint32_t {  // two's-complement nibble of (row, k); 0 outside the weight
+    if (row >= N || k >= K) return 0u;
+    uint32_t n;
+    if (layout == 0) {  // byte j of a row: k = j (low nibble), k = j + K/2 (high nibble)
+      const int half = K / 2;
+      const uint32_t b = q[(int64_t)row * ldq + (k < half ? k : k - half)];
+      n = k < half ? (b & 0xFu) : (b >> 4);
+    } else {  // int32 word j of a row: nibble i holds k = 8j + i
+      const uint32_t w = reinterpret_cast<const uint32_t*>(q)[(int64_t)row * ldq + k / 8];
+      n = (w >> (4 * (k % 8))) & 0xFu;
+    }
+    return n ^ 8u;  // offset-8 nibble -> two's complement
+  };
+  uint32_t d[2];
+#pragma unroll
+  for (int dd = 0; dd < 2; ++dd) {
+    uint32_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v |= (nib(k0 + 8 * dd + i) | (nib(k0 + 8 * dd + 4 + i) << 4)) << (8 * i);
+    d[dd] = v;
+  }
+  *reinterpret_cast<v2i*>(out + frag * 512 + l * 8) = v2i{(int)d[0], (int)d[1]};
+}
+
 // Kernel family override (0 = automatic), set through specq_set_option("w8a8_path", v).
 std::atomic<int> g_w8a8_path{0};
 extern std::atomic<int> g_w4a16_path;  // api_w4a16.hip
@@ -82,15 +121,19 @@ const void* legacy_fn(int mt, int rw, int vec) {
 }
 
 const void* ws_fn(int bnsel, int layout, int mt) {
-  switch (bnsel * 2 + layout) {
+  switch (bnsel * 3 + layout) {
     case 0: return w8a8_ws_fn_n16_l0(mt);
     case 1: return w8a8_ws_fn_n16_l1(mt);
-    case 2: return w8a8_ws_fn_n32_l0(mt);
-    case 3: return w8a8_ws_fn_n32_l1(mt);
-    case 4: return w8a8_ws_fn_n64_l0(mt);
-    case 5: return w8a8_ws_fn_n64_l1(mt);
-    case 6: return w8a8_ws_fn_n128_l0(mt);
-    case 7: return w8a8_ws_fn_n128_l1(mt);
+    case 2: return w8a8_ws_fn_n16_l2(mt);
+    case 3: return w8a8_ws_fn_n32_l0(mt);
+    case 4: return w8a8_ws_fn_n32_l1(mt);
+    case 5: return w8a8_ws_fn_n32_l2(mt);
+    case 6: return w8a8_ws_fn_n64_l0(mt);
+    case 7: return w8a8_ws_fn_n64_l1(mt);
+    case 8: return w8a8_ws_fn_n64_l2(mt);
+    case 9: return w8a8_ws_fn_n128_l0(mt);
+    case 10: return w8a8_ws_fn_n128_l1(mt);
+    case 11: return w8a8_ws_fn_n128_l2(mt);
   }
   return nullptr;
 }
@@ -105,7 +148,9 @@ int kw_of_sel(int sel) { return sel == 0 ? 4 : (sel == 1 ? 2 : 1); }  // waves s
 // split costs ~2 us plus writing and reading its INT32 partial tiles at ~2 TB/s.  Shapes that
 // need more workgroups than CUs are left out (one workgroup per CU streams best).
 // `bnsel_fixed` >= 0 keeps the caller's BLOCK_N; `splits_fixed` > 0 keeps its split count.
-void ws_auto_tiles(int rows, int m_chunks, int N, int K, int bnsel_fixed, int splits_fixed, int* bnsel, int* splits) {
+// `wb` is the weight bytes per element (1 for INT8, 0.5 for the INT4 weights of W4A8).
+void ws_auto_tiles(int rows, int m_chunks, int N, int K, double wb, int bnsel_fixed, int splits_fixed, int* bnsel,
+                   int* splits) {
   const int cus = device_cus();
   const int mpad = ceil_div(rows, 16) * 16;
   double best_t = 0;
@@ -118,7 +163,7 @@ void ws_auto_tiles(int rows, int m_chunks, int N, int K, int bnsel_fixed, int sp
       for (int ci = 0; ci < (splits_fixed > 0 ? 1 : 3); ++ci) {
         const int s = cand[ci];
         if (pass == 0 && (int64_t)ceil_div(N, bn) * s * m_chunks > cus) continue;
-        double t = std::max((double)(bn + rows) * K / s / 50e3, (double)N * K / 7e6);
+        double t = std::max((bn * wb + rows) * K / s / 50e3, N * wb * K / 7e6);
         if (s > 1) t += 2.0 + (double)s * mpad * N * 8 / 2e6;
         if (pass == 1) t *= (double)ceil_div(ceil_div(N, bn) * s * m_chunks, cus);  // rounds of workgroups
         if (best_sel < 0 || t < best_t) { best_t = t; best_sel = sel; best_s = s; }
@@ -169,7 +214,7 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
       // With a plan the grid is sized for the largest M, but usually one M-chunk is active.
       const int rows = std::min(std::max(m_grid, 1), mt * 16);
       const int chunks = plan_mode ? 1 : ceil_div(std::max(m_grid, 1), mt * 16);
-      ws_auto_tiles(rows, chunks, N, K, want, split_k, &bnsel, &ws_splits);
+      ws_auto_tiles(rows, chunks, N, K, layout == 2 ? 0.5 : 1.0, want, split_k, &bnsel, &ws_splits);
     } else if (want >= 0) {
       bnsel = want;
     } else {
@@ -254,7 +299,7 @@ int run_w8a8(int layout, const int8_t* a, int64_t lda, const void* w, int64_t ld
              int num_warps, int split_k, void* workspace, size_t workspace_bytes, void* stream) {
   SPECQ_REQUIRE(M >= 0 && N > 0 && K > 0, SPECQ_EINVAL, "w8a8: bad sizes M=%d N=%d K=%d", M, N, K);
   SPECQ_REQUIRE(a && w && sa && sw && c, SPECQ_EINVAL, "w8a8: null tensor pointer");
-  SPECQ_REQUIRE(lda >= K && (layout == 1 || ldw >= K) && ldc >= N, SPECQ_EINVAL,
+  SPECQ_REQUIRE(lda >= K && (layout != 0 || ldw >= K) && ldc >= N, SPECQ_EINVAL,
                 "w8a8: row strides must cover a row (lda=%lld ldw=%lld ldc=%lld)", (long long)lda, (long long)ldw,
                 (long long)ldc);
   SPECQ_REQUIRE(grid_m_max == 0 || grid_m_max >= M, SPECQ_EINVAL, "w8a8: grid_m_max=%d < M=%d", grid_m_max, M);
@@ -265,6 +310,7 @@ int run_w8a8(int layout, const int8_t* a, int64_t lda, const void* w, int64_t ld
   SPECQ_REQUIRE(layout == 0 || vec == 16, SPECQ_ENOTSUP,
                 "w8a8: packed weights need 16-byte aligned activations and K %% 16 == 0");
   SPECQ_REQUIRE(layout == 0 || (uintptr_t)w % 16 == 0, SPECQ_EINVAL, "w8a8: misaligned packed weight");
+  SPECQ_REQUIRE(layout != 2 || K <= 131072, SPECQ_ENOTSUP, "w4a8: K=%d exceeds 131072 (INT32 range of 16*sum)", K);
   W8A8Cfg cfg;
   int rc = w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, vec, plan != nullptr, &cfg);
   if (rc) return rc;
@@ -290,7 +336,7 @@ size_t workspace_size(int layout, int m_grid, int N, int K, int block_m, int blo
   size_t best = 0;
   // Size for every alignment class and mode (eager or plan) the call could resolve to.
   for (int vec : {16, 1}) {
-    if (layout == 1 && vec != 16) continue;
+    if (layout != 0 && vec != 16) continue;
     for (bool plan_mode : {false, true}) {
       if (w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, vec, plan_mode, &cfg) == SPECQ_OK) {
         const size_t s = cfg.ws_partials + cfg.ws_counters;
@@ -309,7 +355,7 @@ int w8a8_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, i
   W8A8Cfg cfg;
   const bool plan_mode = (layout & kAttrsPlan) != 0;
   layout &= ~kAttrsPlan;
-  SPECQ_REQUIRE(layout == 0 || layout == 1, SPECQ_EINVAL, "w8a8 attrs: layout %d", layout);
+  SPECQ_REQUIRE(layout >= 0 && layout <= 2, SPECQ_EINVAL, "w8a8 attrs: layout %d", layout);
   int rc = w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, 16, plan_mode, &cfg);
   if (rc) return rc;
   hipFuncAttributes fa;
@@ -404,4 +450,45 @@ extern "C" int specq_set_option(const char* name, int value) {
   }
   set_error("set_option: unknown option '%s'", name);
   return SPECQ_EINVAL;
+}
+
+extern "C" size_t specq_w4a8_packed_bytes(int N, int K) {
+  if (N <= 0 || K <= 0) return 0;
+  return (size_t)ceil_div(N, 16) * ceil_div(K, 64) * 512;
+}
+
+extern "C" int specq_w4a8_pack_weight(const void* wq, int64_t ldq, int wq_layout, int N, int K, void* packed,
+                                      void* stream) {
+  clear_error();
+  SPECQ_REQUIRE(wq && packed, SPECQ_EINVAL, "w4a8_pack_weight: null tensor pointer");
+  SPECQ_REQUIRE(wq_layout == 0 || wq_layout == 1, SPECQ_EINVAL, "w4a8_pack_weight: source layout must be 0 or 1");
+  SPECQ_REQUIRE(N > 0 && K > 0 && (wq_layout == 0 ? K % 2 == 0 && ldq >= K / 2 : K % 8 == 0 && ldq >= K / 8),
+                SPECQ_EINVAL, "w4a8_pack_weight: bad sizes N=%d K=%d ldq=%lld for layout %d", N, K, (long long)ldq,
+                wq_layout);
+  SPECQ_REQUIRE(wq_layout == 0 || (uintptr_t)wq % 4 == 0, SPECQ_EINVAL, "w4a8_pack_weight: misaligned int32 source");
+  SPECQ_REQUIRE((uintptr_t)packed % 16 == 0, SPECQ_EINVAL, "w4a8_pack_weight: misaligned output");
+  const int64_t frags = (int64_t)ceil_div(N, 16) * ceil_div(K, 64);
+  SPECQ_REQUIRE(ceil_div64(frags, 4) <= INT32_MAX, SPECQ_ENOTSUP, "w4a8_pack_weight: weight too large");
+  void* args[] = {(void*)&wq, (void*)&ldq, (void*)&wq_layout, (void*)&N, (void*)&K, (void*)&packed};
+  hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&w4a8_pack_kernel),
+                                 dim3((unsigned)ceil_div64(frags, 4)), dim3(256), args, 0, (hipStream_t)stream);
+  if (e != hipSuccess) {
+    set_error("w4a8_pack_weight: hipLaunchKernel failed: %s", hipGetErrorString(e));
+    return SPECQ_EIO;
+  }
+  return SPECQ_OK;
+}
+
+extern "C" size_t specq_w4a8_packed_workspace_size(int m_grid, int N, int K, int block_m, int block_n,
+                                                   int num_warps, int split_k) {
+  return workspace_size(2, m_grid, N, K, block_m, block_n, num_warps, split_k);
+}
+
+extern "C" int specq_w4a8_packed(const int8_t* a, int64_t lda, const void* w_packed, const float* sa,
+                                 const float* sw, void* c, int64_t ldc, int M, int N, int K, int grid_m_max,
+                                 const int32_t* plan, int block_m, int block_n, int num_warps, int split_k,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  return run_w8a8(2, a, lda, w_packed, 0, sa, sw, c, ldc, M, N, K, grid_m_max, plan, block_m, block_n, num_warps,
+                  split_k, workspace, workspace_bytes, stream);
 }

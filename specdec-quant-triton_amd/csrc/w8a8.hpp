@@ -60,6 +60,48 @@ __device__ __forceinline__ void w8a8_mma_step(const v4i (&wf)[RW], const v4i (&a
       acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[i], af[j], acc[i][j], 0, 0, 0);
 }
 
+// ---------------------------------------------------------------------------------------
+// Weight fragments of the streaming kernels, by weight layout WL:
+//   0  row-major int8 [N, K], read as 16 rows x 64 bytes per instruction (16 bytes per lane)
+//   1  packed int8 MFMA fragments, 1 KB per (64-byte K step, 16-row tile)
+//   2  packed INT4 (W4A8): 512 bytes per (K step, tile), 8 bytes per lane.  Lane l holds row
+//      16t + l%16; byte i (0..3) of its dword d carries, as two's-complement nibbles, the
+//      weights at K offset 16*(l/16) + 8d + i (low nibble) and 16*(l/16) + 8d + 4 + i (high).
+// ---------------------------------------------------------------------------------------
+template <int WL> struct W8A8WFragT { using type = v4i; };
+template <> struct W8A8WFragT<2> { using type = v2i; };
+template <int WL> using W8A8WFrag = typename W8A8WFragT<WL>::type;
+template <int WL> struct W8A8WFragBytes { static constexpr uint32_t value = WL == 2 ? 512u : 1024u; };
+
+template <int WL>
+__device__ __forceinline__ W8A8WFrag<WL> w8a8_wload(rsrc_t rs, uint32_t off) {
+  if constexpr (WL == 2) {
+    return __builtin_bit_cast(v2i, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 2));
+  } else {
+    return __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 2);
+  }
+}
+
+// The MFMA A operand of a weight fragment.  An INT4 fragment expands to 16 int8 values that
+// hold 16 * q: the nibble is moved to the top of its byte (low nibbles by a 4-bit shift), and
+// the byte read as int8 is then 16 times the two's-complement nibble, with no carries between
+// bytes.  Products and sums are therefore exactly 16 times the W4A8 ones (|16 * sum| stays
+// below 2^31 for K <= 131072) and w8a8_unscale16 restores them with an exact shift.
+__device__ __forceinline__ v4i w8a8_wop(v4i w) { return w; }
+__device__ __forceinline__ v4i w8a8_wop(v2i w) {
+  const uint32_t d0 = (uint32_t)w.x, d1 = (uint32_t)w.y;
+  return v4i{(int)((d0 << 4) & 0xF0F0F0F0u), (int)(d0 & 0xF0F0F0F0u),
+             (int)((d1 << 4) & 0xF0F0F0F0u), (int)(d1 & 0xF0F0F0F0u)};
+}
+
+template <int RW, int MT>
+__device__ __forceinline__ void w8a8_unscale16(v4i (&acc)[RW][MT]) {
+#pragma unroll
+  for (int a = 0; a < RW; ++a)
+#pragma unroll
+    for (int u = 0; u < MT; ++u) acc[a][u] = acc[a][u] >> 4;  // every sum is a multiple of 16
+}
+
 // Epilogue for 4 consecutive output channels of one token row, with the token scale `a` and
 // the channel scales `w` already in registers (entries past N are not stored).
 __device__ __forceinline__ void w8a8_store4s(const W8A8Params& p, int m, int n, v4i s, float a, const float (&w)[4]) {

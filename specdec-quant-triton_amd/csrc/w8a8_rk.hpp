@@ -28,6 +28,8 @@
 //    plan mode and the epilogue are shared with w8a8_kernel.
 //  * Used for short token batches (M <= 16): one activation fragment per K step is cheap to
 //    fetch per wave, and without LDS staging any number of waves can split K.
+//  * LAYOUT 2 is the packed INT4 weight of W4A8 (w8a8_wop): half the weight bytes per step,
+//    INT32 sums shifted right by 4 (exact) before the shared epilogue.
 #pragma once
 #include "w8a8.hpp"
 
@@ -80,6 +82,8 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
 #pragma unroll
   for (int j = 0; j < MT; ++j) arow[j] = (j * 16 + r < m_rows) ? (uint32_t)((j * 16 + r) * p.lda + g * 16) : kOOB;
 
+  using WFrag = W8A8WFrag<LAYOUT>;
+  constexpr uint32_t FB = W8A8WFragBytes<LAYOUT>::value;  // bytes of one packed fragment
   const int n_rows_w = uniform(max(0, min(BNW, p.N - n0)));
   rsrc_t wsrc;
   uint32_t wrow[RW];
@@ -89,21 +93,22 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
 #pragma unroll
     for (int i = 0; i < RW; ++i) wrow[i] = (i * 16 + r < n_rows_w) ? (uint32_t)((i * 16 + r) * p.ldw + g * 16) : kOOB;
   } else {
-    // K-step-major packed fragments: (tile t, step s) at (s * ntiles + t) KB.
+    // K-step-major packed fragments: (tile t, step s) at fragment s * ntiles + t (FB bytes each).
     const int ntiles = (p.N + 15) / 16;
     const int ksteps = (p.K + 63) / 64;
-    wsrc = make_rsrc(p.W, (uint32_t)((size_t)ksteps * ntiles * 1024));
+    wsrc = make_rsrc(p.W, (uint32_t)((size_t)ksteps * ntiles * FB));
 #pragma unroll
-    for (int i = 0; i < RW; ++i) wrow[i] = (n0 / 16 + i < ntiles) ? (uint32_t)((n0 / 16 + i) * 1024 + lane * 16) : kOOB;
+    for (int i = 0; i < RW; ++i)
+      wrow[i] = (n0 / 16 + i < ntiles) ? (uint32_t)((n0 / 16 + i) * FB + lane * (FB / 64)) : kOOB;
   }
-  const uint32_t sstride = LAYOUT == 0 ? 64u : (uint32_t)((p.N + 15) / 16) * 1024u;
+  const uint32_t sstride = LAYOUT == 0 ? 64u : (uint32_t)((p.N + 15) / 16) * FB;
 
   // Per-lane copies of the loop bounds (see w8a8_stream2: wave-uniform bounds turn the load
   // masks into branches, and a branch around a load forces a full vmcnt wait at the join).
   int cnt_v = cnt, ke_v = ke;
   asm volatile("" : "+v"(cnt_v), "+v"(ke_v));
 
-  auto issue = [&](int i, v4i (&slot)[PER]) {
+  auto issue = [&](int i, WFrag (&wslot)[RW], v4i (&aslot)[MT]) {
     int pos = kw + i * KW + rot;
     pos = pos >= nsteps ? pos - nsteps : pos;
     const int k0 = kb + pos * 64;
@@ -111,11 +116,11 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
 #pragma unroll
     for (int t = 0; t < RW; ++t) {
       const uint32_t off = oob_unless(live & (wrow[t] != kOOB), wrow[t] + (uint32_t)(k0 / 64) * sstride);
-      slot[t] = __builtin_amdgcn_raw_buffer_load_b128(wsrc, off, 0, 2);
+      wslot[t] = w8a8_wload<LAYOUT>(wsrc, off);
     }
 #pragma unroll
     for (int j = 0; j < MT; ++j)
-      slot[RW + j] = __builtin_amdgcn_raw_buffer_load_b128(asrc, oob_unless(live & (arow[j] != kOOB), arow[j] + (uint32_t)k0), 0, 0);
+      aslot[j] = __builtin_amdgcn_raw_buffer_load_b128(asrc, oob_unless(live & (arow[j] != kOOB), arow[j] + (uint32_t)k0), 0, 0);
   };
 
   const bool owner = kw == 0;
@@ -128,13 +133,14 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
 #pragma unroll
     for (int j = 0; j < MT; ++j) acc[t][j] = v4i{0, 0, 0, 0};
 
-  v4i ring[NS][PER];
+  WFrag wring[NS][RW];
+  v4i aring[NS][MT];
   // Prologue: steps 0 .. D-1 in flight, issued in step order.  The scheduling barriers keep
   // the load order identical to the main loop's, so the wait counts the compiler derives at
   // the loop header agree on both incoming paths (otherwise it falls back to vmcnt(0)).
   static_for<0, D>([&](auto sc) {
     constexpr int s = decltype(sc)::value;
-    issue(s, ring[s]);
+    issue(s, wring[s], aring[s]);
     __builtin_amdgcn_sched_barrier(0);
   });
   // Whole turns of the ring; steps past `cnt` load zeros (out-of-range offsets) and their
@@ -144,17 +150,20 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
     static_for<0, NS>([&](auto tc) __attribute__((always_inline)) {
       constexpr int t = decltype(tc)::value;
       constexpr int tn = (t + D) % NS;
-      issue(it * NS + t + D, ring[tn]);
+      issue(it * NS + t + D, wring[tn], aring[tn]);
       __builtin_amdgcn_sched_barrier(0);
       wait_vmcnt<D * PER>();
 #pragma unroll
-      for (int a = 0; a < RW; ++a)
+      for (int a = 0; a < RW; ++a) {
+        const v4i wf = w8a8_wop(wring[t][a]);
 #pragma unroll
         for (int j = 0; j < MT; ++j)
-          acc[a][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ring[t][a], ring[t][RW + j], acc[a][j], 0, 0, 0);
+          acc[a][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, aring[t][j], acc[a][j], 0, 0, 0);
+      }
     });
   }
   wait_vmcnt<0>();
+  if constexpr (LAYOUT == 2) w8a8_unscale16(acc);
 
   // Reduce the KW waves of each channel group through LDS in one round: each non-owner wave
   // writes its slice, then the owner adds them.

@@ -57,6 +57,10 @@ const void* w8a8_ws_fn_n64_l0(int mt);
 const void* w8a8_ws_fn_n64_l1(int mt);
 const void* w8a8_ws_fn_n128_l0(int mt);
 const void* w8a8_ws_fn_n128_l1(int mt);
+const void* w8a8_ws_fn_n16_l2(int mt);
+const void* w8a8_ws_fn_n32_l2(int mt);
+const void* w8a8_ws_fn_n64_l2(int mt);
+const void* w8a8_ws_fn_n128_l2(int mt);
 const void* w8a8_rk_fn(int bnsel, int layout);
 
 }  // namespace specq

@@ -28,6 +28,9 @@
 //    buffer reads (they return zero), so each iteration issues the same loads.
 //  * Split-K across workgroups hands INT32 tiles off 16 bytes per lane (w8a8_splitk_finish);
 //    plan mode and the epilogue are shared with w8a8_kernel.
+//  * WL 2 is the W4A8 weight: packed INT4 fragments of 512 bytes (8 bytes per lane per K
+//    step, w8a8_wop) that become INT8 operands holding 16 * q; the INT32 sums are shifted
+//    right by 4 (exact) before the shared epilogue.
 #pragma once
 #include "w8a8.hpp"
 
@@ -124,6 +127,7 @@ __global__ __launch_bounds__(NW * 64) void w8a8_ws_kernel(W8A8Params p) {
 
   // ---- Weight stream.  Wave-local step i belongs to chunk i / S; its step j = i % S of the
   // chunk is K step kw + KW * j of the chunk.
+  using WFrag = W8A8WFrag<WL>;
   const int n_rows_w = uniform(max(0, min(BNW, p.N - n0)));
   rsrc_t wsrc;
   uint32_t wrow[RW];
@@ -135,20 +139,22 @@ __global__ __launch_bounds__(NW * 64) void w8a8_ws_kernel(W8A8Params p) {
     for (int i = 0; i < RW; ++i) wrow[i] = (i * 16 + r < n_rows_w) ? (uint32_t)((i * 16 + r) * p.ldw + g * 16) : kOOB;
     sstride = 64;
   } else {
+    constexpr uint32_t FB = W8A8WFragBytes<WL>::value;  // bytes of one packed fragment
     const int ntiles = (p.N + 15) / 16;
     const int ksteps = (p.K + 63) / 64;
-    wsrc = make_rsrc(p.W, (uint32_t)((size_t)ksteps * ntiles * 1024));
+    wsrc = make_rsrc(p.W, (uint32_t)((size_t)ksteps * ntiles * FB));
 #pragma unroll
-    for (int i = 0; i < RW; ++i) wrow[i] = (n0 / 16 + i < ntiles) ? (uint32_t)((n0 / 16 + i) * 1024 + lane * 16) : kOOB;
-    sstride = (uint32_t)ntiles * 1024u;
+    for (int i = 0; i < RW; ++i)
+      wrow[i] = (n0 / 16 + i < ntiles) ? (uint32_t)((n0 / 16 + i) * FB + lane * (FB / 64)) : kOOB;
+    sstride = (uint32_t)ntiles * FB;
   }
-  auto w_issue = [&](int c, int j, v4i (&slot)[RW]) {
+  auto w_issue = [&](int c, int j, WFrag (&slot)[RW]) {
     const int step = (chunk_k0(c) >> 6) + kw + KW * j;  // global K step of chunk c, step j
     const bool live = (c < nchunks) & (step * 64 + g * 16 < ke_v);
 #pragma unroll
     for (int t = 0; t < RW; ++t) {
       const uint32_t off = oob_unless(live & (wrow[t] != kOOB), wrow[t] + (uint32_t)step * sstride);
-      slot[t] = __builtin_amdgcn_raw_buffer_load_b128(wsrc, off, 0, 2);
+      slot[t] = w8a8_wload<WL>(wsrc, off);
     }
   };
 
@@ -169,7 +175,7 @@ __global__ __launch_bounds__(NW * 64) void w8a8_ws_kernel(W8A8Params p) {
   // every wait count below is a compile-time constant:
   //   after step i's weights:  D weight steps + NSLOT DMA groups (j < S-1) or P (j = S-1);
   //   after chunk c's DMA:     P*S weight steps + P-1 DMA groups.
-  v4i ring[NS][RW];
+  WFrag ring[NS][RW];
   static_for<0, S - 1>([&](auto sc) {
     constexpr int s = decltype(sc)::value;
     w_issue(0, s, ring[s]);
@@ -217,15 +223,18 @@ __global__ __launch_bounds__(NW * 64) void w8a8_ws_kernel(W8A8Params p) {
           af[u] = *reinterpret_cast<const v4i*>(aslot + (blk * BM + row) * 256 + 16 * (piece ^ r));
         }
 #pragma unroll
-        for (int a = 0; a < RW; ++a)
+        for (int a = 0; a < RW; ++a) {
+          const v4i wf = w8a8_wop(ring[ri][a]);
 #pragma unroll
           for (int u = 0; u < MT; ++u)
-            acc[a][u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ring[ri][a], af[u], acc[a][u], 0, 0, 0);
+            acc[a][u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf, af[u], acc[a][u], 0, 0, 0);
+        }
       });
     });
   }
   wait_vmcnt<0>();
   wg_barrier_lds();  // every wave is done with the activation slots
+  if constexpr (WL == 2) w8a8_unscale16(acc);
 
   // Reduce the KW waves of each channel group through LDS: every non-owner wave writes its
   // slice into its own activation slot (up to NSLOT slices per round), then the owner adds

@@ -13,6 +13,12 @@ HIP for gfx950 in csrc/, reached through the C ABI of libspecq.so (include/specq
                    program, QPP=1 (decode style) or QPP=q_len (fused)
                    (reference kernels.py:178-236, 239-262)
 
+and the steps either side of them on the device: paged_kv_append (the new tokens' K/V
+quantised into the cache pages, the q8 of kernels.py:280-284), silu_mul /
+silu_mul_quant_int8 / quantize_act_int8_gpu (kernels.py:58-62 on the device), and
+w4a8_matmul (INT4 weights on the INT8 MFMA path, the reference's REPORT.md:156
+recommendation; no reference kernel).
+
 Every launcher takes `plan` (an int32 device tensor read by the kernel at run time) and a
 fixed grid size, so a single captured graph replays every (B, k) (reference kernels.py:14-17).
 Launches go to torch's current stream and never synchronise or allocate (except the
@@ -60,8 +66,9 @@ __all__ = [
     "w8a8_matmul", "w4a16_matmul", "paged_attention",
     "quantize_act_int8", "quantize_weight_int8", "quantize_weight_int4",
     "make_paged_kv", "paged_attention_ref",
-    "silu_mul", "quantize_act_int8_gpu", "silu_mul_quant_int8",
+    "silu_mul", "quantize_act_int8_gpu", "silu_mul_quant_int8", "paged_kv_append",
     "pack_int4_i32", "KernelInfo", "PackedWeightInt8", "pack_weight_int8", "PackedWeightInt4", "pack_weight_int4",
+    "w4a8_matmul", "quantize_weight_int4_channel", "PackedWeightW4A8", "pack_weight_w4a8",
 ]
 
 
@@ -543,3 +550,146 @@ def silu_mul_quant_int8(gate, up, q=None, s=None, plan=None, grid_m_max=None):
               q.data_ptr(), q.stride(0), s.data_ptr(), M, N, int(grid_m_max or 0), _plan_ptr(plan),
               _stream_ptr(gate))
     return q, s
+
+
+# ----------------------------------------------------------------------------------------
+# Paged INT8 KV-cache append (the device-side counterpart of make_paged_kv's q8)
+# ----------------------------------------------------------------------------------------
+def paged_kv_append(k_new, v_new, kc, vc, ks, vs, block_tbl, ctx_len, q_len=None, plan=None, n_seqs=None):
+    """Quantise the new tokens' K/V into the paged INT8 cache, in place (kernels.py:280-284).
+
+    k_new, v_new fp16 [B, QLMAX, H_KV, D] (the q_len tokens being verified); kc/vc int8
+    [pages, PAGE, H_KV, D]; ks/vs fp16 or fp32 [pages, PAGE, H_KV]; block_tbl int32
+    [B, max_pages]; ctx_len int32 [B], already counting the new tokens, so token i of
+    sequence b goes to position ctx_len[b] - q_len + i.  Each (token, head) row gets
+    s = max(amax, 1e-8) / 127 and q = clamp(rne(x / s), -127, 127), exactly as the
+    reference quantises its cache.  With `plan`, (n_seqs, q_len) = plan[0:2] on the device
+    and the grid covers (B, QLMAX).  Slots of inactive sequences and tokens are not written.
+    """
+    _require_gpu(k_new, v_new, kc, vc, ks, vs, block_tbl, ctx_len)
+    B, QLMAX, H_KV, D = k_new.shape
+    if v_new.shape != k_new.shape:
+        raise RuntimeError("paged_kv_append: k_new and v_new must have the same shape")
+    if k_new.dtype != torch.float16 or v_new.dtype != torch.float16:
+        raise RuntimeError("paged_kv_append expects fp16 k_new and v_new")
+    if kc.dtype != torch.int8 or vc.dtype != torch.int8 or kc.shape != vc.shape:
+        raise RuntimeError("paged_kv_append expects int8 K/V caches of one shape")
+    if kc.shape[2] != H_KV or kc.shape[3] != D:
+        raise RuntimeError(f"paged_kv_append: cache {tuple(kc.shape)} does not match new K/V {tuple(k_new.shape)}")
+    if kc.stride() != vc.stride() or ks.stride() != vs.stride() or ks.dtype != vs.dtype:
+        raise RuntimeError("paged_kv_append: K and V (and their scales) must share layout and dtype")
+    if ks.dtype not in (torch.float16, torch.float32):
+        raise RuntimeError("paged_kv_append: scales must be fp16 or fp32")
+    if block_tbl.dtype != torch.int32 or ctx_len.dtype != torch.int32:
+        raise RuntimeError("paged_kv_append: block_tbl and ctx_len must be int32")
+    if kc.stride(3) != 1:
+        raise RuntimeError("paged_kv_append: head_dim of the cache must be contiguous")
+    if k_new.stride() != v_new.stride() or k_new.stride(3) != 1:
+        k_new, v_new = k_new.contiguous(), v_new.contiguous()
+    block_tbl = _rowmajor(block_tbl)
+    ctx_len = ctx_len.contiguous()
+    q_len = QLMAX if q_len is None else int(q_len)
+    n_seqs = B if n_seqs is None else int(n_seqs)
+    if not (0 <= n_seqs <= B and 0 <= q_len <= QLMAX):
+        raise RuntimeError(f"paged_kv_append: need 0 <= n_seqs <= {B} and 0 <= q_len <= {QLMAX}")
+    B_grid = B if plan is not None else n_seqs
+    ql_grid = QLMAX if plan is not None else q_len
+    if block_tbl.dim() != 2 or block_tbl.shape[0] < B_grid or ctx_len.numel() < B_grid:
+        raise RuntimeError("paged_kv_append: block_tbl and ctx_len must cover every sequence of the grid")
+    _lib.call("specq_kv_append_int8",
+              k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1), k_new.stride(2),
+              kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2),
+              ks.data_ptr(), vs.data_ptr(), ks.stride(0), ks.stride(1), ks.stride(2),
+              1 if ks.dtype == torch.float32 else 0,
+              block_tbl.data_ptr(), block_tbl.stride(0), block_tbl.shape[1], kc.shape[0], ctx_len.data_ptr(),
+              B_grid, n_seqs, q_len, ql_grid, H_KV, D, kc.shape[1], _plan_ptr(plan), _stream_ptr(k_new))
+
+
+# ----------------------------------------------------------------------------------------
+# W4A8: INT4 weights on the INT8 MFMA path, per-channel scale in the W8A8 epilogue
+# ----------------------------------------------------------------------------------------
+def quantize_weight_int4_channel(w):
+    """Per-channel symmetric INT4 weight for w4a8_matmul: (packed uint8 [N, K/2], scale fp32 [N]).
+
+    The reference quantiser with one group per row (kernels.py:138-147 at group = K) and the
+    scale kept in fp32: sc = max(amax_row, 1e-8) / 7, q = clamp(round(w / sc), -8, 7) + 8,
+    packed as the reference packs (byte j = q[:, j] | q[:, j + K/2] << 4).
+    """
+    N, K = w.shape
+    if K % 2:
+        raise RuntimeError("quantize_weight_int4_channel: K must be even")
+    wf = w.float()
+    sc = wf.abs().amax(-1).clamp(min=1e-8) / 7.0
+    q = (torch.round(wf / sc[:, None]).clamp(-8, 7) + 8).to(torch.uint8)
+    half = K // 2
+    return (q[:, :half] | (q[:, half:] << 4)).contiguous(), sc
+
+
+class PackedWeightW4A8:
+    """An INT4 weight packed once into the W4A8 kernel's 512-byte MFMA fragments.
+
+    Source: the reference uint8 packing [N, K/2] (byte j holds k = j and k = j + K/2) or the
+    int32 packing [N, K/8] (nibble i of word j holds k = 8j + i), nibbles with offset 8.
+    Fragment (64-wide K step s, 16-row tile t) is the 512 bytes at (s * ceil(N/16) + t) * 512.
+    """
+
+    def __init__(self, wq: torch.Tensor, K: int = None):
+        _require_gpu(wq)
+        if wq.dim() != 2 or wq.dtype not in (torch.uint8, torch.int32):
+            raise RuntimeError("PackedWeightW4A8 expects a uint8 [N, K/2] or int32 [N, K/8] INT4 weight")
+        wq = _rowmajor(wq)
+        layout = 0 if wq.dtype == torch.uint8 else 1
+        self.N = wq.shape[0]
+        self.K = int(K) if K is not None else wq.shape[1] * (2 if layout == 0 else 8)
+        self.shape = (self.N, self.K)
+        self.device = wq.device
+        nbytes = _lib.lib().specq_w4a8_packed_bytes(self.N, self.K)
+        self.data = torch.empty(nbytes, dtype=torch.int8, device=wq.device)
+        _lib.call("specq_w4a8_pack_weight", wq.data_ptr(), wq.stride(0), layout, self.N, self.K,
+                  self.data.data_ptr(), _stream_ptr(wq))
+
+
+def pack_weight_w4a8(wq, K: int = None):
+    """Pack an INT4 weight (uint8 [N, K/2] or int32 [N, K/8]) for w4a8_matmul."""
+    return PackedWeightW4A8(wq, K)
+
+
+def w4a8_matmul(a_q, sa, wq, sw, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK_K=128, num_warps=4,
+                num_stages=3, plan=None, grid_m_max=None, split_k=0, workspace=None):
+    """C[M, N] = fp16((int32(a_q @ (q - 8).T) * sa[:, None]) * sw[None, :]).  Returns (out, ck).
+
+    a_q int8 [M, K] with per-token scale sa fp32 [M] (quantize_act_int8); wq a
+    PackedWeightW4A8, or an INT4 weight in the reference uint8 / int32 packing (packed here on
+    every call; pack once at load time instead); sw fp32 [N] per-channel scale
+    (quantize_weight_int4_channel).  Arguments otherwise as w8a8_matmul; results are
+    bit-identical to w8a8_matmul on the unpacked INT4 weight.
+    """
+    if not isinstance(wq, PackedWeightW4A8):
+        wq = PackedWeightW4A8(wq, a_q.shape[1])
+    _require_gpu(a_q, sa, sw)
+    if a_q.dtype != torch.int8:
+        raise RuntimeError("w4a8_matmul expects int8 activations")
+    M, K = a_q.shape
+    N = wq.N
+    if wq.K != K:
+        raise RuntimeError(f"w4a8_matmul: K mismatch {tuple(a_q.shape)} vs {wq.shape}")
+    a_q = _rowmajor(a_q)
+    sa = sa.float().contiguous()
+    sw = sw.float().contiguous()
+    if out is None:
+        out = torch.empty((M, N), device=a_q.device, dtype=torch.float16)
+    if out.dtype != torch.float16 or out.stride(-1) != 1:
+        raise RuntimeError("w4a8_matmul: out must be fp16 with unit inner stride")
+    m_grid = int(grid_m_max) if grid_m_max is not None else M
+    bm = BLOCK_M if BLOCK_M else pick_block_m("w8a8", m_grid, N, K)
+    bn = _w8a8_block_n(BLOCK_N)
+    nw = int(num_warps) if num_warps else 4
+    ws = workspace or _ws.shared(a_q.device)
+    need = _lib.lib().specq_w4a8_packed_workspace_size(m_grid, N, K, bm, bn, nw, split_k)
+    wptr, wbytes = ws.ensure(need)
+    _lib.call("specq_w4a8_packed", a_q.data_ptr(), a_q.stride(0), wq.data.data_ptr(),
+              sa.data_ptr(), sw.data_ptr(), out.data_ptr(), out.stride(0),
+              M, N, K, int(grid_m_max or 0), _plan_ptr(plan), bm, bn, nw, split_k,
+              wptr, wbytes, _stream_ptr(a_q))
+    _w8a8_kernel._note(a_q.device.index or 0, (bm, bn, nw, "w4a8"))
+    return out, KernelInfo(0, 2 | (16 if plan is not None else 0), m_grid, N, K, bm, bn, nw, split_k)

@@ -44,6 +44,12 @@ SIGNATURES = {
     "specq_w8a8_packed": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
                                    _c_int, _c_int, _c_int, _c_int, _c_vp,
                                    _c_int, _c_int, _c_int, _c_int, _c_vp, _c_size, _c_vp]),
+    "specq_w4a8_packed_bytes": (_c_size, [_c_int, _c_int]),
+    "specq_w4a8_pack_weight": (_c_int, [_c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp, _c_vp]),
+    "specq_w4a8_packed_workspace_size": (_c_size, [_c_int] * 7),
+    "specq_w4a8_packed": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
+                                   _c_int, _c_int, _c_int, _c_int, _c_vp,
+                                   _c_int, _c_int, _c_int, _c_int, _c_vp, _c_size, _c_vp]),
     "specq_set_option": (_c_int, [ctypes.c_char_p, _c_int]),
     "specq_w4a16_workspace_size": (_c_size, [_c_int] * 7),
     "specq_w4a16_packed_bytes": (_c_size, [_c_int, _c_int]),
@@ -59,6 +65,11 @@ SIGNATURES = {
                                   _c_vp, _c_i64, _c_i64, _c_i64,
                                   _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                   _c_int, _c_int, _c_float, _c_vp, _c_vp, _c_size, _c_vp]),
+    "specq_kv_append_int8": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                                      _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                                      _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
+                                      _c_vp, _c_i64, _c_int, _c_int, _c_vp,
+                                      _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp]),
     "specq_silu_mul": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp, _c_vp]),
     "specq_quantize_act_int8": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_int, _c_int, _c_int, _c_vp, _c_vp]),
     "specq_silu_mul_quant_int8": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp,

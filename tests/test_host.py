@@ -27,7 +27,8 @@ def test_header_lists_every_entry_point():
     for s in ["specq_w8a8", "specq_w4a16", "specq_paged_attn", "specq_w8a8_workspace_size",
               "specq_w4a16_workspace_size", "specq_paged_attn_workspace_size", "specq_silu_mul",
               "specq_quantize_act_int8", "specq_silu_mul_quant_int8", "specq_kernel_attrs_query",
-              "specq_last_error", "specq_version"]:
+              "specq_last_error", "specq_version", "specq_kv_append_int8", "specq_w4a8_packed",
+              "specq_w4a8_pack_weight", "specq_w4a8_packed_bytes", "specq_w4a8_packed_workspace_size"]:
         assert s in syms, s
 
 
@@ -93,6 +94,37 @@ def test_attn_validation_errors(built_lib):
     assert f(*bad_heads) == -22
     null_q = list(args); null_q[0] = 0
     assert f(*null_q) == -22
+
+
+def test_kv_append_validation_errors(built_lib):
+    from specq import _lib
+    f = _lib.lib().specq_kv_append_int8
+    # k_new, v_new, s_nb, s_nt, s_nh, kc, vc, s_kp, s_ko, s_kh, ks, vs, s_sp, s_so, s_sh, fp32,
+    # bt, s_bt, max_pages, n_pages, ctx, B_grid, n_seqs, q_len, ql_grid, H_KV, D, PAGE, plan, stream
+    args = [16, 16, 9 * 8 * 128, 8 * 128, 128, 16, 16, 16 * 8 * 128, 8 * 128, 128, 16, 16, 128, 8, 1, 1,
+            16, 64, 64, 100, 16, 2, 2, 9, 9, 8, 128, 16, 0, 0]
+    bad_d = list(args); bad_d[26] = 96
+    assert f(*bad_d) == -95
+    misaligned = list(args); misaligned[0] = 24
+    assert f(*misaligned) == -95
+    too_many = list(args); too_many[22] = 3            # n_seqs > B_grid
+    assert f(*too_many) == -22
+    null_bt = list(args); null_bt[16] = 0
+    assert f(*null_bt) == -22
+    assert f(*[a if i not in (21, 24) else 0 for i, a in enumerate(args)][:21] + [0, 0, 0, 0] + args[25:]) == 0
+
+
+def test_w4a8_validation_errors(built_lib):
+    from specq import _lib
+    L = _lib.lib()
+    assert L.specq_w4a8_packed_bytes(1000, 576) == 63 * 9 * 512
+    # a, lda, w, sa, sw, c, ldc, M, N, K, gmm, plan, bm, bn, nw, sk, ws, wsb, stream
+    base = [16, 131088, 16, 16, 16, 16, 32, 4, 32, 131088, 0, 0, 0, 0, 4, 0, 0, 0, 0]
+    assert L.specq_w4a8_packed(*base) == -95            # K beyond the INT32 range of 16 * sum
+    odd = list(base); odd[1] = odd[9] = 520
+    assert L.specq_w4a8_packed(*odd) == -95             # K % 16 != 0
+    assert L.specq_w4a8_pack_weight(16, 100, 2, 32, 200, 16, 0) == -22   # unknown source layout
+    assert L.specq_w4a8_pack_weight(16, 10, 0, 32, 200, 16, 0) == -22    # ldq < K/2
 
 
 def test_workspace_sizes(built_lib):

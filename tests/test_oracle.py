@@ -243,3 +243,122 @@ def test_silu_mul_matches_torch():
     u = torch.randn(8, 64, generator=torch.Generator().manual_seed(17)).half()
     ref = torch.nn.functional.silu(g.double()) * u.double()
     assert np.allclose(O.silu_mul(g.numpy(), u.numpy()), ref.numpy(), atol=1e-12)
+
+
+# ---------------------------------------------------------------- paged KV append
+def _q8_torch(x):
+    """kernels.py:280-283 evaluated with torch's own ops (library round half to even)."""
+    s = x.float().abs().amax(-1).clamp(min=1e-8) / 127.0
+    return torch.round(x.float() / s[..., None]).clamp(-127, 127).to(torch.int8), s
+
+
+def test_kv_append_rebuilds_make_paged_kv_cache():
+    # Appending every context token of every sequence into an empty cache reproduces the
+    # reference generator's cache bit for bit (same generator calls as kernels.py:265-286).
+    import kernels as K
+
+    B, ctx, H_KV, D, PAGE, seed = 3, [37, 16, 50], 2, 16, 16, 5
+    kc, vc, ks, vs, bt, cl = (t.numpy() for t in K.make_paged_kv(B, ctx, H_KV, D, PAGE, device="cpu", seed=seed))
+    g = torch.Generator().manual_seed(seed)
+    pages = [(l + PAGE - 1) // PAGE for l in ctx]
+    torch.randperm(sum(pages), generator=g)
+    kf = torch.randn((sum(pages), PAGE, H_KV, D), generator=g).half().numpy()
+    vf = torch.randn((sum(pages), PAGE, H_KV, D), generator=g).half().numpy()
+    QL = max(ctx)
+    k_new = np.zeros((B, QL, H_KV, D), np.float16)
+    v_new = np.zeros((B, QL, H_KV, D), np.float16)
+    for b in range(B):
+        pos = np.arange(ctx[b])
+        k_new[b, :ctx[b]] = kf[bt[b, pos // PAGE], pos % PAGE]
+        v_new[b, :ctx[b]] = vf[bt[b, pos // PAGE], pos % PAGE]
+    for b in range(B):  # one sequence at a time: q_len = its whole context
+        zk, zv = np.zeros_like(kc), np.zeros_like(vc)
+        zs, zt = np.zeros_like(ks), np.zeros_like(vs)
+        ok, ov, oks, ovs = O.paged_kv_append(k_new[b:b + 1], v_new[b:b + 1], zk, zv, zs, zt, bt[b:b + 1],
+                                             cl[b:b + 1], ctx[b])
+        pos = np.arange(ctx[b])
+        p, s = bt[b, pos // PAGE], pos % PAGE
+        assert np.array_equal(ok[p, s], kc[p, s]) and np.array_equal(ov[p, s], vc[p, s])
+        assert np.array_equal(oks[p, s].view(np.uint16), ks[p, s].view(np.uint16))
+        assert np.array_equal(ovs[p, s].view(np.uint16), vs[p, s].view(np.uint16))
+
+
+def test_kv_append_kats_and_torch_rounding():
+    # amax 127 gives s = 1 exactly: x / s = x, so 2.5 -> 2 and -3.5 -> -4 (half to even).
+    row = np.zeros(16, np.float16)
+    row[:5] = [127.0, 2.5, -3.5, 0.5, -127.0]
+    k_new = np.zeros((1, 1, 1, 16), np.float16)
+    k_new[0, 0, 0] = row
+    kc = np.zeros((2, 16, 1, 16), np.int8)
+    ks = np.zeros((2, 16, 1), np.float32)
+    bt = np.array([[1]], np.int32)
+    cl = np.array([4], np.int32)  # the new token sits at position 3 of page 1
+    ok, _, oks, _ = O.paged_kv_append(k_new, k_new, kc, kc, ks, ks, bt, cl, 1)
+    assert list(ok[1, 3, 0, :5]) == [127, 2, -4, 0, -127] and oks[1, 3, 0] == 1.0
+    assert (ok[0] == 0).all() and (ok[1, :3] == 0).all() and (ok[1, 4:] == 0).all()
+    # all-zero row: the 1e-8 clamp gives s = 1e-8 / 127 and q = 0
+    zero = np.zeros_like(k_new)
+    ok, _, oks, _ = O.paged_kv_append(zero, zero, kc, kc, ks, ks, bt, cl, 1)
+    assert (ok == 0).all() and oks[1, 3, 0] == np.float32(np.float32(1e-8) / np.float32(127))
+    # random rows against torch's own round/clamp
+    r = rng(9)
+    x = (r.standard_normal((2, 3, 2, 64)) * 3).astype(np.float16)
+    kc = np.zeros((4, 16, 2, 64), np.int8)
+    ks = np.zeros((4, 16, 2), np.float16)
+    bt = np.array([[2, 0], [3, 1]], np.int32)
+    cl = np.array([18, 3], np.int32)
+    ok, _, oks, _ = O.paged_kv_append(x, x, kc, kc, ks, ks, bt, cl, 3)
+    tq, ts = _q8_torch(torch.from_numpy(x))
+    for b, (p, s0) in enumerate([(0, 15), (3, 0)]):
+        pos = cl[b] - 3 + np.arange(3)
+        pages, slots = bt[b, pos // 16], pos % 16
+        assert np.array_equal(ok[pages, slots], tq[b].numpy())
+        assert np.array_equal(oks[pages, slots].view(np.uint16), ts[b].half().numpy().view(np.uint16))
+
+
+def test_kv_append_skips_rows_outside_the_cache():
+    x = np.ones((2, 2, 1, 16), np.float16)
+    kc = np.full((2, 16, 1, 16), 7, np.int8)
+    ks = np.full((2, 16, 1), 3.0, np.float16)
+    bt = np.array([[0], [5]], np.int32)      # sequence 1 names a page outside the pool
+    cl = np.array([17, 2], np.int32)         # sequence 0's second token falls past max_pages
+    ok, _, oks, _ = O.paged_kv_append(x, x, kc, kc, ks, ks, bt, cl, 2)
+    assert (ok[0, 15] == 127).all() and (ok[0, :15] == 7).all() and (ok[1] == 7).all()
+    assert oks[0, 15, 0] == np.float16(1.0 / 127.0) and (oks[1] == 3.0).all()
+
+
+# ---------------------------------------------------------------- W4A8
+def test_w4a8_brute_force_and_kats():
+    r = rng(21)
+    a = r.integers(-127, 128, (3, 10), dtype=np.int8)
+    qu = r.integers(0, 16, (4, 10)).astype(np.uint8)
+    sa = r.uniform(0.005, 0.02, 3).astype(np.float32)
+    sw = r.uniform(0.001, 0.01, 4).astype(np.float32)
+    got = O.w4a8(a, sa, qu, sw)
+    for m in range(3):
+        for n in range(4):
+            acc = sum(int(a[m, k]) * (int(qu[n, k]) - 8) for k in range(10))
+            want = np.float16(np.float32(np.float32(np.float32(acc) * sa[m]) * sw[n]))
+            assert got[m, n].view(np.uint16) == want.view(np.uint16)
+    # nibble 8 is weight 0; nibble 0 is -8; nibble 15 is +7
+    ones = np.ones((1, 64), np.int8)
+    s1 = np.ones(1, np.float32)
+    assert O.w4a8(ones, s1, np.full((1, 64), 8, np.uint8), s1)[0, 0] == 0
+    assert O.w4a8(ones, s1, np.zeros((1, 64), np.uint8), s1)[0, 0] == -512
+    assert O.w4a8(ones, s1, np.full((1, 64), 15, np.uint8), s1)[0, 0] == 448
+
+
+def test_w4a8_channel_quantizer_matches_torch_restatement():
+    import kernels as K
+
+    r = rng(22)
+    w = (r.standard_normal((24, 256)) * 0.05).astype(np.float32)
+    w[3, :] = 0.0                              # the 1e-8 clamp
+    w[5, :4] = [7.0, 3.5, -2.5, 0.5]           # amax 7 -> sc 1: half to even on 3.5, -2.5, 0.5
+    w[5, 4:] = 0.0
+    qu, sc = O.quantize_weight_int4_channel(w)
+    assert list(qu[5, :4].astype(int) - 8) == [7, 4, -2, 0] and sc[5] == 1.0
+    assert (qu[3] == 8).all() and sc[3] == np.float32(np.float32(1e-8) / np.float32(7))
+    packed, tsc = K.quantize_weight_int4_channel(torch.from_numpy(w))
+    assert np.array_equal(O.unpack_int4_u8(packed.numpy()), qu)
+    assert np.array_equal(tsc.numpy().view(np.uint32), sc.view(np.uint32))
