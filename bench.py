@@ -332,13 +332,21 @@ def bench_attention(args, K, torch):
 
 
 def bench_plan_graph(args, K, torch):
-    """Config 4: one plan-buffer graph of a 4-layer INT8 stack (d_model 4096, weights packed at
-    load) captured at B=32, k=8 (M=288), replayed over a seeded (B, k) trace; eager per-step
-    time for comparison."""
+    """Config 4: a 4-layer INT8 stack (d_model 4096, weights packed at load) replayed over a
+    seeded (B, k) trace, B in 1..32, k in {0, 2, 4, 8}, under five launch strategies:
+      eager     every step launched with its exact shapes
+      allshapes one graph per distinct (B, k) of the trace (captured before timing)
+      maxpad    one graph at B=32, k=8 (M=288) without a plan: every step computes M=288
+      plan      one plan-buffer graph captured at B=32, k=8, the active (B, k) read on device
+      bucketed  plan-buffer graphs per (B bucket 1/2/3/4/6/8/12/16/24/32, k): the GEMMs of each
+                bucket run the tile picked for its row count (PlanGraphSet)
+    Host perf_counter around plan write + replay + sync per step (bench_graphs.py:126-136).
+    Padding waste is the token rows the GEMMs compute beyond M, per step (the tile the library
+    resolved for that strategy's grid, chunks past the active M skipped in plan mode)."""
     import random
 
     from specq import gen
-    from specq.plan import Plan
+    from specq.plan import Plan, PlanGraphSet
 
     L, HID, QKV, FF = 4, 4096, 6144, 14336
     H, H_KV, D, CTX = 32, 8, 128, 1024
@@ -363,58 +371,104 @@ def bench_plan_graph(args, K, torch):
             for n, N in (("qkv", QKV), ("o", HID), ("gate", FF), ("up", FF), ("down", HID))}
     hq = torch.zeros(M_MAX, FF, device="cuda", dtype=torch.int8)
     hs = torch.zeros(M_MAX, device="cuda", dtype=torch.float32)
-    plan = Plan("cuda")
 
-    def step(B, ql, use_plan):
-        M = B * ql
-        kw = dict(plan=plan.gemm, grid_m_max=M_MAX) if use_plan else {}
-        aa, ss = (a, sa) if use_plan else (a[:M], sa[:M])
+    def step(Bg, qg, plan=None):
+        """One step with grids sized for (Bg, qg): the exact shape without a plan, else the
+        maxima of a plan-mode launch whose active (B, q_len) is read on the device."""
+        Mg = Bg * qg
+        kw = dict(plan=plan.gemm, grid_m_max=Mg) if plan is not None else {}
+        aa, ss = a[:Mg], sa[:Mg]
         for lw in layers:
-            K.w8a8_matmul(aa, ss, *lw["qkv"], out=bufs["qkv"], BLOCK_M=None, **kw)
+            K.w8a8_matmul(aa, ss, *lw["qkv"], out=bufs["qkv"][:Mg], BLOCK_M=None, **kw)
             kc, vc, ks, vs, bt, cl = lw["kv"]
-            if use_plan:
-                K.paged_attention(q_buf, kc, vc, ks, vs, bt, cl, QL_MAX, QPP=QL_MAX, plan=plan.attn, out=o_buf)
-            else:
-                K.paged_attention(q_buf[:B], kc, vc, ks, vs, bt[:B], cl[:B], ql, QPP=ql, out=o_buf[:B])
-            K.w8a8_matmul(aa, ss, *lw["o"], out=bufs["o"], BLOCK_M=None, **kw)
-            K.w8a8_matmul(aa, ss, *lw["gate"], out=bufs["gate"], BLOCK_M=None, **kw)
-            K.w8a8_matmul(aa, ss, *lw["up"], out=bufs["up"], BLOCK_M=None, **kw)
-            gt, up = (bufs["gate"], bufs["up"]) if use_plan else (bufs["gate"][:M], bufs["up"][:M])
-            K.silu_mul_quant_int8(gt, up, q=hq if use_plan else hq[:M], s=hs if use_plan else hs[:M],
-                                  plan=kw.get("plan"), grid_m_max=kw.get("grid_m_max"))
-            h, hsc = (hq, hs) if use_plan else (hq[:M], hs[:M])
-            K.w8a8_matmul(h, hsc, *lw["down"], out=bufs["down"], BLOCK_M=None, **kw)
+            K.paged_attention(q_buf[:Bg, :qg], kc, vc, ks, vs, bt[:Bg], cl[:Bg], qg, QPP=qg,
+                              plan=plan.attn if plan is not None else None, out=o_buf[:Bg, :qg])
+            K.w8a8_matmul(aa, ss, *lw["o"], out=bufs["o"][:Mg], BLOCK_M=None, **kw)
+            K.w8a8_matmul(aa, ss, *lw["gate"], out=bufs["gate"][:Mg], BLOCK_M=None, **kw)
+            K.w8a8_matmul(aa, ss, *lw["up"], out=bufs["up"][:Mg], BLOCK_M=None, **kw)
+            K.silu_mul_quant_int8(bufs["gate"][:Mg], bufs["up"][:Mg], q=hq[:Mg], s=hs[:Mg], **kw)
+            K.w8a8_matmul(hq[:Mg], hs[:Mg], *lw["down"], out=bufs["down"][:Mg], BLOCK_M=None, **kw)
+
+    def rows_computed(Mg, M, plan_mode):
+        """Token rows the qkv GEMM computes for active M on a grid of Mg rows (the tile the
+        library resolves for that call; plan-mode chunks past M exit without computing)."""
+        bm = K.KernelInfo(0, 1 | (16 if plan_mode else 0), Mg, QKV, HID, 0, 0, 4, 0).config["block_m"]
+        return bm * -(-M // bm) if plan_mode else bm * -(-Mg // bm)
 
     rng = random.Random(0)
     trace = [(rng.randint(1, B_MAX), rng.choice(KS)) for _ in range(args.trace)]
-    for B in (1, B_MAX):
-        for k in KS:
-            step(B, k + 1, False)
-    plan.set(B_MAX, QL_MAX)
-    graph = capture(lambda: step(B_MAX, QL_MAX, True))
+    shapes = sorted(set(trace))
+    for B, k in shapes:  # warm every exact shape (also sizes the shared workspace)
+        step(B, k + 1)
+    torch.cuda.synchronize()
 
-    # Plan-graph replay latency per step (host perf_counter around replay + sync, as the
-    # reference's graph bench does), and eager launches of the same steps.
-    lat_plan, lat_eager = [], []
-    for B, k in trace:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        plan.set(B, k + 1)
-        graph.replay()
-        torch.cuda.synchronize()
-        lat_plan.append((time.perf_counter() - t0) * 1e3)
+    def timed(run):
+        lat = []
+        for B, k in trace:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            run(B, k + 1)
+            torch.cuda.synchronize()
+            lat.append((time.perf_counter() - t0) * 1e3)
+        return lat
+
+    res = {}
+    # eager (a fifth of the trace: launch-bound on the host)
+    lat = []
     for B, k in trace[: max(20, args.trace // 5)]:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        step(B, k + 1, False)
+        step(B, k + 1)
         torch.cuda.synchronize()
-        lat_eager.append((time.perf_counter() - t0) * 1e3)
+        lat.append((time.perf_counter() - t0) * 1e3)
+    res["eager"] = lat
+    # allshapes
+    per_shape = {bk: capture(lambda bk=bk: step(bk[0], bk[1] + 1)) for bk in shapes}
+    res["allshapes"] = timed(lambda B, ql: per_shape[(B, ql - 1)].replay())
+    del per_shape
+    # maxpad
+    gmax = capture(lambda: step(B_MAX, QL_MAX))
+    res["maxpad"] = timed(lambda B, ql: gmax.replay())
+    del gmax
+    # one plan graph at the maximum grid
+    plan1 = Plan("cuda")
+    plan1.set(B_MAX, QL_MAX)
+    gplan = capture(lambda: step(B_MAX, QL_MAX, plan1))
+
+    def run_plan(B, ql):
+        plan1.set(B, ql)
+        gplan.replay()
+    res["plan"] = timed(run_plan)
+    # bucketed plan graphs
+    t0 = time.perf_counter()
+    gset = PlanGraphSet(step, B_MAX, [k + 1 for k in KS])
+    build_s = time.perf_counter() - t0
+    res["bucketed"] = timed(gset.replay)
+
     tokens = sum(B * (k + 1) for B, k in trace)
-    log(f"plan graph: P50 {statistics.median(lat_plan):.3f} ms over {len(trace)} steps")
-    return dict(steps=len(trace), plan_p50_ms=statistics.median(lat_plan),
-                plan_p99_ms=sorted(lat_plan)[int(0.99 * (len(lat_plan) - 1))],
-                plan_tokens_per_s=tokens / (sum(lat_plan) * 1e-3),
-                eager_p50_ms=statistics.median(lat_eager))
+    out = dict(steps=len(trace), bucketed_graphs=len(gset.graphs), bucketed_build_s=build_s,
+               allshapes_graphs=len(shapes))
+    for name, lat in res.items():
+        out[f"{name}_p50_ms"] = statistics.median(lat)
+        out[f"{name}_p99_ms"] = sorted(lat)[int(0.99 * (len(lat) - 1))]
+        if name != "eager":
+            out[f"{name}_tokens_per_s"] = tokens / (sum(lat) * 1e-3)
+    # padding waste in token rows per step (qkv GEMM; every GEMM of a step shares its grid)
+    waste = dict(eager=0.0, maxpad=0.0, plan=0.0, bucketed=0.0)
+    for B, k in trace:
+        M = B * (k + 1)
+        waste["eager"] += rows_computed(M, M, False) - M
+        waste["maxpad"] += rows_computed(M_MAX, M, False) - M
+        waste["plan"] += rows_computed(M_MAX, M, True) - M
+        waste["bucketed"] += rows_computed(gset.bucket(B) * (k + 1), M, True) - M
+    torch.cuda.synchronize()
+    for name, v in waste.items():
+        out[f"{name}_pad_rows_per_step"] = v / len(trace)
+    out["allshapes_pad_rows_per_step"] = out["eager_pad_rows_per_step"]
+    log(f"plan graphs: P50 plan {out['plan_p50_ms']:.3f} / bucketed {out['bucketed_p50_ms']:.3f} / "
+        f"allshapes {out['allshapes_p50_ms']:.3f} / maxpad {out['maxpad_p50_ms']:.3f} / "
+        f"eager {out['eager_p50_ms']:.3f} ms")
+    return out
 
 
 def cpu_baseline(args, M: int, seconds: float):

@@ -6,7 +6,9 @@ stream order.  One shared workspace per device serves every call on one stream; 
 other streams that may overlap should pass their own (``Workspace(device)``).
 
 Growing a workspace allocates, so it is refused while a graph is being captured: warm up
-(run each shape once) before capture, as the reference's graph bench does.
+(run each shape once) before capture, as the reference's graph bench does.  A buffer that is
+outgrown is kept alive (never freed) rather than released: graphs captured before the growth
+still point at it, and since every kernel leaves its counters at zero, they stay valid.
 """
 from __future__ import annotations
 
@@ -19,6 +21,7 @@ class Workspace:
     def __init__(self, device, nbytes: int = 0):
         self.device = torch.device(device)
         self._buf = None
+        self._retired = []  # outgrown buffers, still referenced by graphs captured earlier
         self._lock = threading.Lock()
         if nbytes:
             self.ensure(nbytes)
@@ -39,6 +42,8 @@ class Workspace:
                             f"specq workspace must grow to {nbytes} bytes during graph capture; "
                             "run the same call once before capturing")
                     size = max(nbytes, 2 * (self._buf.numel() if self._buf is not None else 0), 1 << 20)
+                    if self._buf is not None:
+                        self._retired.append(self._buf)
                     # Ordered after the work already queued on the current stream.
                     self._buf = torch.zeros(size, dtype=torch.uint8, device=self.device)
         return (self._buf.data_ptr(), self._buf.numel())

@@ -106,3 +106,78 @@ def test_plan_graph_replays_every_shape_bit_exact():
         assert torch.equal(o_buf[:B, :ql], ref_o), f"attention differs at B={B} k={k}"
         assert bool((o_buf[B:] == 0).all()) and bool((o_buf[:B, ql:] == 0).all())
         assert torch.equal(hq[:M], ref_h[0]) and torch.equal(hs[:M], ref_h[1])
+
+
+def test_bucketed_plan_graphs_replay_bit_exact():
+    # PlanGraphSet: one plan graph per (B bucket, q_len), each with the tile its row count
+    # gets.  Every replay must equal eager bit for bit and leave rows past M untouched.  The
+    # second half of the trace replays back to back without host syncs (outputs copied out on
+    # the stream), so the plan's host slots are reused while earlier copies may still pend.
+    from specq.plan import PlanGraphSet
+
+    layers = build_stack()
+    x_in = [t.to(DEV) for t in gen.w8a8_acts(M_MAX, HID, seed=17)]
+    q_buf = gen.queries(B_MAX, QL_MAX, H, D, seed=18).to(DEV)
+    bufs = {n: torch.zeros(M_MAX, N, device=DEV, dtype=torch.float16)
+            for n, N in (("qkv", QKV), ("o", HID), ("gate", FF), ("up", FF), ("down", HID))}
+    o_buf = torch.zeros_like(q_buf)
+    hq = torch.zeros(M_MAX, FF, device=DEV, dtype=torch.int8)
+    hs = torch.zeros(M_MAX, device=DEV, dtype=torch.float32)
+
+    def step(Bg, qg, plan=None):
+        Mg = Bg * qg
+        kw = dict(plan=plan.gemm, grid_m_max=Mg) if plan is not None else {}
+        a, sa = x_in[0][:Mg], x_in[1][:Mg]
+        for lw in layers:
+            K.w8a8_matmul(a, sa, *lw["qkv"], out=bufs["qkv"][:Mg], BLOCK_M=None, **kw)
+            kc, vc, ks, vs, bt, cl = lw["kv"]
+            K.paged_attention(q_buf[:Bg, :qg], kc, vc, ks, vs, bt[:Bg], cl[:Bg], qg, QPP=qg,
+                              plan=plan.attn if plan is not None else None, out=o_buf[:Bg, :qg])
+            K.w8a8_matmul(a, sa, *lw["o"], out=bufs["o"][:Mg], BLOCK_M=None, **kw)
+            K.w8a8_matmul(a, sa, *lw["gate"], out=bufs["gate"][:Mg], BLOCK_M=None, **kw)
+            K.w8a8_matmul(a, sa, *lw["up"], out=bufs["up"][:Mg], BLOCK_M=None, **kw)
+            K.silu_mul_quant_int8(bufs["gate"][:Mg], bufs["up"][:Mg], q=hq[:Mg], s=hs[:Mg], **kw)
+            K.w8a8_matmul(hq[:Mg], hs[:Mg], *lw["down"], out=bufs["down"][:Mg], BLOCK_M=None, **kw)
+
+    note("bucketed graphs: capture")
+    gset = PlanGraphSet(step, B_MAX, [k + 1 for k in KS])
+    assert gset.buckets == [1, 2, 3, 4, 6, 8] and len(gset.graphs) == 24
+
+    rng = random.Random(1)
+    trace = [(rng.randint(1, B_MAX), rng.choice(KS)) for _ in range(20)] + [(B_MAX, 8), (1, 0), (3, 2)]
+    refs = []
+    for B, k in trace:
+        ql = k + 1
+        M = B * ql
+        step(B, ql)
+        torch.cuda.synchronize()
+        refs.append(({n: t[:M].clone() for n, t in bufs.items()}, o_buf[:B, :ql].clone(), hq[:M].clone()))
+
+    def check(i, got, B, ql):
+        M = B * ql
+        ref, ref_o, ref_h = refs[i]
+        for n in bufs:
+            assert torch.equal(got[n][:M], ref[n]), f"{n} differs at B={B} q_len={ql} (replay {i})"
+            assert bool((got[n][M:] == 0).all()), f"{n} wrote inactive rows at B={B} q_len={ql}"
+        assert torch.equal(got["o_buf"][:B, :ql], ref_o), f"attention differs at B={B} q_len={ql}"
+        assert bool((got["o_buf"][B:] == 0).all()) and bool((got["o_buf"][:B, ql:] == 0).all())
+        assert torch.equal(got["hq"][:M], ref_h)
+
+    half = len(trace) // 2
+    for i, (B, k) in enumerate(trace[:half]):  # synchronised replays
+        note(f"bucketed replay {i}: B={B} k={k}")
+        for t in list(bufs.values()) + [o_buf, hq, hs]:
+            t.zero_()
+        gset.replay(B, k + 1)
+        torch.cuda.synchronize()
+        check(i, dict(bufs, o_buf=o_buf, hq=hq), B, k + 1)
+    note("bucketed replays back to back")
+    snaps = []
+    for B, k in trace[half:]:  # no host sync between replays: snapshots taken on the stream
+        for t in list(bufs.values()) + [o_buf, hq, hs]:
+            t.zero_()
+        gset.replay(B, k + 1)
+        snaps.append(dict({n: t.clone() for n, t in bufs.items()}, o_buf=o_buf.clone(), hq=hq.clone()))
+    torch.cuda.synchronize()
+    for j, ((B, k), got) in enumerate(zip(trace[half:], snaps)):
+        check(half + j, got, B, k + 1)
