@@ -250,7 +250,7 @@ int specq_silu_mul_quant_int8(const void* gate, int64_t ld_gate, const void* up,
  * compiled-kernel metadata ck.n_regs / ck.n_spills / ck.metadata.shared, regs.py:29-32).
  * kind: 0 = W8A8 (weight layout in `variant`: 0 row-major, 1 packed, 2 the packed INT4 weight
  * of W4A8), 1 = W4A16 (layout in
- * `variant`), 2 = paged attention (D in `variant`).  For the GEMMs, `variant` | 16 describes a
+ * `variant`), 2 = paged attention (D in `variant`, | 1 << 16 for fp32 K/V scales).  For the GEMMs, `variant` | 16 describes a
  * call made with a plan (m_grid is then grid_m_max).
  * ------------------------------------------------------------------------------------- */
 typedef struct specq_kernel_attrs {

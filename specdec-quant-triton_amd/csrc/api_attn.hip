@@ -1,4 +1,6 @@
 // C ABI for the INT8 paged verification attention: validation, grid, workspace and launch.
+#include <algorithm>
+
 #include "api_common.hpp"
 #include "paged_attn.hpp"
 
@@ -27,33 +29,37 @@ const void* attn_fn(int D, int rb, int fp32) {
   return nullptr;
 }
 
-// 512-token sub-splits per split: 1 until the block table holds more than kAttnMergeMax of them.
-int split_sub_for(int max_pages, int PAGE) {
-  const int64_t subs = ((int64_t)max_pages * PAGE + kAttnSplitTokens - 1) / kAttnSplitTokens;
-  return subs <= kAttnMergeMax ? 1 : (int)((subs + kAttnMergeMax - 1) / kAttnMergeMax);
-}
-
-int n_splits_for(int max_pages, int PAGE) {
+// grid.x: the most splits a sequence of at most max_pages * PAGE tokens is cut into when at
+// least `pairs_min` (sequence, KV head) pairs are active (fewer pairs never means fewer splits).
+int n_splits_for(int max_pages, int PAGE, int pairs_min, int target) {
   const int64_t tokens = (int64_t)max_pages * PAGE;
-  const int64_t per = (int64_t)kAttnSplitTokens * split_sub_for(max_pages, PAGE);
-  const int ns = (int)((tokens + per - 1) / per);
-  return ns > 0 ? ns : 1;
+  const int n_units = (int)((tokens + kAttnUnit - 1) / kAttnUnit);
+  int ns = 1;
+  for (int n = 1; n <= n_units; ++n) {
+    const int u = attn_split_units(n * kAttnUnit, pairs_min, target);
+    ns = std::max(ns, ceil_div(n, u));
+  }
+  return ns;
 }
 
 }  // namespace
 
-int attn_attrs(int D, int rows, specq_kernel_attrs* out) {
+// `variant` is the head dim, | kAttrsScaleFp32 for fp32 K/V scales.
+int attn_attrs(int variant, int rows, specq_kernel_attrs* out) {
+  const bool fp32 = (variant & kAttrsScaleFp32) != 0;
+  const int D = variant & ~kAttrsScaleFp32;
   SPECQ_REQUIRE(rows >= 1 && rows <= 64, SPECQ_ENOTSUP, "paged_attn: %d packed rows (1..64 supported)", rows);
   const int rb = ceil_div(rows, 16);
-  const void* fn = attn_fn(D, rb, 0);
+  const void* fn = attn_fn(D, rb, fp32 ? 1 : 0);
   SPECQ_REQUIRE(fn != nullptr, SPECQ_ENOTSUP, "paged_attn: head_dim %d not supported", D);
   hipFuncAttributes fa;
   if (hipFuncGetAttributes(&fa, fn) != hipSuccess) return fail(SPECQ_EIO, "paged_attn: hipFuncGetAttributes failed");
-  snprintf(out->name, sizeof(out->name), "specq::paged_attn_kernel<%d,%d,half>", D, rb);
+  // The name carries the template arguments exactly as profilers print the kernel symbol.
+  snprintf(out->name, sizeof(out->name), "specq::paged_attn_kernel<%d, %d, %s>", D, rb, fp32 ? "float" : "_Float16");
   out->num_regs = fa.numRegs;
   out->lds_bytes = (int)fa.sharedSizeBytes;
   out->scratch_bytes = (int)fa.localSizeBytes;
-  out->threads = kAttnWaves * 64;
+  out->threads = kAttnThreads;
   out->block_m = rb * 16;
   return SPECQ_OK;
 }
@@ -69,7 +75,9 @@ extern "C" size_t specq_paged_attn_workspace_size(int B_grid, int H, int H_KV, i
   const int rows = ceil_div(QPP * G, 16) * 16;
   const int n_qc = ceil_div(ql_grid, QPP);
   const int64_t progs = (int64_t)B_grid * H_KV * n_qc;
-  const int ns = n_splits_for(max_pages, PAGE);
+  if ((int64_t)max_pages * PAGE > kAttnMaxTokens) return 0;
+  // Plan-mode bound: at least one active sequence.
+  const int ns = n_splits_for(max_pages, PAGE, H_KV, device_cus());
   if (ns <= 1) return 0;
   // Sized for D = 128 (the largest supported head dimension).
   const size_t part = (size_t)progs * ns * rows * (128 + 2) * 4;
@@ -91,6 +99,9 @@ extern "C" int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64
   SPECQ_REQUIRE(D == 64 || D == 128, SPECQ_ENOTSUP, "paged_attn: head_dim %d (64 or 128 supported)", D);
   SPECQ_REQUIRE(PAGE > 0 && PAGE % 16 == 0, SPECQ_ENOTSUP, "paged_attn: PAGE=%d must be a multiple of 16", PAGE);
   SPECQ_REQUIRE(max_pages > 0, SPECQ_EINVAL, "paged_attn: empty block table");
+  SPECQ_REQUIRE((int64_t)max_pages * PAGE <= kAttnMaxTokens, SPECQ_ENOTSUP,
+                "paged_attn: block table of %lld tokens exceeds %lld", (long long)max_pages * PAGE,
+                (long long)kAttnMaxTokens);
   SPECQ_REQUIRE(QPP > 0, SPECQ_EINVAL, "paged_attn: QPP=%d", QPP);
   const int G = H / H_KV;
   SPECQ_REQUIRE(QPP * G <= 64, SPECQ_ENOTSUP, "paged_attn: QPP*G=%d packed rows exceed 64", QPP * G);
@@ -111,7 +122,9 @@ extern "C" int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64
   SPECQ_REQUIRE(fn != nullptr, SPECQ_ENOTSUP, "paged_attn: no kernel for D=%d rows=%d", D, QPP * G);
   const int n_qc = ceil_div(plan ? ql_grid : q_len, QPP);
   if (n_qc == 0) return SPECQ_OK;
-  const int ns = n_splits_for(max_pages, PAGE);
+  const int target = device_cus();
+  // Eager calls know the active sequences; a plan may activate as few as one.
+  const int ns = n_splits_for(max_pages, PAGE, (plan ? 1 : std::max(n_seqs, 1)) * H_KV, target);
   const int64_t progs = (int64_t)B_grid * H_KV * n_qc;
   const int rows = rb * 16;
   size_t need = 0;
@@ -131,12 +144,12 @@ extern "C" int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64
   p.out = (_Float16*)out; p.s_ob = s_ob; p.s_ot = s_ot; p.s_oh = s_oh;
   p.plan = plan; p.B_grid = B_grid; p.n_seqs = plan ? B_grid : n_seqs; p.q_len = plan ? ql_grid : q_len;
   p.ql_grid = ql_grid; p.G = G; p.QPP = QPP; p.n_qc = n_qc; p.H_KV = H_KV; p.PAGE = PAGE; p.n_splits = ns;
-  p.split_sub = split_sub_for(max_pages, PAGE);
+  p.target_wgs = target;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   p.counters = need ? (int32_t*)workspace : nullptr;
   p.part = need ? (float*)((char*)workspace + kCounterBytes) : nullptr;
   void* args[] = {&p};
-  hipError_t e = hipLaunchKernel(fn, dim3(ns, H_KV * n_qc, B_grid), dim3(kAttnWaves * 64), args, 0,
+  hipError_t e = hipLaunchKernel(fn, dim3(ns, H_KV * n_qc, B_grid), dim3(kAttnThreads), args, 0,
                                  (hipStream_t)stream);
   if (e != hipSuccess) {
     set_error("paged_attn: hipLaunchKernel failed: %s", hipGetErrorString(e));

@@ -28,6 +28,8 @@ inline int fail(int code, const char* what) {
 
 // Flag in the `variant` of a GEMM resource query: the call ran with a plan (tile rules differ).
 constexpr int kAttrsPlan = 16;
+// Flag in the `variant` of an attention resource query: fp32 K/V scales (else fp16).
+constexpr int kAttrsScaleFp32 = 1 << 16;
 
 // Every workspace starts with a fixed counter region (zero between calls), then scratch.
 constexpr size_t kCounterBytes = 256 * 1024;

@@ -176,6 +176,51 @@ void ws_auto_tiles(int rows, int m_chunks, int N, int K, double wb, int bnsel_fi
 static_assert(W8A8BnSel<0>::KW == 4 && W8A8BnSel<1>::KW == 2 && W8A8BnSel<2>::KW == 1 && W8A8BnSel<3>::KW == 1,
               "kw_of_sel mirrors the tile table");
 
+// Eager tile choice over the token-tile depth as well: M is cut into c = 1..6 chunks of
+// mt = ceil(rows16 / c) 16-row tiles, and each (mt, channel block, split count) is priced by
+// a model fitted to a sweep of 3,600 measured tiles (qkv, o, gate_up, down, gate, k/v at
+// M = 17..300; mean regret 0.85% against the best measured tile, where a single chunk over
+// all of M lost up to 48% at M >= 128):
+//   t = max(rounds * (BN * wb + rows) * K / s / 45 GB/s, N * wb * K / 6 TB/s) + 1 us
+//       (+ 2 us and the INT32 partial tiles at 2 TB/s when s > 1),
+// with rounds = ceil(workgroups / CUs): a CU pulls its workgroups' activation chunks and
+// weight tiles at ~45 GB/s, and the weight re-reads of later M chunks come from L2 / MALL.
+// 16-row chunks run on the direct-activation kernel, measured fast only with 16-channel
+// blocks, no split and one round of workgroups.
+void w8a8_auto_tiles(int M, int N, int K, double wb, int bnsel_fixed, int splits_fixed, int* mt_out, int* bnsel,
+                     int* splits) {
+  const int cus = device_cus();
+  const int rows16 = ceil_div(std::max(M, 1), 16);
+  const int ksteps = ceil_div(K, 64), kq = ceil_div(ksteps, 4);
+  double best_t = 0;
+  int best_mt = -1, best_sel = 2, best_s = 1, last_mt = -1;
+  const int max_c = std::max(6, ceil_div(rows16, kW8A8MaxMt));  // past 6 chunks only when M needs it
+  for (int c = 1; c <= max_c; ++c) {
+    const int mt = ceil_div(rows16, c);
+    if (mt == last_mt || mt > kW8A8MaxMt) continue;
+    last_mt = mt;
+    const int chunks = ceil_div(rows16, mt), rows = mt * 16;
+    for (int sel = 0; sel < 4; ++sel) {
+      if (bnsel_fixed >= 0 && sel != bnsel_fixed) continue;
+      const int bn = bn_of_sel(sel);
+      const int cand[3] = {splits_fixed > 0 ? splits_fixed : 1, 2, 4};
+      for (int ci = 0; ci < (splits_fixed > 0 ? 1 : 3); ++ci) {
+        int s = std::min(cand[ci], kq);
+        s = ceil_div(K, ceil_div(kq, s) * 256);  // split count after whole-chunk boundaries
+        const int64_t wgs = (int64_t)ceil_div(N, bn) * s * chunks;
+        if (mt == 1 && (sel != 0 || s != 1 || wgs > cus)) continue;
+        const double rounds = (double)ceil_div((int)wgs, cus);
+        double t = std::max(rounds * (bn * wb + rows) * K / s / 45e3, N * wb * K / 6e6) + 1.0;
+        if (s > 1) t += 2.0 + (double)s * rows * chunks * N * 8 / 2e6;
+        if (best_mt < 0 || t < best_t) { best_t = t; best_mt = mt; best_sel = sel; best_s = s; }
+      }
+    }
+  }
+  *mt_out = best_mt;
+  *bnsel = best_sel;
+  *splits = best_s;
+}
+
 // Resolve the kernel and its tiles.  `vec` is the operand alignment (16 when unknown),
 // `layout` 0 = row-major weight, 1 = packed fragments.
 int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k,
@@ -184,8 +229,16 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   SPECQ_REQUIRE(block_n == 0 || block_n == 16 || block_n == 32 || block_n == 64 || block_n == 128, SPECQ_ENOTSUP,
                 "w8a8: BLOCK_N=%d must be 16, 32, 64 or 128", block_n);
   const int rows16 = ceil_div(m_grid > 0 ? m_grid : 1, 16);
+  const int want = block_n > 0 ? (block_n == 16 ? 0 : (block_n == 32 ? 1 : (block_n == 64 ? 2 : 3))) : -1;
+  const int path = g_w8a8_path.load();
+  // Eager calls with an automatic BLOCK_M on the streaming kernels choose the token-tile depth,
+  // channel block and split count together.
+  const bool joint = block_m <= 0 && !plan_mode && vec == 16 && path == 0 && rows16 > 1;
+  int joint_sel = -1, joint_splits = 1;
   int mt;
-  if (block_m > 0) {
+  if (joint) {
+    w8a8_auto_tiles(m_grid, N, K, layout == 2 ? 0.5 : 1.0, want, split_k, &mt, &joint_sel, &joint_splits);
+  } else if (block_m > 0) {
     SPECQ_REQUIRE(block_m % 16 == 0 && block_m <= 16 * kW8A8MaxMt, SPECQ_ENOTSUP,
                   "w8a8: BLOCK_M=%d must be a multiple of 16 and at most %d", block_m, 16 * kW8A8MaxMt);
     mt = block_m / 16;
@@ -198,7 +251,6 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
     const int chunks = ceil_div(rows16, cap);
     mt = ceil_div(rows16, chunks);
   }
-  const int path = g_w8a8_path.load();
   int family;
   if (vec != 16) family = kLegacy;
   else if (path == kLegacy && layout == 0) family = kLegacy;
@@ -209,8 +261,10 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   int nw = 4, rw = 1, bnsel = 2, ws_splits = 1;
   const void* fn = nullptr;
   if (family == kRk || family == kWs) {
-    const int want = block_n > 0 ? (block_n == 16 ? 0 : (block_n == 32 ? 1 : (block_n == 64 ? 2 : 3))) : -1;
-    if (family == kWs) {
+    if (joint) {
+      bnsel = joint_sel;
+      ws_splits = joint_splits;
+    } else if (family == kWs) {
       // With a plan the grid is sized for the largest M, but usually one M-chunk is active.
       const int rows = std::min(std::max(m_grid, 1), mt * 16);
       const int chunks = plan_mode ? 1 : ceil_div(std::max(m_grid, 1), mt * 16);

@@ -8,30 +8,43 @@
 // K/V are int8 [pages, PAGE, H_KV, D] reached through a block table; scales are fp16 or fp32.
 //
 // MI355X schedule:
-//  * One workgroup = (KV split, KV head, query chunk of QPP tokens, sequence).  A split is 512
-//    tokens, or a multiple of 512 for block tables longer than 64 x 512 tokens.
-//    The QPP * G query rows sharing the KV head are packed into RB 16-row blocks, so a fused
-//    verification program reads each K/V byte once for all (k+1) * G rows.
-//  * The four waves take interleaved 32-token chunks of the split (chunk c of the split goes
-//    to wave c % 4) and stream them through a two-deep register pipeline: the K rows, V rows
-//    and scales of the wave's next chunk are in flight while the current one is multiplied.
-//    Every lane loads 16-byte pieces: a K row is 4 lanes x 32 B, a V row 8 lanes x 16 B, one
-//    lane per token for each scale, all through the block table (one 16-token page sub-tile
-//    per page lookup).  Loads are never branched around: tokens past the program's last
-//    visible key read a valid dummy address (finite int8 whose P is 0).
-//  * S^T = K . Q^T on v_mfma_f32_16x16x32_f16 with K as the A-operand (int8 converted to fp16
-//    in registers by exponent injection).  The result lands with the query row in lane % 16,
-//    which is exactly the B-operand layout of the next product, so P never moves between
-//    lanes.  The scales of the chunk pass through a small wave-private LDS staging area so a
-//    lane reads the 4 consecutive tokens it needs with one 16-byte LDS read.
-//  * O^T = V^T . P^T with V^T as the A-operand.  V rows are transposed through a wave-private
-//    LDS tile (4x4 byte transposes with v_perm, dword writes, two dword reads per operand).
-//    The O accumulator then also has the query row in lane % 16, so the online-softmax
-//    rescale is lane local.
-//  * The waves merge in a fixed order through LDS; splits merge in split order through the
-//    workspace (16-byte hand-offs, last workgroup to arrive).  The split boundaries and the
-//    chunk-to-wave assignment are fixed token positions, so a row's result is bit-identical
-//    whether it is computed by a QPP=1 or a fused program, eagerly or from a plan-mode graph.
+//  * One workgroup = (KV split, KV head, query chunk of QPP tokens, sequence).  The QPP * G
+//    query rows sharing the KV head are packed into RB 16-row blocks, so a fused verification
+//    program reads each K/V byte once for all (k+1) * G rows.
+//  * Split length follows the work on the device: a split is a whole number of 128-token
+//    units, as many as make (active sequences) x (KV heads) x (splits) reach the CU count,
+//    between 256 and 4096 tokens and at most 64 splits per sequence (attn_split_units).  It
+//    depends only on the sequence length and the number of active sequences, so a QPP=1 and a
+//    fused program, and an eager and a plan-mode call, cut a sequence at the same tokens.
+//  * Eight waves (two per SIMD, so one wave's MFMA and LDS latencies hide behind the other's
+//    arithmetic) take interleaved 16-token chunks of the split (chunk c, one page sub-tile,
+//    goes to wave c % 8) and stream them through a wave-private LDS ring of 4 slots by LDS DMA
+//    (global_load_lds_dwordx4, 64-bit per-lane addresses through the block table): three
+//    chunks per wave (12 KB, 96 KB per CU) are in flight while one is multiplied, with no
+//    register cost.  K and V rows land in LDS with their 16-byte granules XOR-swizzled by
+//    token, so the MFMA-layout reads below are bank-conflict free.  Every iteration issues
+//    the same DMAs (past the end they read a fixed valid address), so each s_waitcnt vmcnt is
+//    a compile-time constant; the DMAs are inline asm the compiler does not track, so all
+//    waits on them are the kernel's own, and each slot is its own LDS variable.  Page ids of
+//    all of a wave's chunks are fetched with one load per lane at the start and picked out
+//    with v_readlane.
+//  * S^T = K . Q^T on v_mfma_f32_16x16x32_f16 with K (int8 -> fp16 in registers) as the A
+//    operand: operand row x is token perm(x) of the chunk.  The result lands with the query
+//    row in lane % 16, the B-operand layout of the PV product, so P never moves between
+//    lanes.  perm interleaves the token rows so that the two 32-lane halves of each V read
+//    below touch rows of opposite parity (different LDS bank halves).
+//  * O^T = V^T . P^T on v_mfma_f32_16x16x16f16 with V^T as the A operand: lane (i, g) reads
+//    bytes [ND*i, ND*i + ND) of its 4 tokens with 4 LDS reads and transposes them with v_perm
+//    (4x4 byte transposes), so O^T block b row i is d = ND*i + b.  The O accumulator has the
+//    query row in lane % 16, so the online-softmax rescale is lane local; the row max across
+//    the four 16-lane rows uses the gfx950 row-swap permutes.
+//  * The waves merge through LDS: wave v + 4 writes its rescaled O into the idle ring slots
+//    of the pair (v, v + 4), wave v adds it to its own and writes the pair's sum back, then
+//    all threads sum the four pairs in order.  Splits merge in
+//    split order through the workspace (16-byte hand-offs, valid rows only, last workgroup to
+//    arrive).  Split boundaries and the chunk-to-wave assignment are fixed token positions,
+//    so a row's result is bit-identical whether it is computed by a QPP=1 or a fused program,
+//    eagerly or from a plan-mode graph.
 //  * Plan mode reads (n_seqs, q_len) from plan[0..1]; programs for inactive sequences or
 //    query slots return before any load or store.
 #pragma once
@@ -49,23 +62,47 @@ struct AttnParams {
   const int32_t* plan;
   int B_grid, n_seqs, q_len, ql_grid;
   int G, QPP, n_qc, H_KV, PAGE;
-  int n_splits;        // splits the grid covers per program
-  int split_sub;       // 512-token sub-splits per split (longer contexts keep n_splits <= 64)
+  int n_splits;        // grid.x: the most splits any active sequence can have
+  int target_wgs;      // workgroups the split length aims at (the device's CUs)
   float scale_log2;    // sm_scale * log2(e)
   float* part;         // [progs][n_splits][rows][D] unnormalised O, then [progs][n_splits][rows][2] (m, l)
   int32_t* counters;   // [progs]
 };
 
-constexpr int kAttnSplitTokens = 512;  // tokens per workgroup (KV split)
-constexpr int kAttnChunk = 32;         // tokens per wave iteration
-constexpr int kAttnWaves = 4;
-constexpr int kAttnVtPitch = 36;       // bytes per d-row of the transposed V tile (32 tokens + pad)
-constexpr int kAttnMergeMax = 64;      // most splits one program merges (fits the o_lds tile for D >= 64)
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
-template <typename ST>
-__device__ __forceinline__ float load_scale(const void* base, int64_t idx) {
-  return (float)reinterpret_cast<const ST*>(base)[idx];
+constexpr int kAttnChunk = 16;                      // tokens per wave iteration (one page sub-tile)
+constexpr int kAttnWaves = 8;                       // two per SIMD
+constexpr int kAttnThreads = kAttnWaves * 64;
+constexpr int kAttnUnit = kAttnChunk * kAttnWaves;  // 128 tokens: one chunk of every wave
+constexpr int kAttnMinUnits = 2;                    // shortest split: 256 tokens
+constexpr int kAttnMaxUnits = 32;                   // longest split: 4096 tokens (32 page ids per wave)
+constexpr int kAttnMergeMax = 64;                   // most splits one program merges
+constexpr int kAttnRing = 4;                        // LDS chunk slots per wave
+constexpr int64_t kAttnMaxTokens = (int64_t)kAttnUnit * kAttnMaxUnits * kAttnMergeMax;  // 262144
+
+// 128-token units per split for a sequence of L tokens when `pairs` (sequence, KV head) pairs
+// are active and the device has `target` CUs.
+__host__ __device__ inline int attn_split_units(int L, int pairs, int target) {
+  const int n = L > 0 ? (L + kAttnUnit - 1) / kAttnUnit : 1;
+  const int pr = pairs > 0 ? pairs : 1;
+  const int want = pr >= target ? 1 : (target + pr - 1) / pr;
+  int u = (n + want - 1) / want;
+  const int u_min = (n + kAttnMergeMax - 1) / kAttnMergeMax;
+  if (u < u_min) u = u_min;
+  if (u < kAttnMinUnits) u = kAttnMinUnits;
+  if (u > kAttnMaxUnits) u = kAttnMaxUnits;
+  return u;
 }
+
+// Operand row x of a 16-token sub-tile holds token attn_perm(x): rows 4g..4g+3 (one lane group
+// of the S^T result) hold tokens 2e + (g & 1) + 8 (g >> 1), e = 0..3.
+__device__ __forceinline__ int attn_perm(int x) { return 2 * (x & 3) + ((x >> 2) & 1) + 8 * (x >> 3); }
+
+// Granule slot key of chunk token T (GR 16-byte granules per row): granule q of the row is
+// stored in slot q ^ key(T).
+template <int GR>
+__device__ __forceinline__ int attn_key(int T) { return (T + (T >> 3)) & (GR - 1); }
 
 // 4x4 byte transpose: x[j] holds 4 consecutive d bytes of token j; y[d] gets the 4 token bytes of d.
 __device__ __forceinline__ void transpose4x4(const uint32_t (&x)[4], uint32_t (&y)[4]) {
@@ -79,23 +116,64 @@ __device__ __forceinline__ void transpose4x4(const uint32_t (&x)[4], uint32_t (&
   y[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
 }
 
+// Max over the four 16-lane rows of a lane's column (lanes l, l^16, l^32, l^48), with the
+// gfx950 row-swap permutes (no LDS round trip).
+__device__ __forceinline__ float group_max4(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float m1 = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
+  const uint32_t v = __builtin_bit_cast(uint32_t, m1);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
+}
+
+// LDS DMA from 64-bit per-lane addresses (lds wave-uniform): lane l's 16 bytes land at
+// lds + 16 l (dwordx4), its dword at lds + 4 l (dword), its 16-bit value in the low half of the
+// dword at lds + 4 l (ushort).  Issued as inline asm: the compiler then neither counts these
+// loads nor makes LDS accesses wait for them, and every dependence on them is an explicit
+// wait_vmcnt of the kernel (its own loads only ever get stricter waits, which stays correct).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_ptr_t)p;
+}
+__device__ __forceinline__ void dma16_global(const void* src, uint8_t* lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4_global(const void* src, uint8_t* lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void dma2_global(const void* src, uint8_t* lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_ushort %0, off" ::"v"(src), "s"(lds_addr(lds)) : "memory", "m0");
+}
+
 template <int D, int RB, typename ST>
-__global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
-  constexpr int NU = D / 32;          // MFMA K-steps over the head dimension
-  constexpr int ND = D / 16;          // 16-wide d blocks of the output
-  constexpr int DS = D / 4;           // head-dim bytes a lane holds per token (K) or row (Q)
-  constexpr int DB = D / 8;           // V bytes per lane per token
+__global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) {
+  constexpr int NU = D / 32;              // MFMA K-steps over the head dimension
+  constexpr int ND = D / 16;              // 16-row d blocks of O^T = V bytes per lane per token
+  constexpr int GR = D / 16;              // 16-byte granules per K/V row
+  constexpr int KV4 = D / 64;             // 16-byte K granules per lane per token
+  constexpr int DS = D / 4;               // head-dim bytes per lane per token (K) or row (Q)
   constexpr int ROWS = RB * 16;
-  constexpr int IT = kAttnSplitTokens / kAttnChunk / kAttnWaves;  // chunks per wave
-  constexpr int KV4 = D / 64;         // 16-byte K pieces per lane per 16-token sub-tile
-  constexpr int VW = D / 32;          // dwords per lane per V row piece
-  __shared__ __attribute__((aligned(16))) uint8_t vt_lds[kAttnWaves][D * kAttnVtPitch];
-  __shared__ __attribute__((aligned(16))) float sc_lds[kAttnWaves][64];
+  constexpr int NS = kAttnRing;
+  constexpr int NT = kAttnThreads;
+  constexpr int KB = kAttnChunk * D;      // K (or V) bytes per chunk
+  constexpr int SC = 2 * KB;              // offset of the chunk's scale dwords in a slot
+  constexpr int SLOT = 2 * KB + 256;      // K, V, then ks / vs (one dword per lane)
+  constexpr int NDMA = KB / 1024;         // 1 KB DMA instructions for K, and again for V
+  constexpr int NVM = 2 * NDMA + 1;       // DMA instructions per chunk (K, V, scales)
+  constexpr int HALF = 8 * D * 4;         // bytes of 8 fp32 O rows: one half of a merge block
+  static_assert(D == 64 || D == 128, "head dim");
+  static_assert(RB >= 1 && RB <= NS && HALF <= SLOT, "merge block halves fit a ring slot");
+  static_assert((NS - 1) * NVM <= 63, "vmcnt range");
+  // The ring slots are separate LDS variables (see the schedule notes).
+  __shared__ __attribute__((aligned(16))) uint8_t ring0[kAttnWaves][SLOT];
+  __shared__ __attribute__((aligned(16))) uint8_t ring1[kAttnWaves][SLOT];
+  __shared__ __attribute__((aligned(16))) uint8_t ring2[kAttnWaves][SLOT];
+  __shared__ __attribute__((aligned(16))) uint8_t ring3[kAttnWaves][SLOT];
   __shared__ float ml_lds[kAttnWaves][2][ROWS];
-  __shared__ __attribute__((aligned(16))) float o_lds[ROWS][D + 4];
   // Q fragments in MFMA B-operand order: [rb][u][lane] of 16 bytes (zero for padding rows).
   __shared__ __attribute__((aligned(16))) v8h q_lds[RB][NU][64];
   __shared__ int s_last;
+  static_assert(NS == 4, "four ring variables");
 
   const int split = blockIdx.x;
   const int kvh = blockIdx.y / p.n_qc, qc = blockIdx.y % p.n_qc;
@@ -111,18 +189,22 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
   // The block table holds max_pages pages: never look past them.
   const int L = uniform(min(p.ctx_len[b], p.max_pages * p.PAGE));
   const int kv_end = L - q_len + min(qc * p.QPP + p.QPP, q_len);
+  const int split_tokens = kAttnUnit * attn_split_units(L, n_seqs * p.H_KV, p.target_wgs);
   // Split 0 always runs, so rows with no visible key still get their zero output.
-  const int split_tokens = kAttnSplitTokens * p.split_sub;
   if (split > 0 && split * split_tokens >= kv_end) return;
   const int n_active = kv_end > split_tokens ? (kv_end + split_tokens - 1) / split_tokens : 1;
 
-  const int lane = lane_id(), w = wave_id(), g = lane >> 4, r = lane & 15;
+  const int lane = lane_id(), w = uniform(wave_id()), g = lane >> 4, r = lane & 15;
   const int G = p.G;
+  auto ring_of = [&](auto ic, int wave) -> uint8_t* {
+    constexpr int i = decltype(ic)::value;
+    if constexpr (i == 0) return ring0[wave];
+    else if constexpr (i == 1) return ring1[wave];
+    else if constexpr (i == 2) return ring2[wave];
+    else return ring3[wave];
+  };
 
-  // Query rows held by this lane (one per row block): row = rb*16 + r.  Their B-operand
-  // fragments go to LDS once (each wave writes its share of the row blocks) and are read back
-  // per MFMA, which leaves registers for a three-chunk load pipeline.
-  int qpos[RB];
+  int qpos[RB];  // absolute position of the query row this lane holds in each row block
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int row = rb * 16 + r;
@@ -130,7 +212,6 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
     const bool valid = (row < p.QPP * G) && (qi < q_len);
     qpos[rb] = valid ? (L - q_len + qi) : -1;
   }
-
   float m_run[RB], l_run[RB];
   v4f acc[RB][ND];
 #pragma unroll
@@ -141,234 +222,245 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
     for (int db = 0; db < ND; ++db) acc[rb][db] = v4f{0.f, 0.f, 0.f, 0.f};
   }
 
-  uint8_t* vt = vt_lds[w];
-  float* scw = sc_lds[w];
-  const int64_t kv_head_off = (int64_t)kvh * p.s_kh;
-  const int64_t sc_head_off = (int64_t)kvh * p.s_sh;
+  // This wave's chunks of the split: chunk `it` is the 16 tokens from s0 + 16 (w + 8 it), one
+  // page sub-tile.
+  const int s0 = split * split_tokens;
+  const int s1 = min(s0 + split_tokens, kv_end);
+  const int n_it = uniform(s1 > s0 + kAttnChunk * w ? (s1 - s0 - kAttnChunk * w + kAttnUnit - 1) / kAttnUnit : 0);
+  auto chunk_t0 = [&](int it) { return s0 + kAttnChunk * (w + kAttnWaves * it); };
   const int32_t* bt_row = p.bt + (int64_t)b * p.s_bt;
-  const int PAGE = p.PAGE;
-
-  // ---- Chunk loads.  Chunk `it` of this wave starts at token t0(it); its two 16-token
-  // sub-tiles each lie in one page.  Masked tokens (at or past kv_end) read the first bytes of
-  // the cache instead: their int8 K/V are finite, their scores are masked to -inf and their P
-  // is 0, so they add nothing; their scales are zeroed.
-  int sub_base = split * split_tokens;  // first token of the current 512-token sub-split
-  auto chunk_t0 = [&](int it) { return sub_base + (it * kAttnWaves + w) * kAttnChunk; };
-  // Register double buffer of the raw chunk bytes: K pieces, V pieces, one scale per lane
-  // (lane l < 32: ks of token l; lane >= 32: vs of token l - 32).
-  constexpr int NB = 2;  // chunks in the register pipeline
-  v4i kbuf[NB][2][KV4];
-  uint32_t vbuf[NB][4][VW];
-  float sbuf[NB];
-  // Pages of the wave's 2 * IT sub-tiles in the current 512-token sub-split, looked up together
-  // at its start (one block-table round trip instead of one per chunk).
-  int pages[IT][2];
-  auto lookup_pages = [&]() __attribute__((always_inline)) {
+  // Page of the wave's chunk `lane` (n_it <= 32).
+  int page_v;
+  {
+    const int ts = chunk_t0(lane);
+    page_v = (lane < n_it && ts < kv_end) ? bt_row[ts / p.PAGE] : 0;
+  }
+  // Q fragments: thread t stages fragments t, t + NT, ... of [rb][u][lane].
+  constexpr int QF = (RB * NU * 64 + NT - 1) / NT;
+  v8h qtmp[QF];
 #pragma unroll
-    for (int it = 0; it < IT; ++it)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int ts = chunk_t0(it) + 16 * j;
-        pages[it][j] = ts < kv_end ? bt_row[ts / PAGE] : 0;
-      }
-  };
-  auto load_chunk = [&](auto bic, auto itc) __attribute__((always_inline)) {
-    constexpr int bi = decltype(bic)::value;
-    constexpr int it = decltype(itc)::value;
-    const int t0 = chunk_t0(it);
-    int64_t pbase[2];  // element offset of (page, token 0 of the sub-tile, this KV head) in the cache
-    int64_t sbase[2];  // element offset of the sub-tile's first scale
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int ts = t0 + 16 * j;
-      pbase[j] = (int64_t)pages[it][j] * p.s_kp + (int64_t)(ts % PAGE) * p.s_ko + kv_head_off;
-      sbase[j] = (int64_t)pages[it][j] * p.s_sp + (int64_t)(ts % PAGE) * p.s_so + sc_head_off;
-    }
-    // K: lane (r, g) holds bytes [DS*g, DS*g + DS) of token 16j + r.
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const bool ok = t0 + 16 * j + r < kv_end;
-      const int8_t* src = p.kc + (ok ? pbase[j] + (int64_t)r * p.s_ko + DS * g : 0);
-#pragma unroll
-      for (int h = 0; h < KV4; ++h) kbuf[bi][j][h] = *reinterpret_cast<const v4i*>(src + 16 * h);
-    }
-    // V: lane (tq = lane / 8, dq = lane % 8) holds DB bytes at d = DB*dq of tokens 4tq .. 4tq+3.
-    {
-      const int tq = lane >> 3, dq = lane & 7, j = tq >> 2;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tl = 4 * (tq & 3) + i;  // token within sub-tile j
-        const bool ok = t0 + 16 * j + tl < kv_end;
-        const int8_t* src = p.vc + (ok ? pbase[j] + (int64_t)tl * p.s_ko + DB * dq : 0);
-        if constexpr (VW == 4) {
-          const v4i x = *reinterpret_cast<const v4i*>(src);
-          vbuf[bi][i][0] = (uint32_t)x.x; vbuf[bi][i][1] = (uint32_t)x.y;
-          vbuf[bi][i][2] = (uint32_t)x.z; vbuf[bi][i][3] = (uint32_t)x.w;
-        } else {
-          const v2i x = *reinterpret_cast<const v2i*>(src);
-          vbuf[bi][i][0] = (uint32_t)x.x; vbuf[bi][i][1] = (uint32_t)x.y;
-        }
-      }
-    }
-    // Scales: lane l holds ks (l < 32) or vs (l >= 32) of token l % 32.
-    {
-      const int tl = lane & 31, j = tl >> 4;
-      const bool ok = t0 + tl < kv_end;
-      const int64_t si = ok ? sbase[j] + (int64_t)(tl & 15) * p.s_so : 0;
-      const float x = load_scale<ST>(lane < 32 ? p.ks : p.vs, si);
-      sbuf[bi] = ok ? x : 0.f;
-    }
-  };
-
-  // ---- One chunk: stage V^T and the scales in LDS, S^T, online softmax, O^T += V^T . P^T.
-  auto compute_chunk = [&](auto bic, int it) __attribute__((always_inline)) {
-    constexpr int bi = decltype(bic)::value;
-    const int t0 = chunk_t0(it);
-    // Stage: Vt[d][token] for d in [DB*dq, DB*dq + DB), tokens 4tq..4tq+3; the 64 scales.
-    {
-      const int tq = lane >> 3, dq = lane & 7;
-#pragma unroll
-      for (int cc = 0; cc < DB / 4; ++cc) {
-        uint32_t x[4] = {vbuf[bi][0][cc], vbuf[bi][1][cc], vbuf[bi][2][cc], vbuf[bi][3][cc]};
-        uint32_t y[4];
-        transpose4x4(x, y);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          *reinterpret_cast<uint32_t*>(vt + (DB * dq + 4 * cc + e) * kAttnVtPitch + 4 * tq) = y[e];
-      }
-      scw[lane] = sbuf[bi];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // Scales of the lane's tokens 16j + 4g + i: ks at [0, 32), vs at [32, 64).
-    v4f ksc[2], vsc[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      ksc[j] = *reinterpret_cast<const v4f*>(scw + 16 * j + 4 * g);
-      vsc[j] = *reinterpret_cast<const v4f*>(scw + 32 + 16 * j + 4 * g);
-    }
-    // K fragment u of sub-tile j (8 int8 -> fp16), converted where it is used.
-    auto kfrag = [&](int j, int u) __attribute__((always_inline)) {
-      const v4i& x = kbuf[bi][j][u >> 1];
-      return (u & 1) ? i8x8_to_h8((uint32_t)x.z, (uint32_t)x.w) : i8x8_to_h8((uint32_t)x.x, (uint32_t)x.y);
-    };
-
-    // Every row of the program sees every token of the chunk: no causal mask needed.
-    const bool full = t0 + kAttnChunk - 1 <= L - q_len + qc * p.QPP;
-    v8h pf[RB];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      float s[2][4];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        v4f cs = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int u = 0; u < NU; ++u) cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfrag(j, u), q_lds[rb][u][lane], cs, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int t = t0 + 16 * j + 4 * g + i;
-          const float v = cs[i] * (ksc[j][i] * p.scale_log2);
-          s[j][i] = (full || t <= qpos[rb]) ? v : -INFINITY;
-        }
-      }
-      float cmax = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
-                         fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 16));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 32));
-      const float m_new = fmaxf(m_run[rb], cmax);
-      const float m_safe = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run[rb] - m_safe);
-      float psum = 0.f;
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float pv = fast_exp2(s[j][i] - m_safe);
-          psum += pv;
-          pf[rb][4 * j + i] = (_Float16)(pv * vsc[j][i]);
-        }
-      l_run[rb] = l_run[rb] * alpha + psum;
-      // alpha is exactly 1 for every row whose running max did not grow, so the O rescale is
-      // skipped (bit-identically) unless some row of the wave's block grew, which after the
-      // first chunks is rare; the accumulators then stay in the MFMA's registers.
-      const bool grew = m_new > m_run[rb];
-      m_run[rb] = m_new;
-      if (__builtin_amdgcn_ballot_w64(grew) != 0) {
-#pragma unroll
-        for (int db = 0; db < ND; ++db) acc[rb][db] *= alpha;
-      }
-    }
-
-    // O^T += V^T . P^T  (A-operand: lane (d, g) holds tokens {4g..4g+3, 16+4g..16+4g+3} of d)
-#pragma unroll
-    for (int db = 0; db < ND; ++db) {
-      const uint8_t* vrow = vt + (db * 16 + r) * kAttnVtPitch;
-      const uint32_t v0 = *reinterpret_cast<const uint32_t*>(vrow + 4 * g);
-      const uint32_t v1 = *reinterpret_cast<const uint32_t*>(vrow + 16 + 4 * g);
-      const v8h vf = i8x8_to_h8(v0, v1);
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-        acc[rb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[rb], acc[rb][db], 0, 0, 0);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  };
-
-  // Chunk it + 1 is in flight while chunk it is multiplied; the first sub-split's
-  // page lookups and first loads are issued before the Q fragments are staged, so those
-  // memory round trips overlap.
-  // Q fragments: thread t stages fragments t, t + 256, ... of [rb][u][lane].
-  constexpr int QF = (RB * NU * 64 + 255) / 256;
-  auto q_frag_valid = [&](int f) {
-    const int row = (f / (NU * 64)) * 16 + (f % 64 & 15);
-    return f < RB * NU * 64 && (row < p.QPP * G) && (qc * p.QPP + row / G < q_len);
-  };
-  auto q_frag_src = [&](int f) -> const _Float16* {  // a valid fragment's 8 halves
+  for (int i = 0; i < QF; ++i) {
+    const int f = threadIdx.x + NT * i;
     const int rb = f / (NU * 64), u = (f / 64) % NU, ln = f % 64;
     const int row = rb * 16 + (ln & 15);
     const int qi = qc * p.QPP + row / G;
+    const bool ok = f < RB * NU * 64 && row < p.QPP * G && qi < q_len;
     const int head = kvh * G + row % G;
-    return p.q + (int64_t)b * p.s_qb + (int64_t)qi * p.s_qt + (int64_t)head * p.s_qh + DS * (ln >> 4) + 8 * u;
-  };
-  bool staged = false;
-  for (int sub = 0; sub < p.split_sub && sub_base < kv_end; ++sub, sub_base += kAttnSplitTokens) {
-    lookup_pages();
-    v8h qtmp[QF];
-    if (!staged) {
-#pragma unroll
-      for (int i = 0; i < QF; ++i) {
-        const int f = threadIdx.x + 256 * i;
-        const bool ok = q_frag_valid(f);
-        const v8h x = *reinterpret_cast<const v8h*>(ok ? q_frag_src(f) : p.q);
-        qtmp[i] = ok ? x : v8h{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-    }
-    static_for<0, NB - 1>([&](auto ic) __attribute__((always_inline)) {
-      constexpr int i = decltype(ic)::value;
-      if constexpr (i < IT) load_chunk(std::integral_constant<int, i>{}, std::integral_constant<int, i>{});
-    });
-    if (!staged) {
-      // The Q fragments go to LDS while the first chunks stay in flight (the barrier waits
-      // for LDS only).
-#pragma unroll
-      for (int i = 0; i < QF; ++i) {
-        const int f = threadIdx.x + 256 * i;
-        if (f < RB * NU * 64) (&q_lds[0][0][0])[f] = qtmp[i];
-      }
-      wg_barrier_lds();
-      staged = true;
-    }
-    static_for<0, IT>([&](auto itc) __attribute__((always_inline)) {
-      constexpr int it = decltype(itc)::value;
-      if constexpr (it + NB - 1 < IT)
-        load_chunk(std::integral_constant<int, (it + NB - 1) % NB>{}, std::integral_constant<int, it + NB - 1>{});
-      if (chunk_t0(it) < kv_end) compute_chunk(std::integral_constant<int, it % NB>{}, it);
-    });
+    const _Float16* src = ok ? p.q + (int64_t)b * p.s_qb + (int64_t)qi * p.s_qt + (int64_t)head * p.s_qh + DS * (ln >> 4) + 8 * u
+                             : p.q;
+    const v8h x = *reinterpret_cast<const v8h*>(src);
+    qtmp[i] = ok ? x : v8h{0, 0, 0, 0, 0, 0, 0, 0};
   }
 
-  // ---- Merge the four waves in a fixed order.
+  // Page ids and Q fragments arrive together (one memory round trip); Q goes to LDS before any
+  // DMA is issued, so no LDS store ever waits behind the ring's DMA.
+  wait_vmcnt<0>();
+#pragma unroll
+  for (int i = 0; i < QF; ++i) {
+    const int f = threadIdx.x + NT * i;
+    if (f < RB * NU * 64) (&q_lds[0][0][0])[f] = qtmp[i];
+  }
+
+  const int64_t head_k = (int64_t)kvh * p.s_kh;
+  const int64_t head_s = (int64_t)kvh * p.s_sh;
+  // Chunk-invariant per-lane parts of the DMA addresses: the byte offset of the lane's K/V
+  // granule within the chunk's page sub-tile (DMA i covers chunk tokens 64 i / GR ..), and the
+  // element offset of its scale.  Lanes l < 16 fetch ks of token perm(l), 16 <= l < 32 vs of
+  // token perm(l - 16), lanes 32.. repeat lanes 0..31.
+  int64_t kvoff[NDMA];
+#pragma unroll
+  for (int i = 0; i < NDMA; ++i) {
+    const int gi = 64 * i + lane, T = gi / GR, s = gi % GR;
+    kvoff[i] = (int64_t)T * p.s_ko + 16 * (s ^ attn_key<GR>(T));
+  }
+  const int sc_T = attn_perm(lane & 15);
+  const int64_t sc_off = (int64_t)sc_T * p.s_so * (int64_t)sizeof(ST);
+  const uint8_t* sc_src = reinterpret_cast<const uint8_t*>((lane & 16) ? p.vs : p.ks);
+  // Issue the DMAs of chunk `it` into ring slot SL.  Chunks past the wave's last, and tokens at
+  // or past kv_end, read a fixed valid address instead.
+  auto issue = [&](auto slc, int it) __attribute__((always_inline)) {
+    uint8_t* dst = ring_of(slc, w);
+    const bool real = it < n_it;
+    const int t0 = chunk_t0(it);
+    const int pg = real ? __builtin_amdgcn_readlane(page_v, min(it, 63)) : 0;
+    const int tk = t0 % p.PAGE;
+    const int64_t pb = (int64_t)pg * p.s_kp + (int64_t)tk * p.s_ko + head_k;
+    const int64_t sb = ((int64_t)pg * p.s_sp + (int64_t)tk * p.s_so + head_s) * (int64_t)sizeof(ST);
+    if (real && t0 + kAttnChunk <= kv_end) {
+#pragma unroll
+      for (int i = 0; i < NDMA; ++i) dma16_global(p.kc + pb + kvoff[i], dst + 1024 * i);
+#pragma unroll
+      for (int i = 0; i < NDMA; ++i) dma16_global(p.vc + pb + kvoff[i], dst + KB + 1024 * i);
+      const uint8_t* src = sc_src + sb + sc_off;
+      if constexpr (sizeof(ST) == 4) dma4_global(src, dst + SC);
+      else dma2_global(src, dst + SC);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NDMA; ++i) {
+        const int gi = 64 * i + lane;
+        const bool ok = real && t0 + gi / GR < kv_end;
+        dma16_global(p.kc + (ok ? pb + kvoff[i] : 16 * (gi % GR)), dst + 1024 * i);
+      }
+#pragma unroll
+      for (int i = 0; i < NDMA; ++i) {
+        const int gi = 64 * i + lane;
+        const bool ok = real && t0 + gi / GR < kv_end;
+        dma16_global(p.vc + (ok ? pb + kvoff[i] : 16 * (gi % GR)), dst + KB + 1024 * i);
+      }
+      const bool ok = real && t0 + sc_T < kv_end;
+      const uint8_t* src = sc_src + (ok ? sb + sc_off : 0);
+      if constexpr (sizeof(ST) == 4) dma4_global(src, dst + SC);
+      else dma2_global(src, dst + SC);
+    }
+  };
+
+  // One chunk from ring slot SL: S^T, online softmax, O^T += V^T . P^T.
+  auto compute = [&](auto slc, int it) __attribute__((always_inline)) {
+    const uint8_t* kb = ring_of(slc, w);
+    const uint8_t* vb = kb + KB;
+    const int t0 = chunk_t0(it);
+    // K operands: lane (r, g) holds head-dim bytes [DS*g, DS*g + DS) of token perm(r).
+    v8h kf[NU];
+    {
+      const int T = attn_perm(r), key = attn_key<GR>(T);
+#pragma unroll
+      for (int h = 0; h < KV4; ++h) {
+        const v4i x = *reinterpret_cast<const v4i*>(kb + T * D + 16 * ((g * KV4 + h) ^ key));
+        kf[2 * h] = i8x8_to_h8((uint32_t)x.x, (uint32_t)x.y);
+        kf[2 * h + 1] = i8x8_to_h8((uint32_t)x.z, (uint32_t)x.w);
+      }
+    }
+    // V^T operands: lane (r, g) reads bytes [ND*r, ND*r + ND) of tokens perm(4g + e), operand
+    // slot 4g + e of the 16x16x16 product.
+    uint32_t vx[4][ND / 4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int T = attn_perm(4 * g + e);
+      const uint8_t* src = vb + T * D + 16 * (((ND * r) >> 4) ^ attn_key<GR>(T)) + ((ND * r) & 15);
+      if constexpr (ND == 8) {
+        const v2i x = *reinterpret_cast<const v2i*>(src);
+        vx[e][0] = (uint32_t)x.x;
+        vx[e][1] = (uint32_t)x.y;
+      } else {
+        vx[e][0] = *reinterpret_cast<const uint32_t*>(src);
+      }
+    }
+    // Scales in operand order: dword 4g + e holds ks of token perm(4g + e), dword 16 + 4g + e
+    // its vs (an fp16 scale in the low half); zero V scale for tokens at or past kv_end.
+    float ksc[4], vsc[4];
+    {
+      const v4i kr = *reinterpret_cast<const v4i*>(kb + SC + 16 * g);
+      const v4i vr = *reinterpret_cast<const v4i*>(kb + SC + 64 + 16 * g);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // Vector elements are copied out before the bit casts (a bit cast of a vector-element
+        // expression reads the vector's first element).
+        const int ki = kr[e], vi = vr[e];
+        float kv, vv;
+        if constexpr (sizeof(ST) == 4) {
+          kv = __builtin_bit_cast(float, ki);
+          vv = __builtin_bit_cast(float, vi);
+        } else {
+          kv = (float)__builtin_bit_cast(_Float16, (uint16_t)(ki & 0xFFFF));
+          vv = (float)__builtin_bit_cast(_Float16, (uint16_t)(vi & 0xFFFF));
+        }
+        ksc[e] = kv * p.scale_log2;
+        vsc[e] = (t0 + attn_perm(4 * g + e) < kv_end) ? vv : 0.f;
+      }
+    }
+
+    // S^T of every row block first (RB independent MFMA chains), then the softmax of every
+    // row block, so the chains and the softmax arithmetic of different row blocks interleave.
+    v4f cs[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      v4f c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < NU; ++u) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[u], q_lds[rb][u][lane], c, 0, 0, 0);
+      cs[rb] = c;
+    }
+    // Every row of the program sees every token of the chunk: no causal mask needed.
+    const bool full = t0 + kAttnChunk - 1 <= L - q_len + qc * p.QPP;
+    v4h pf[RB];
+    float alpha[RB];
+    bool grew = false;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      float s[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[e] = cs[rb][e] * ksc[e];
+      if (!full) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (t0 + attn_perm(4 * g + e) > qpos[rb]) s[e] = -INFINITY;
+      }
+      const float m_new = fmaxf(m_run[rb], group_max4(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]))));
+      const float m_safe = (m_new == -INFINITY) ? 0.f : m_new;
+      alpha[rb] = fast_exp2(m_run[rb] - m_safe);
+      float psum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float pv = fast_exp2(s[e] - m_safe);
+        psum += pv;
+        pf[rb][e] = (_Float16)(pv * vsc[e]);
+      }
+      l_run[rb] = l_run[rb] * alpha[rb] + psum;
+      grew |= m_new > m_run[rb];
+      m_run[rb] = m_new;
+    }
+    // alpha is exactly 1 for every row whose running max did not grow, so the O rescale is
+    // skipped (bit-identically) unless some row grew, which after the first chunks is rare.
+    if (__builtin_amdgcn_ballot_w64(grew) != 0) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int db = 0; db < ND; ++db) acc[rb][db] *= alpha[rb];
+    }
+    // V bytes to d-major: vt[db] = the 4 token bytes (operand slots 4g..4g+3) of d = ND*r + db.
+#pragma unroll
+    for (int c = 0; c < ND / 4; ++c) {
+      const uint32_t x[4] = {vx[0][c], vx[1][c], vx[2][c], vx[3][c]};
+      uint32_t y[4];
+      transpose4x4(x, y);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v2h lo, hi;
+        i8x4_to_h2x2(y[e], lo, hi);
+        const v4h vf = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          acc[rb][4 * c + e] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, pf[rb], acc[rb][4 * c + e], 0, 0, 0);
+      }
+    }
+  };
+
+  // Chunk c lives in slot (c + 1) % NS, so the loop body fills slots 0, 1, 2, 3 in order, the
+  // order in which the prologue first touches them.
+  // Prologue: chunks 0 .. NS-2; the barrier makes every wave's Q fragments visible.
+  static_for<0, NS - 1>([&](auto ic) __attribute__((always_inline)) {
+    constexpr int i = decltype(ic)::value;
+    issue(std::integral_constant<int, (i + 1) % NS>{}, i);
+  });
+  wg_barrier_lds();
+  // Steady state: issue chunk it + NS - 1 into the slot chunk it - 1 left, wait for chunk it
+  // (NS - 1 chunks may stay in flight), multiply it.
+  for (int base = 0; base < n_it; base += NS) {
+    static_for<0, NS>([&](auto ic) __attribute__((always_inline)) {
+      constexpr int i = decltype(ic)::value;
+      const int it = base + i;
+      issue(ic, it + NS - 1);
+      wait_vmcnt<(NS - 1) * NVM>();
+      if (it < n_it) compute(std::integral_constant<int, (i + 1) % NS>{}, it);
+    });
+  }
+  // Every DMA has landed before the ring is reused for the merge.
+  wait_vmcnt<0>();
+
+  // ---- Merge the eight waves.  Row statistics first; every wave's O is scaled to the
+  // workgroup's row max.  Wave pair (v, v + 4) shares a merge region: row block rb in ring
+  // slot rb, rows 0-7 in wave v's slot and rows 8-15 in wave v + 4's, granule c of row n at
+  // c ^ n.  Wave v + 4 writes its O, wave v adds it to its own and writes the pair's sum, then
+  // all threads add the four pair sums in pair order.
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     float lr = l_run[rb];
@@ -380,84 +472,129 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
     }
   }
   __syncthreads();
-  float wscale[RB];
+  constexpr int QPR = D / 4;  // 4-float granules per row
+  float wsc[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int row = rb * 16 + r;
     float mx = ml_lds[0][0][row];
 #pragma unroll
     for (int ww = 1; ww < kAttnWaves; ++ww) mx = fmaxf(mx, ml_lds[ww][0][row]);
-    const float ms = (mx == -INFINITY) ? 0.f : mx;
-    wscale[rb] = fast_exp2(m_run[rb] - ms);
+    wsc[rb] = fast_exp2(m_run[rb] - ((mx == -INFINITY) ? 0.f : mx));
   }
-  for (int ww = 0; ww < kAttnWaves; ++ww) {
-    if (w == ww) {
+  const int pr = w & 3;  // the wave pair
+  // O^T rows 4g + e of block db hold d = ND (4g + e) + db: granule (ND / 4)(4g + e) + cc.
+  auto merge_io = [&](auto rbc, bool store) __attribute__((always_inline)) {
+    constexpr int rb = decltype(rbc)::value;
+    float* half0 = reinterpret_cast<float*>(ring_of(rbc, pr));
+    float* half1 = reinterpret_cast<float*>(ring_of(rbc, pr + 4));
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
+    for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int db = 0; db < ND; ++db) {
-          v4f* dst = reinterpret_cast<v4f*>(&o_lds[rb * 16 + r][db * 16 + 4 * g]);
-          const v4f v = acc[rb][db] * wscale[rb];
-          *dst = (ww == 0) ? v : (*dst + v);
+      for (int cc = 0; cc < ND / 4; ++cc) {
+        const int gran = (ND / 4) * (4 * g + e) + cc;
+        float* dst = (r < 8 ? half0 : half1) + (r & 7) * D + 4 * (gran ^ r);
+        v4f* a = &acc[rb][0];
+        if (store) {
+          *reinterpret_cast<v4f*>(dst) = v4f{a[4 * cc][e], a[4 * cc + 1][e], a[4 * cc + 2][e], a[4 * cc + 3][e]};
+        } else {
+          const v4f v = *reinterpret_cast<const v4f*>(dst);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) a[4 * cc + k][e] += v[k];
         }
-    }
-    __syncthreads();
-  }
-  // Row statistics of the workgroup: max and scaled sum, in wave order.
-  if (threadIdx.x < ROWS) {
-    const int row = threadIdx.x;
-    float mx = ml_lds[0][0][row];
+      }
+  };
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int db = 0; db < ND; ++db) acc[rb][db] *= wsc[rb];
+  if (w >= 4) static_for<0, RB>([&](auto rbc) __attribute__((always_inline)) { merge_io(rbc, true); });
+  __syncthreads();
+  if (w < 4) static_for<0, RB>([&](auto rbc) __attribute__((always_inline)) { merge_io(rbc, false); });
+  __syncthreads();
+  if (w < 4) static_for<0, RB>([&](auto rbc) __attribute__((always_inline)) { merge_io(rbc, true); });
+  __syncthreads();
+  auto pair_o = [&](int pp, int row, int c) -> v4f {
+    const int n = row & 15, rb = row >> 4;
+    const int wv = pp + ((n >> 3) << 2);
+    const uint8_t* base = rb == 0 ? ring0[wv] : rb == 1 ? ring1[wv] : rb == 2 ? ring2[wv] : ring3[wv];
+    return *reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(base) + (n & 7) * D + 4 * (c ^ n));
+  };
+  auto row_stats = [&](int row, float& mx, float& l) {
+    mx = ml_lds[0][0][row];
     for (int ww = 1; ww < kAttnWaves; ++ww) mx = fmaxf(mx, ml_lds[ww][0][row]);
     const float ms = (mx == -INFINITY) ? 0.f : mx;
-    float ls = 0.f;
-    for (int ww = 0; ww < kAttnWaves; ++ww) ls += fast_exp2(ml_lds[ww][0][row] - ms) * ml_lds[ww][1][row];
-    ml_lds[0][0][row] = mx;
-    ml_lds[0][1][row] = ls;
+    l = 0.f;
+    for (int ww = 0; ww < kAttnWaves; ++ww) l += fast_exp2(ml_lds[ww][0][row] - ms) * ml_lds[ww][1][row];
+  };
+  constexpr int ITEMS = (ROWS * QPR + NT - 1) / NT;
+  v4f o[ITEMS];
+  bool ivalid[ITEMS];
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it) {
+    const int e = threadIdx.x + NT * it;
+    const int row = e / QPR, c = e % QPR;
+    const int qi = qc * p.QPP + row / G;
+    ivalid[it] = e < ROWS * QPR && row < p.QPP * G && qi < q_len;
+    o[it] = v4f{0.f, 0.f, 0.f, 0.f};
+    if (ivalid[it]) {
+      o[it] = pair_o(0, row, c);
+#pragma unroll
+      for (int pp = 1; pp < 4; ++pp) o[it] += pair_o(pp, row, c);
+    }
   }
-  __syncthreads();
+  typedef _Float16 v4h_t __attribute__((ext_vector_type(4)));
+  auto store_row4 = [&](int e, v4f v) {
+    const int row = e / QPR, d0 = (e % QPR) * 4;
+    const int qi = qc * p.QPP + row / G;
+    const int head = kvh * G + row % G;
+    *reinterpret_cast<v4h_t*>(p.out + (int64_t)b * p.s_ob + (int64_t)qi * p.s_ot + (int64_t)head * p.s_oh + d0) =
+        v4h_t{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+  };
 
   const int prog = (b * p.H_KV + kvh) * p.n_qc + qc;
-  constexpr int DCH = D / 8;  // 8-element chunks per row
   if (n_active == 1) {
-    for (int e = threadIdx.x; e < ROWS * DCH; e += blockDim.x) {
-      const int row = e / DCH, d0 = (e % DCH) * 8;
-      const int qi = qc * p.QPP + row / G;
-      if (!(row < p.QPP * G && qi < q_len)) continue;
-      const int head = kvh * G + row % G;
-      const float l = ml_lds[0][1][row];
-      const float inv = (l == 0.f) ? 0.f : 1.f / l;
-      v8h o;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = (_Float16)(o_lds[row][d0 + i] * inv);
-      *reinterpret_cast<v8h*>(p.out + (int64_t)b * p.s_ob + (int64_t)qi * p.s_ot + (int64_t)head * p.s_oh + d0) = o;
+    for (int it = 0; it < ITEMS; ++it) {
+      if (!ivalid[it]) continue;
+      const int e = threadIdx.x + NT * it;
+      float mx, l;
+      row_stats(e / QPR, mx, l);
+      const float inv = (l == 0.f) ? 0.f : 1.f / l;
+      store_row4(e, o[it] * inv);
     }
     return;
   }
 
-  // ---- Cross-split merge: publish this split (16 bytes per lane), the last to arrive combines
-  // the splits in split order.
+  // ---- Cross-split merge: publish this split's valid rows (16 bytes per lane), the last to
+  // arrive combines the splits in split order.
   const int64_t prog_base = (int64_t)prog * p.n_splits;
   const int64_t n_o = (int64_t)gridDim.y * gridDim.z * p.n_splits * ROWS * D;  // floats of the O region
   const rsrc_t ors = make_rsrc(p.part + prog_base * ROWS * D, (uint32_t)(p.n_splits * ROWS * D * 4));
   float* mlpart = p.part + n_o;
-  for (int e = threadIdx.x; e < ROWS * D / 4; e += blockDim.x) {
-    const int row = e / (D / 4), d = (e % (D / 4)) * 4;
-    const v4f v = *reinterpret_cast<const v4f*>(&o_lds[row][d]);
-    publish16(ors, (uint32_t)(((split * ROWS + row) * D + d) * 4), __builtin_bit_cast(v4i, v));
-  }
+#pragma unroll
+  for (int it = 0; it < ITEMS; ++it)
+    if (ivalid[it]) {
+      const int e = threadIdx.x + NT * it;
+      publish16(ors, (uint32_t)((split * ROWS * QPR + e) * 16), __builtin_bit_cast(v4i, o[it]));
+    }
   if (threadIdx.x < ROWS) {
+    float mx, l;
+    row_stats(threadIdx.x, mx, l);
     float* mlp = mlpart + ((prog_base + split) * ROWS + threadIdx.x) * 2;
-    publish(mlp, ml_lds[0][0][threadIdx.x]);
-    publish(mlp + 1, ml_lds[0][1][threadIdx.x]);
+    publish(mlp, mx);
+    publish(mlp + 1, l);
   }
   if (!arrive_last(p.counters + prog, n_active, &s_last)) return;
-  // Row weights of the splits, exp2(m_s - max) / l (l summed in split order), kept in the
-  // o_lds tile (already published).  Up to 16 splits the (m, l) pairs are loaded once, all in
-  // flight together; more splits take a second pass.
+  // Row weights of the splits, exp2(m_s - max) / l (l summed in split order), in LDS (the first
+  // ring, no longer read).  Up to 16 splits the (m, l) pairs are loaded once, all in flight
+  // together; more splits take a second pass.
+  float* wts = reinterpret_cast<float*>(&ring0[0][0]);  // [ROWS][kAttnMergeMax]
+  static_assert(kAttnWaves * SLOT >= 64 * kAttnMergeMax * 4, "split weights fit the first ring");
   constexpr int kMergeBatch = 16;
   if (threadIdx.x < ROWS) {
     const int row = threadIdx.x;
-    float* wt = &o_lds[row][0];
+    float* wt = wts + row * kAttnMergeMax;
     auto ml_at = [&](int sp) { return mlpart + ((prog_base + (sp < n_active ? sp : 0)) * ROWS + row) * 2; };
     float mv[kMergeBatch], lv[kMergeBatch];
 #pragma unroll
@@ -489,51 +626,33 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(AttnParams p) {
     for (int sp = 0; sp < n_active; ++sp) wt[sp] *= inv;
   }
   __syncthreads();
-  // O rows: sum over splits in split order of weight * partial O.  Thread t owns the 4-column
-  // items t, t + 256, ...; all of its items' loads of 4 splits are in flight together.
-  constexpr int QPR = D / 4;                       // 4-column items per row
-  constexpr int ITEMS = (ROWS * QPR + 255) / 256;  // items per thread
-  constexpr int SB = 8;                            // splits per batch
-  v4f o[ITEMS];
-  uint32_t ioff[ITEMS];
-  bool ivalid[ITEMS];
+  // O rows: sum over splits in split order of weight * partial O.  All of a thread's items'
+  // loads of SB splits are in flight together.
+  constexpr int SB = ITEMS <= 2 ? 8 : (ITEMS <= 4 ? 4 : 2);  // at most 16 16-byte loads in flight per thread
 #pragma unroll
-  for (int it = 0; it < ITEMS; ++it) {
-    const int e = threadIdx.x + 256 * it;
-    const int row = e / QPR, d0 = (e % QPR) * 4;
-    const int qi = qc * p.QPP + row / G;
-    ivalid[it] = e < ROWS * QPR && row < p.QPP * G && qi < q_len;
-    ioff[it] = (uint32_t)((row * D + d0) * 4);
-    o[it] = v4f{0.f, 0.f, 0.f, 0.f};
-  }
-  for (int s0 = 0; s0 < n_active; s0 += SB) {
+  for (int it = 0; it < ITEMS; ++it) o[it] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int s0m = 0; s0m < n_active; s0m += SB) {
     v4i t[SB][ITEMS];
 #pragma unroll
     for (int u = 0; u < SB; ++u)
 #pragma unroll
-      for (int it = 0; it < ITEMS; ++it)
-        t[u][it] = collect16(ors, oob_unless(ivalid[it] && s0 + u < n_active,
-                                             (uint32_t)((s0 + u) * ROWS * D * 4) + ioff[it]));
+      for (int it = 0; it < ITEMS; ++it) {
+        const int e = threadIdx.x + NT * it;
+        t[u][it] = collect16(ors, oob_unless(ivalid[it] && s0m + u < n_active,
+                                             (uint32_t)(((s0m + u) * ROWS * QPR + e) * 16)));
+      }
 #pragma unroll
     for (int u = 0; u < SB; ++u)
 #pragma unroll
       for (int it = 0; it < ITEMS; ++it)
-        if (ivalid[it] && s0 + u < n_active) {
-          const int e = threadIdx.x + 256 * it;
-          o[it] += o_lds[e / QPR][s0 + u] * __builtin_bit_cast(v4f, t[u][it]);
+        if (ivalid[it] && s0m + u < n_active) {
+          const int e = threadIdx.x + NT * it;
+          o[it] += wts[(e / QPR) * kAttnMergeMax + s0m + u] * __builtin_bit_cast(v4f, t[u][it]);
         }
   }
-  typedef _Float16 v4h_t __attribute__((ext_vector_type(4)));
 #pragma unroll
-  for (int it = 0; it < ITEMS; ++it) {
-    if (!ivalid[it]) continue;
-    const int e = threadIdx.x + 256 * it;
-    const int row = e / QPR, d0 = (e % QPR) * 4;
-    const int qi = qc * p.QPP + row / G;
-    const int head = kvh * G + row % G;
-    *reinterpret_cast<v4h_t*>(p.out + (int64_t)b * p.s_ob + (int64_t)qi * p.s_ot + (int64_t)head * p.s_oh + d0) =
-        v4h_t{(_Float16)o[it].x, (_Float16)o[it].y, (_Float16)o[it].z, (_Float16)o[it].w};
-  }
+  for (int it = 0; it < ITEMS; ++it)
+    if (ivalid[it]) store_row4(threadIdx.x + NT * it, o[it]);
 }
 
 }  // namespace specq

@@ -460,7 +460,7 @@ def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len, QPP=None, BLOC
               1.0 / math.sqrt(D), _plan_ptr(plan), wptr, wbytes, _stream_ptr(q))
     rows = int(QPP) * G
     _paged_attn_kernel._note(q.device.index or 0, (D, (rows + 15) // 16, str(ks.dtype)))
-    return out, KernelInfo(2, D, 0, 0, 0, rows, 0, 4, 0)
+    return out, KernelInfo(2, D | (1 << 16 if ks.dtype == torch.float32 else 0), 0, 0, 0, rows, 0, 4, 0)
 
 
 def make_paged_kv(B, ctx_len, H_KV, D, PAGE=16, device="cuda", seed=0):
