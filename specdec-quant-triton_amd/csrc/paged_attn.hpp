@@ -346,7 +346,8 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
       }
     }
     // Scales in operand order: dword 4g + e holds ks of token perm(4g + e), dword 16 + 4g + e
-    // its vs (an fp16 scale in the low half); zero V scale for tokens at or past kv_end.
+    // its vs (an fp16 scale in the low half); zero V scale for tokens at or past kv_end (their
+    // scale slots hold the dummy address's scale).
     float ksc[4], vsc[4];
     {
       const v4i kr = *reinterpret_cast<const v4i*>(kb + SC + 16 * g);
@@ -365,10 +366,15 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
           vv = (float)__builtin_bit_cast(_Float16, (uint16_t)(vi & 0xFFFF));
         }
         ksc[e] = kv * p.scale_log2;
-        vsc[e] = (t0 + attn_perm(4 * g + e) < kv_end) ? vv : 0.f;
+        vsc[e] = vv;
       }
     }
 
+    if (t0 + kAttnChunk > kv_end) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (t0 + attn_perm(4 * g + e) >= kv_end) vsc[e] = 0.f;
+    }
     // S^T of every row block first (RB independent MFMA chains), then the softmax of every
     // row block, so the chains and the softmax arithmetic of different row blocks interleave.
     v4f cs[RB];
@@ -394,9 +400,19 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
         for (int e = 0; e < 4; ++e)
           if (t0 + attn_perm(4 * g + e) > qpos[rb]) s[e] = -INFINITY;
       }
-      const float m_new = fmaxf(m_run[rb], group_max4(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]))));
+      // The running max is the same in the four lanes of a row, so the row max only needs the
+      // cross-lane reduction (and alpha its exp) when some lane's own max exceeds it; after the
+      // first chunks that is rare, and the result is the same either way.
+      const float lmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      float m_new = m_run[rb];
+      alpha[rb] = 1.f;
+      if (__builtin_amdgcn_ballot_w64(lmax > m_run[rb]) != 0) {
+        m_new = fmaxf(m_run[rb], group_max4(lmax));
+        const float m_safe0 = (m_new == -INFINITY) ? 0.f : m_new;
+        alpha[rb] = fast_exp2(m_run[rb] - m_safe0);
+        grew |= m_new > m_run[rb];
+      }
       const float m_safe = (m_new == -INFINITY) ? 0.f : m_new;
-      alpha[rb] = fast_exp2(m_run[rb] - m_safe);
       float psum = 0.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -405,7 +421,6 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
         pf[rb][e] = (_Float16)(pv * vsc[e]);
       }
       l_run[rb] = l_run[rb] * alpha[rb] + psum;
-      grew |= m_new > m_run[rb];
       m_run[rb] = m_new;
     }
     // alpha is exactly 1 for every row whose running max did not grow, so the O rescale is
