@@ -4,6 +4,7 @@
 // Kernel families (identical fp32 summation order, so every choice is bit-identical):
 //   WS  LDS-staged activations (w4a16_ws.hpp) for any token tile up to 256 rows (default).
 //   RK  register-stream kernel (w4a16_rk.hpp) for 16- and 32-row token tiles (w4a16_path 1).
+#include <algorithm>
 #include <atomic>
 
 #include "api_common.hpp"
@@ -75,6 +76,42 @@ int w4_auto_splits(int N, int nblocks) {
   return splits;
 }
 
+// Eager tile choice for M > 16 over the token-tile depth (M cut into c = 1..6 chunks) and the
+// channel block (64 or 128), from a model fitted to 130 measured shapes x tiles of the
+// Llama-3-8B linears at M = 8..288 (mean regret 4.5 % against the best measured tile; one chunk
+// over all of M lost 21 % on average and up to 2.7x at M >= 192).  Per workgroup round:
+//   max(activation + weight intake at 60 GB/s per CU, dequant and MFMA work), against all
+//   weights at 7 TB/s, plus 2 us.
+// The split count is the caller's or w4_auto_splits(N, K), so the summation order, and with it
+// every result, is the same for every tile.
+void w4_auto_tiles(int M, int N, int K, int splits, int rw_fixed, int* mt_out, int* rw_out) {
+  const int cus = device_cus();
+  const int rows16 = ceil_div(std::max(M, 1), 16);
+  double best_t = 0;
+  int best_mt = -1, best_rw = 1, last_mt = -1;
+  // No measured best tile was deeper than 144 rows (9 x 16), where the model is least accurate.
+  constexpr int kMaxAutoMt = 9;
+  const int max_c = std::max(6, ceil_div(rows16, kMaxAutoMt));
+  for (int c = 1; c <= max_c; ++c) {
+    const int mt = ceil_div(rows16, c);
+    if (mt == last_mt || mt > kMaxAutoMt) continue;
+    last_mt = mt;
+    const int chunks = ceil_div(rows16, mt), rows = mt * 16;
+    for (int rw = 1; rw <= 2; ++rw) {
+      if (rw_fixed > 0 && rw != rw_fixed) continue;
+      const int bn = 64 * rw;
+      const double rounds = (double)ceil_div(ceil_div(N, bn) * splits * chunks, cus);
+      const double kk = (double)K / splits;
+      const double t_in = rounds * (bn * 0.5 + rows * 2.0) * kk / 60e3;
+      const double t_work = rounds * (bn * kk * 8e-6 + (double)rows * bn * kk * 4e-7);
+      const double t = std::max(std::max(t_in, t_work), (double)N * K * 0.5 / 7e6) + 2.0;
+      if (best_mt < 0 || t < best_t) { best_t = t; best_mt = mt; best_rw = rw; }
+    }
+  }
+  *mt_out = best_mt;
+  *rw_out = best_rw;
+}
+
 int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, int split_k, bool plan_mode,
               W4Cfg* cfg) {
   SPECQ_REQUIRE(layout >= 0 && layout <= 2, SPECQ_EINVAL, "w4a16: unknown weight layout %d", layout);
@@ -100,6 +137,12 @@ int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, in
     rw = block_n / 64;
   } else if (ceil_div(N, 64) > device_cus()) {
     rw = 2;  // 128-channel blocks keep wide N (the fused gate_up) to one workgroup per CU
+  }
+  if (block_m <= 0 && !plan_mode && rows16 > 1) {
+    const int nb = K / 128;
+    const int s_auto = std::min(split_k > 0 ? split_k : w4_auto_splits(N, nb), nb);
+    const int s_eff = ceil_div(nb, ceil_div(nb, s_auto));
+    w4_auto_tiles(m_grid, N, K, s_eff, block_n > 0 ? rw : 0, &mt, &rw);
   }
   // The LDS-staged kernel is the default at every depth (measured faster than the register
   // stream even for 16-row tiles on the Llama-3-8B linears); the register stream stays
