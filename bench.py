@@ -339,7 +339,8 @@ def bench_plan_graph(args, K, torch):
       maxpad    one graph at B=32, k=8 (M=288) without a plan: every step computes M=288
       plan      one plan-buffer graph captured at B=32, k=8, the active (B, k) read on device
       bucketed  plan-buffer graphs per (B bucket 1/2/3/4/6/8/12/16/24/32, k): the GEMMs of each
-                bucket run the tile picked for its row count (PlanGraphSet)
+                bucket run the tiles an eager call of its row count would pick (PlanGraphSet,
+                plan_tiles="grid")
     Host perf_counter around plan write + replay + sync per step (bench_graphs.py:126-136).
     Padding waste is the token rows the GEMMs compute beyond M, per step (the tile the library
     resolved for that strategy's grid, chunks past the active M skipped in plan mode)."""
@@ -377,22 +378,23 @@ def bench_plan_graph(args, K, torch):
         maxima of a plan-mode launch whose active (B, q_len) is read on the device."""
         Mg = Bg * qg
         kw = dict(plan=plan.gemm, grid_m_max=Mg) if plan is not None else {}
+        gk = dict(kw, plan_tiles=plan.tiles) if plan is not None else {}
         aa, ss = a[:Mg], sa[:Mg]
         for lw in layers:
-            K.w8a8_matmul(aa, ss, *lw["qkv"], out=bufs["qkv"][:Mg], BLOCK_M=None, **kw)
+            K.w8a8_matmul(aa, ss, *lw["qkv"], out=bufs["qkv"][:Mg], BLOCK_M=None, **gk)
             kc, vc, ks, vs, bt, cl = lw["kv"]
             K.paged_attention(q_buf[:Bg, :qg], kc, vc, ks, vs, bt[:Bg], cl[:Bg], qg, QPP=qg,
                               plan=plan.attn if plan is not None else None, out=o_buf[:Bg, :qg])
-            K.w8a8_matmul(aa, ss, *lw["o"], out=bufs["o"][:Mg], BLOCK_M=None, **kw)
-            K.w8a8_matmul(aa, ss, *lw["gate"], out=bufs["gate"][:Mg], BLOCK_M=None, **kw)
-            K.w8a8_matmul(aa, ss, *lw["up"], out=bufs["up"][:Mg], BLOCK_M=None, **kw)
+            K.w8a8_matmul(aa, ss, *lw["o"], out=bufs["o"][:Mg], BLOCK_M=None, **gk)
+            K.w8a8_matmul(aa, ss, *lw["gate"], out=bufs["gate"][:Mg], BLOCK_M=None, **gk)
+            K.w8a8_matmul(aa, ss, *lw["up"], out=bufs["up"][:Mg], BLOCK_M=None, **gk)
             K.silu_mul_quant_int8(bufs["gate"][:Mg], bufs["up"][:Mg], q=hq[:Mg], s=hs[:Mg], **kw)
-            K.w8a8_matmul(hq[:Mg], hs[:Mg], *lw["down"], out=bufs["down"][:Mg], BLOCK_M=None, **kw)
+            K.w8a8_matmul(hq[:Mg], hs[:Mg], *lw["down"], out=bufs["down"][:Mg], BLOCK_M=None, **gk)
 
-    def rows_computed(Mg, M, plan_mode):
+    def rows_computed(Mg, M, plan_mode, grid_tiles=False):
         """Token rows the qkv GEMM computes for active M on a grid of Mg rows (the tile the
         library resolves for that call; plan-mode chunks past M exit without computing)."""
-        bm = K.KernelInfo(0, 1 | (16 if plan_mode else 0), Mg, QKV, HID, 0, 0, 4, 0).config["block_m"]
+        bm = K.KernelInfo(0, 1 | (16 if plan_mode and not grid_tiles else 0), Mg, QKV, HID, 0, 0, 4, 0).config["block_m"]
         return bm * -(-M // bm) if plan_mode else bm * -(-Mg // bm)
 
     rng = random.Random(0)
@@ -460,7 +462,7 @@ def bench_plan_graph(args, K, torch):
         waste["eager"] += rows_computed(M, M, False) - M
         waste["maxpad"] += rows_computed(M_MAX, M, False) - M
         waste["plan"] += rows_computed(M_MAX, M, True) - M
-        waste["bucketed"] += rows_computed(gset.bucket(B) * (k + 1), M, True) - M
+        waste["bucketed"] += rows_computed(gset.bucket(B) * (k + 1), M, True, grid_tiles=True) - M
     torch.cuda.synchronize()
     for name, v in waste.items():
         out[f"{name}_pad_rows_per_step"] = v / len(trace)

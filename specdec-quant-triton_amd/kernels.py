@@ -224,12 +224,17 @@ def pack_weight_int8(w_q):
 
 
 def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK_K=128,
-                num_warps=4, num_stages=3, plan=None, grid_m_max=None, split_k=0, workspace=None):
+                num_warps=4, num_stages=3, plan=None, grid_m_max=None, split_k=0, workspace=None,
+                plan_tiles=None):
     """C[M, N] = fp16((int32(a_q @ w_q.T) * sa[:, None]) * sw[None, :]).  Returns (out, ck).
 
     a_q int8 [M, K]; w_q int8 [N, K] (or a PackedWeightInt8); sa fp32 [M]; sw fp32 [N].
     With `plan`, M is read from plan[0] on the device and the grid covers grid_m_max rows
-    (reference kernels.py:71-86).
+    (reference kernels.py:71-86).  Plan-mode calls with an automatic BLOCK_M use tiles of at
+    most 80 rows, so a small active M leaves the later chunks idle; plan_tiles="grid" instead
+    runs the tiles an eager call of grid_m_max rows would pick (for plan graphs whose active M
+    stays close to the grid, e.g. one graph per shape bucket).  The INT32 sums are exact, so
+    every tile gives the same result.
     """
     packed = isinstance(w_q, PackedWeightInt8)
     _require_gpu(a_q, sa, sw)
@@ -254,6 +259,12 @@ def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK_K=12
     bm = BLOCK_M if BLOCK_M else pick_block_m("w8a8", m_grid, N, K)
     bn = _w8a8_block_n(BLOCK_N)
     nw = int(num_warps) if num_warps else 4
+    if plan is not None and plan_tiles is not None:
+        if plan_tiles != "grid":
+            raise RuntimeError(f"w8a8_matmul: plan_tiles={plan_tiles!r} (None or 'grid')")
+        if not bm:
+            cfg = KernelInfo(0, 1 if packed else 0, m_grid, N, K, 0, bn, nw, split_k).config
+            bm, bn, split_k = cfg["block_m"], cfg["block_n"], cfg["split_k"]
     ws = workspace or _ws.shared(a_q.device)
     if packed:
         need = _lib.lib().specq_w8a8_packed_workspace_size(m_grid, N, K, bm, bn, nw, split_k)

@@ -16,6 +16,9 @@ class Plan:
     SLOTS = 4
 
     def __init__(self, device="cuda"):
+        # GEMM tile policy for calls made with this plan (w8a8_matmul's plan_tiles): None for a
+        # graph captured at the maximum grid, "grid" when the active M stays close to the grid.
+        self.tiles = None
         self.dev = torch.zeros(8, dtype=torch.int32, device=device)
         self._host = [torch.zeros(8, dtype=torch.int32).pin_memory() for _ in range(self.SLOTS)]
         self._done = [None] * self.SLOTS
@@ -70,6 +73,9 @@ class PlanGraphSet:
 
     def __init__(self, step, b_max: int, q_lens, buckets=None, device="cuda"):
         self.plan = Plan(device)
+        # The active M of a bucket's graph is at least 2/3 of its grid (buckets 1.5x apart),
+        # so its GEMMs can run the tiles an eager call of the grid's M would pick.
+        self.plan.tiles = "grid"
         self.buckets = sorted(buckets or b_buckets(b_max))
         if self.buckets[-1] < b_max:
             raise ValueError("the largest bucket must hold b_max")

@@ -109,8 +109,8 @@ def test_plan_graph_replays_every_shape_bit_exact():
 
 
 def test_bucketed_plan_graphs_replay_bit_exact():
-    # PlanGraphSet: one plan graph per (B bucket, q_len), each with the tile its row count
-    # gets.  Every replay must equal eager bit for bit and leave rows past M untouched.  The
+    # PlanGraphSet: one plan graph per (B bucket, q_len), its GEMMs on the tiles an eager
+    # call of the bucket's row count gets (plan_tiles="grid").  Every replay must equal eager bit for bit and leave rows past M untouched.  The
     # second half of the trace replays back to back without host syncs (outputs copied out on
     # the stream), so the plan's host slots are reused while earlier copies may still pend.
     from specq.plan import PlanGraphSet
@@ -127,17 +127,18 @@ def test_bucketed_plan_graphs_replay_bit_exact():
     def step(Bg, qg, plan=None):
         Mg = Bg * qg
         kw = dict(plan=plan.gemm, grid_m_max=Mg) if plan is not None else {}
+        gk = dict(kw, plan_tiles=plan.tiles) if plan is not None else {}  # the bucket's eager tiles
         a, sa = x_in[0][:Mg], x_in[1][:Mg]
         for lw in layers:
-            K.w8a8_matmul(a, sa, *lw["qkv"], out=bufs["qkv"][:Mg], BLOCK_M=None, **kw)
+            K.w8a8_matmul(a, sa, *lw["qkv"], out=bufs["qkv"][:Mg], BLOCK_M=None, **gk)
             kc, vc, ks, vs, bt, cl = lw["kv"]
             K.paged_attention(q_buf[:Bg, :qg], kc, vc, ks, vs, bt[:Bg], cl[:Bg], qg, QPP=qg,
                               plan=plan.attn if plan is not None else None, out=o_buf[:Bg, :qg])
-            K.w8a8_matmul(a, sa, *lw["o"], out=bufs["o"][:Mg], BLOCK_M=None, **kw)
-            K.w8a8_matmul(a, sa, *lw["gate"], out=bufs["gate"][:Mg], BLOCK_M=None, **kw)
-            K.w8a8_matmul(a, sa, *lw["up"], out=bufs["up"][:Mg], BLOCK_M=None, **kw)
+            K.w8a8_matmul(a, sa, *lw["o"], out=bufs["o"][:Mg], BLOCK_M=None, **gk)
+            K.w8a8_matmul(a, sa, *lw["gate"], out=bufs["gate"][:Mg], BLOCK_M=None, **gk)
+            K.w8a8_matmul(a, sa, *lw["up"], out=bufs["up"][:Mg], BLOCK_M=None, **gk)
             K.silu_mul_quant_int8(bufs["gate"][:Mg], bufs["up"][:Mg], q=hq[:Mg], s=hs[:Mg], **kw)
-            K.w8a8_matmul(hq[:Mg], hs[:Mg], *lw["down"], out=bufs["down"][:Mg], BLOCK_M=None, **kw)
+            K.w8a8_matmul(hq[:Mg], hs[:Mg], *lw["down"], out=bufs["down"][:Mg], BLOCK_M=None, **gk)
 
     note("bucketed graphs: capture")
     gset = PlanGraphSet(step, B_MAX, [k + 1 for k in KS])
