@@ -314,6 +314,14 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
     }
   };
 
+  // Up to two row blocks the Q fragments stay in registers for the whole loop (RB * NU * 4
+  // VGPRs); deeper packings read them from LDS per chunk.
+  constexpr bool QREG = RB <= 2;
+  v8h qreg[QREG ? RB : 1][NU];
+  auto qfrag = [&](int rb, int u) -> v8h {
+    if constexpr (QREG) return qreg[rb][u];
+    else return q_lds[rb][u][lane];
+  };
   // One chunk from ring slot SL: S^T, online softmax, O^T += V^T . P^T.
   auto compute = [&](auto slc, int it) __attribute__((always_inline)) {
     const uint8_t* kb = ring_of(slc, w);
@@ -382,7 +390,7 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
     for (int rb = 0; rb < RB; ++rb) {
       v4f c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int u = 0; u < NU; ++u) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[u], q_lds[rb][u][lane], c, 0, 0, 0);
+      for (int u = 0; u < NU; ++u) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[u], qfrag(rb, u), c, 0, 0, 0);
       cs[rb] = c;
     }
     // Every row of the program sees every token of the chunk: no causal mask needed.
@@ -457,6 +465,12 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
     issue(std::integral_constant<int, (i + 1) % NS>{}, i);
   });
   wg_barrier_lds();
+  if constexpr (QREG) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int u = 0; u < NU; ++u) qreg[rb][u] = q_lds[rb][u][lane];
+  }
   // Steady state: issue chunk it + NS - 1 into the slot chunk it - 1 left, wait for chunk it
   // (NS - 1 chunks may stay in flight), multiply it.
   for (int base = 0; base < n_it; base += NS) {
