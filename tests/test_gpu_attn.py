@@ -125,3 +125,51 @@ def test_attention_long_context_sub_splits():
         check(out, ref, ql, f"long ctx QPP={QPP}")
         outs[QPP] = out
     assert torch.equal(outs[1], outs[ql]), "QPP=1 and fused results differ"
+
+
+def test_attention_page32_ragged_and_plan_subset():
+    """PAGE=32 (two 16-token sub-tiles per page), ragged contexts from the query tokens alone to
+    1290 tokens, fp16 scales; QPP=1 equals fused, and a plan-mode call with 3 of 5 sequences
+    active equals eager on those 3 and leaves the others untouched."""
+    B, k = 5, 3
+    ql = k + 1
+    ctx = [ql, 9, 33, 517, 1290]
+    kc, vc, ks, vs, bt, cl = gen.paged_kv(B, ctx, H_KV, D, PAGE=32, seed=81, scale_dtype=torch.float16)
+    q = gen.queries(B, ql, H, D, seed=82)
+    ref = O.paged_attention(*cpu(q, kc, vc, ks, vs, bt, cl), ql)
+    kc, vc, ks, vs, bt, cl, q = (t.to(DEV) for t in (kc, vc, ks, vs, bt, cl, q))
+    note(f"attn PAGE=32 ragged ctx={ctx}")
+    outs = {}
+    for QPP in (1, ql):
+        out, _ = K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=QPP)
+        torch.cuda.synchronize()
+        check(out, ref, ql, f"PAGE=32 QPP={QPP}")
+        outs[QPP] = out
+    assert torch.equal(outs[1], outs[ql]), "QPP=1 and fused results differ"
+    from specq.plan import Plan
+    plan = Plan(DEV)
+    plan.set(3, ql)
+    sentinel = torch.full_like(q, 7.0)
+    K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=ql, plan=plan.attn, out=sentinel)
+    torch.cuda.synchronize()
+    eager3, _ = K.paged_attention(q[:3], kc, vc, ks, vs, bt[:3], cl[:3], ql, QPP=ql)
+    torch.cuda.synchronize()
+    assert torch.equal(sentinel[:3], eager3), "plan mode differs from eager on the active sequences"
+    assert bool((sentinel[3:] == 7.0).all()), "plan mode wrote inactive sequences"
+
+
+def test_attention_single_sequence_many_splits():
+    """One sequence of 9000 tokens: the split length targets the CU count, so the sequence is
+    cut into more than 16 splits (the merge's second weight pass); QPP=1 equals fused."""
+    B, k = 1, 8
+    ql = k + 1
+    kc, vc, ks, vs, bt, cl = gen.paged_kv(B, [9000 + ql], H_KV, D, seed=83)
+    q = gen.queries(B, ql, H, D, seed=84)
+    ref = O.paged_attention(*cpu(q, kc, vc, ks, vs, bt, cl), ql)
+    kc, vc, ks, vs, bt, cl, q = (t.to(DEV) for t in (kc, vc, ks, vs, bt, cl, q))
+    note("attn B=1 ctx=9000 many splits")
+    o1, _ = K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=ql)
+    o2, _ = K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=1)
+    torch.cuda.synchronize()
+    check(o1, ref, ql, "B=1 ctx=9000")
+    assert torch.equal(o1, o2)
