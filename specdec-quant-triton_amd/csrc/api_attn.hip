@@ -29,17 +29,12 @@ const void* attn_fn(int D, int rb, int fp32) {
   return nullptr;
 }
 
-// grid.x: the most splits a sequence of at most max_pages * PAGE tokens is cut into when at
-// least `pairs_min` (sequence, KV head) pairs are active (fewer pairs never means fewer splits).
+// grid.x: the splits of a block table of max_pages * PAGE tokens when at least `pairs_min`
+// (sequence, KV head) pairs are active (fewer pairs never means fewer splits).
 int n_splits_for(int max_pages, int PAGE, int pairs_min, int target) {
-  const int64_t tokens = (int64_t)max_pages * PAGE;
-  const int n_units = (int)((tokens + kAttnUnit - 1) / kAttnUnit);
-  int ns = 1;
-  for (int n = 1; n <= n_units; ++n) {
-    const int u = attn_split_units(n * kAttnUnit, pairs_min, target);
-    ns = std::max(ns, ceil_div(n, u));
-  }
-  return ns;
+  const int cap = max_pages * PAGE;
+  const int per = kAttnUnit * attn_split_units(cap, pairs_min, target);
+  return std::max(1, ceil_div(cap, per));
 }
 
 }  // namespace

@@ -12,10 +12,12 @@
 //    query rows sharing the KV head are packed into RB 16-row blocks, so a fused verification
 //    program reads each K/V byte once for all (k+1) * G rows.
 //  * Split length follows the work on the device: a split is a whole number of 128-token
-//    units, as many as make (active sequences) x (KV heads) x (splits) reach the CU count,
-//    between 256 and 4096 tokens and at most 64 splits per sequence (attn_split_units).  It
-//    depends only on the sequence length and the number of active sequences, so a QPP=1 and a
-//    fused program, and an eager and a plan-mode call, cut a sequence at the same tokens.
+//    units, as many as make (active sequences) x (KV heads) x (splits) reach the CU count for
+//    a sequence filling the block table, between 256 and 4096 tokens and at most 64 splits
+//    (attn_split_units).  It depends only on the block table's capacity and the number of
+//    active sequences, so a QPP=1 and a fused program, and an eager and a plan-mode call, cut
+//    a sequence at the same tokens, and the page ids of a split can be fetched before the
+//    sequence's length is known.
 //  * Eight waves (two per SIMD, so one wave's MFMA and LDS latencies hide behind the other's
 //    arithmetic) take interleaved 16-token chunks of the split (chunk c, one page sub-tile,
 //    goes to wave c % 8) and stream them through a wave-private LDS ring of 4 slots by LDS DMA
@@ -186,13 +188,14 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
   n_seqs = uniform(n_seqs);
   q_len = uniform(q_len);
   if (b >= n_seqs || qc * p.QPP >= q_len) return;
-  // The block table holds max_pages pages: never look past them.
-  const int L = uniform(min(p.ctx_len[b], p.max_pages * p.PAGE));
-  const int kv_end = L - q_len + min(qc * p.QPP + p.QPP, q_len);
-  const int split_tokens = kAttnUnit * attn_split_units(L, n_seqs * p.H_KV, p.target_wgs);
-  // Split 0 always runs, so rows with no visible key still get their zero output.
-  if (split > 0 && split * split_tokens >= kv_end) return;
-  const int n_active = kv_end > split_tokens ? (kv_end + split_tokens - 1) / split_tokens : 1;
+  // Splits are sized from the block table's capacity (not the sequence's own length), so the
+  // page ids of the split can be fetched together with the context length and Q: one memory
+  // round trip before the first K/V DMA.
+  const int cap = p.max_pages * p.PAGE;
+  const int split_tokens = kAttnUnit * attn_split_units(cap, n_seqs * p.H_KV, p.target_wgs);
+  const int s0 = split * split_tokens;
+  if (split > 0 && s0 >= cap) return;
+  const int L_raw = p.ctx_len[b];
 
   const int lane = lane_id(), w = uniform(wave_id()), g = lane >> 4, r = lane & 15;
   const int G = p.G;
@@ -204,14 +207,6 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
     else return ring3[wave];
   };
 
-  int qpos[RB];  // absolute position of the query row this lane holds in each row block
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const int row = rb * 16 + r;
-    const int qi = qc * p.QPP + row / G;
-    const bool valid = (row < p.QPP * G) && (qi < q_len);
-    qpos[rb] = valid ? (L - q_len + qi) : -1;
-  }
   float m_run[RB], l_run[RB];
   v4f acc[RB][ND];
 #pragma unroll
@@ -224,16 +219,14 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
 
   // This wave's chunks of the split: chunk `it` is the 16 tokens from s0 + 16 (w + 8 it), one
   // page sub-tile.
-  const int s0 = split * split_tokens;
-  const int s1 = min(s0 + split_tokens, kv_end);
-  const int n_it = uniform(s1 > s0 + kAttnChunk * w ? (s1 - s0 - kAttnChunk * w + kAttnUnit - 1) / kAttnUnit : 0);
   auto chunk_t0 = [&](int it) { return s0 + kAttnChunk * (w + kAttnWaves * it); };
   const int32_t* bt_row = p.bt + (int64_t)b * p.s_bt;
-  // Page of the wave's chunk `lane` (n_it <= 32).
+  // Page of the wave's chunk `lane` within the split and the block table (at most 32 chunks);
+  // chunks at or past kv_end never use theirs.
   int page_v;
   {
     const int ts = chunk_t0(lane);
-    page_v = (lane < n_it && ts < kv_end) ? bt_row[ts / p.PAGE] : 0;
+    page_v = (ts < s0 + split_tokens && ts < cap) ? bt_row[ts / p.PAGE] : 0;
   }
   // Q fragments: thread t stages fragments t, t + NT, ... of [rb][u][lane].
   constexpr int QF = (RB * NU * 64 + NT - 1) / NT;
@@ -250,6 +243,23 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
                              : p.q;
     const v8h x = *reinterpret_cast<const v8h*>(src);
     qtmp[i] = ok ? x : v8h{0, 0, 0, 0, 0, 0, 0, 0};
+  }
+
+  // The context length (a scalar load, in flight with the page ids and Q).
+  const int L = uniform(min(L_raw, cap));
+  const int kv_end = L - q_len + min(qc * p.QPP + p.QPP, q_len);
+  // Split 0 always runs, so rows with no visible key still get their zero output.
+  if (split > 0 && s0 >= kv_end) return;
+  const int n_active = kv_end > split_tokens ? (kv_end + split_tokens - 1) / split_tokens : 1;
+  const int s1 = min(s0 + split_tokens, kv_end);
+  const int n_it = uniform(s1 > s0 + kAttnChunk * w ? (s1 - s0 - kAttnChunk * w + kAttnUnit - 1) / kAttnUnit : 0);
+  int qpos[RB];  // absolute position of the query row this lane holds in each row block
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int row = rb * 16 + r;
+    const int qi = qc * p.QPP + row / G;
+    const bool valid = (row < p.QPP * G) && (qi < q_len);
+    qpos[rb] = valid ? (L - q_len + qi) : -1;
   }
 
   // Page ids and Q fragments arrive together (one memory round trip); Q goes to LDS before any
