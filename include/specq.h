@@ -127,7 +127,9 @@ int specq_w4a8_packed(const int8_t* a, int64_t lda, const void* w_packed,
  * (row-major weights only).  Every family computes the same INT32 sums, so results do not
  * change.  "w4a16_path": W4A16 kernel family, 0 = automatic (LDS-staged activations), 1 =
  * register-stream kernel for token tiles of up to 32 rows, 2 = LDS-staged activations.  Both sum in the
- * same fp32 order, so results do not change either. */
+ * same fp32 order, so results do not change either.  "attn_target_wgs": the workgroup count
+ * the paged attention's split length aims at (0 = the device's CU count); results depend on
+ * the split length, so calls compared bit for bit must use the same value. */
 int specq_set_option(const char* name, int value);
 
 /* ---------------------------------------------------------------------------------------

@@ -1,10 +1,16 @@
 // C ABI for the INT8 paged verification attention: validation, grid, workspace and launch.
 #include <algorithm>
+#include <atomic>
 
 #include "api_common.hpp"
 #include "paged_attn.hpp"
 
 namespace specq {
+
+// Workgroups the split length aims at (0 = the device's CUs), set through
+// specq_set_option("attn_target_wgs", v); eager and plan-mode calls that are compared bit for
+// bit must run with the same value.
+std::atomic<int> g_attn_target{0};
 
 namespace {
 
@@ -72,7 +78,8 @@ extern "C" size_t specq_paged_attn_workspace_size(int B_grid, int H, int H_KV, i
   const int64_t progs = (int64_t)B_grid * H_KV * n_qc;
   if ((int64_t)max_pages * PAGE > kAttnMaxTokens) return 0;
   // Plan-mode bound: at least one active sequence.
-  const int ns = n_splits_for(max_pages, PAGE, H_KV, device_cus());
+  const int tgt = g_attn_target.load();
+  const int ns = n_splits_for(max_pages, PAGE, H_KV, tgt > 0 ? tgt : device_cus());
   if (ns <= 1) return 0;
   // Sized for D = 128 (the largest supported head dimension).
   const size_t part = (size_t)progs * ns * rows * (128 + 2) * 4;
@@ -117,7 +124,7 @@ extern "C" int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64
   SPECQ_REQUIRE(fn != nullptr, SPECQ_ENOTSUP, "paged_attn: no kernel for D=%d rows=%d", D, QPP * G);
   const int n_qc = ceil_div(plan ? ql_grid : q_len, QPP);
   if (n_qc == 0) return SPECQ_OK;
-  const int target = device_cus();
+  const int target = g_attn_target.load() > 0 ? g_attn_target.load() : device_cus();
   // Eager calls know the active sequences; a plan may activate as few as one.
   const int ns = n_splits_for(max_pages, PAGE, (plan ? 1 : std::max(n_seqs, 1)) * H_KV, target);
   const int64_t progs = (int64_t)B_grid * H_KV * n_qc;

@@ -89,6 +89,7 @@ __global__ __launch_bounds__(256) void w4a8_pack_kernel(const uint8_t* __restric
 // Kernel family override (0 = automatic), set through specq_set_option("w8a8_path", v).
 std::atomic<int> g_w8a8_path{0};
 extern std::atomic<int> g_w4a16_path;  // api_w4a16.hip
+extern std::atomic<int> g_attn_target;  // api_attn.hip
 
 namespace {
 
@@ -492,6 +493,11 @@ extern "C" int specq_w8a8_packed(const int8_t* a, int64_t lda, const void* w_pac
 extern "C" int specq_set_option(const char* name, int value) {
   clear_error();
   SPECQ_REQUIRE(name != nullptr, SPECQ_EINVAL, "set_option: null name");
+  if (strcmp(name, "attn_target_wgs") == 0) {
+    SPECQ_REQUIRE(value >= 0 && value <= (1 << 20), SPECQ_EINVAL, "set_option: attn_target_wgs must be 0..2^20");
+    g_attn_target.store(value);
+    return SPECQ_OK;
+  }
   if (strcmp(name, "w8a8_path") == 0) {
     SPECQ_REQUIRE(value >= 0 && value <= 3, SPECQ_EINVAL, "set_option: w8a8_path must be 0..3");
     g_w8a8_path.store(value);

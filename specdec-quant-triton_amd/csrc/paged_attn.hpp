@@ -13,8 +13,8 @@
 //    program reads each K/V byte once for all (k+1) * G rows.
 //  * Split length follows the work on the device: a split is a whole number of 128-token
 //    units, as many as make (active sequences) x (KV heads) x (splits) reach the CU count for
-//    a sequence filling the block table, between 256 and 4096 tokens and at most 64 splits
-//    (attn_split_units).  It depends only on the block table's capacity and the number of
+//    a sequence filling the block table, between 256 and 4096 tokens and at most 64 splits,
+//    the units spread evenly over the splits (attn_split_units).  It depends only on the block table's capacity and the number of
 //    active sequences, so a QPP=1 and a fused program, and an eager and a plan-mode call, cut
 //    a sequence at the same tokens, and the page ids of a split can be fetched before the
 //    sequence's length is known.
@@ -94,7 +94,9 @@ __host__ __device__ inline int attn_split_units(int L, int pairs, int target) {
   if (u < u_min) u = u_min;
   if (u < kAttnMinUnits) u = kAttnMinUnits;
   if (u > kAttnMaxUnits) u = kAttnMaxUnits;
-  return u;
+  // Even out the splits (a 33-unit sequence in 32-unit splits becomes 17 + 16, not 32 + 1).
+  const int ns = (n + u - 1) / u;
+  return (n + ns - 1) / ns;
 }
 
 // Operand row x of a 16-token sub-tile holds token attn_perm(x): rows 4g..4g+3 (one lane group
