@@ -173,3 +173,34 @@ def test_attention_single_sequence_many_splits():
     torch.cuda.synchronize()
     check(o1, ref, ql, "B=1 ctx=9000")
     assert torch.equal(o1, o2)
+
+
+@pytest.mark.parametrize("target", [32, 4096])
+def test_attention_split_target_option(target):
+    """The attn_target_wgs option moves the split length (32: the longest splits, 4096: the
+    shortest).  Results stay within tolerance; QPP=1 equals fused and a plan-mode call equals
+    eager at the same setting."""
+    from specq import _lib
+    from specq.plan import Plan
+    B, k = 3, 4
+    ql = k + 1
+    ctx = [700, 2100, 3333]
+    kc, vc, ks, vs, bt, cl = gen.paged_kv(B, ctx, H_KV, D, seed=85)
+    q = gen.queries(B, ql, H, D, seed=86)
+    ref = O.paged_attention(*cpu(q, kc, vc, ks, vs, bt, cl), ql)
+    kc, vc, ks, vs, bt, cl, q = (t.to(DEV) for t in (kc, vc, ks, vs, bt, cl, q))
+    note(f"attn split target {target}")
+    _lib.set_option("attn_target_wgs", target)
+    try:
+        o1, _ = K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=ql)
+        o2, _ = K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=1)
+        plan = Plan(DEV)
+        plan.set(B, ql)
+        o3 = torch.full_like(q, 7.0)
+        K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=ql, plan=plan.attn, out=o3)
+        torch.cuda.synchronize()
+    finally:
+        _lib.set_option("attn_target_wgs", 0)
+    check(o1, ref, ql, f"target {target}")
+    assert torch.equal(o1, o2), "QPP=1 and fused results differ"
+    assert torch.equal(o1, o3), "plan mode differs from eager"
