@@ -21,7 +21,7 @@ from __future__ import annotations
 import numpy as np
 
 __all__ = [
-    "w8a8_int32", "w8a8", "w8a8_fp32_formula",
+    "w8a8_int32", "w8a8",
     "quantize_rows_int8",
     "quantize_weight_int4", "unpack_int4_u8", "pack_int4_u8", "unpack_int4_i32", "pack_int4_i32",
     "dequant_int4", "w4a16",
@@ -54,12 +54,6 @@ def w8a8(a, sa, w, sw) -> np.ndarray:
     sw = np.asarray(sw, dtype=np.float32)
     c = (acc * sa[:, None]) * sw[None, :]
     return c.astype(np.float16)
-
-
-def w8a8_fp32_formula(a, sa, w, sw) -> np.ndarray:
-    """The reference test's own float formula (correctness.py:37), evaluated in float64."""
-    acc = np.asarray(a, np.float64) @ np.asarray(w, np.float64).T
-    return acc * np.asarray(sa, np.float64)[:, None] * np.asarray(sw, np.float64)[None, :]
 
 
 # ------------------------------------------------------------------------------------------
@@ -149,7 +143,8 @@ def w4a16(a, qu, sc, group: int = 128) -> np.ndarray:
 # ------------------------------------------------------------------------------------------
 # Paged verification attention (kernels.py:178-236, 289-309)
 # ------------------------------------------------------------------------------------------
-def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len: int, round_p_fp16: bool = False) -> np.ndarray:
+def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len: int, round_p_fp16: bool = False,
+                    magnitude: bool = False):
     """float64 dense restatement of paged_attention_ref (kernels.py:289-309).
 
     out[b, i, h] = sum_t softmax_t(q . k_t * ks_t / sqrt(D), t <= L - q_len + i) * v_t * vs_t
@@ -157,7 +152,10 @@ def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len: int, round_p_f
     the GQA group of query head h reading KV head h // G.  With round_p_fp16 the normalised
     softmax weight times vs_t is rounded to fp16 as the kernel does before the PV product
     (kernels.py:232), which is a per-term relative perturbation of at most 2**-11.
-    Rows i >= q_len are left at zero.  Returns float64 [B, QLMAX, H, D].
+    Rows i >= q_len are left at zero.  Returns float64 [B, QLMAX, H, D]; with magnitude=True
+    also mag[b, i, h] = sum_t p_t * |v_t * vs_t| (same shape), the scale against which the
+    rounding of each p_t * vs_t term is measured (it bounds |out| and equals it when every
+    v_t * vs_t >= 0).
     """
     q = np.asarray(q, dtype=np.float16).astype(np.float64)
     kc = np.asarray(kc, dtype=np.int8)
@@ -170,6 +168,7 @@ def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len: int, round_p_f
     PAGE, H_KV = kc.shape[1], kc.shape[2]
     G = H // H_KV
     out = np.zeros((B, QL, H, D), dtype=np.float64)
+    mag = np.zeros((B, QL, H, D), dtype=np.float64) if magnitude else None
     for b in range(B):
         L = int(cl[b])
         pos = np.arange(L)
@@ -178,10 +177,11 @@ def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len: int, round_p_f
         k = kc[page, slot].astype(np.float64) * ks[page, slot][..., None]      # [L, H_KV, D]
         v_int = vc[page, slot].astype(np.float64)
         v_sc = vs[page, slot]                                                  # [L, H_KV]
-        for h in range(H):
-            kh = h // G
-            s = q[b, :q_len, h, :] @ k[:, kh, :].T / np.sqrt(D)               # [q_len, L]
-            qpos = L - q_len + np.arange(q_len)
+        # query row r = i * G + g is token i of query head kh * G + g
+        qpos = np.repeat(L - q_len + np.arange(q_len), G)
+        for kh in range(H_KV):
+            qq = q[b, :q_len, kh * G:(kh + 1) * G, :].reshape(q_len * G, D)
+            s = qq @ k[:, kh, :].T / np.sqrt(D)                                # [q_len * G, L]
             s = np.where(pos[None, :] > qpos[:, None], -np.inf, s)
             mx = s.max(axis=1, keepdims=True)
             mx = np.where(np.isfinite(mx), mx, 0.0)
@@ -191,8 +191,10 @@ def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len: int, round_p_f
             pv = p * v_sc[None, :, kh]
             if round_p_fp16:
                 pv = pv.astype(np.float16).astype(np.float64)
-            out[b, :q_len, h, :] = pv @ v_int[:, kh, :]
-    return out
+            out[b, :q_len, kh * G:(kh + 1) * G, :] = (pv @ v_int[:, kh, :]).reshape(q_len, G, D)
+            if magnitude:
+                mag[b, :q_len, kh * G:(kh + 1) * G, :] = (np.abs(pv) @ np.abs(v_int[:, kh, :])).reshape(q_len, G, D)
+    return (out, mag) if magnitude else out
 
 
 # ------------------------------------------------------------------------------------------

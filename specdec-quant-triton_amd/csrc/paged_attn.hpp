@@ -438,7 +438,7 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
       for (int e = 0; e < 4; ++e) {
         const float pv = fast_exp2(s[e] - m_safe);
         psum += pv;
-        pf[rb][e] = (_Float16)(pv * vsc[e]);
+        pf[rb][e] = (_Float16)f32_opaque(pv * vsc[e]);  // fp32 product, then fp16 (kernels.py:232)
       }
       l_run[rb] = l_run[rb] * alpha[rb] + psum;
       m_run[rb] = m_new;
@@ -585,12 +585,17 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
     }
   }
   typedef _Float16 v4h_t __attribute__((ext_vector_type(4)));
+  // Each value is rounded to fp32 before the fp16 cast (f32_opaque keeps the compiler from
+  // fusing a last multiply and the cast into one v_fma_mixlo with a single rounding, which it
+  // does in some instantiations and not others, so programs of different row counts would
+  // round a midpoint differently).
   auto store_row4 = [&](int e, v4f v) {
     const int row = e / QPR, d0 = (e % QPR) * 4;
     const int qi = qc * p.QPP + row / G;
     const int head = kvh * G + row % G;
     *reinterpret_cast<v4h_t*>(p.out + (int64_t)b * p.s_ob + (int64_t)qi * p.s_ot + (int64_t)head * p.s_oh + d0) =
-        v4h_t{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+        v4h_t{(_Float16)f32_opaque(v.x), (_Float16)f32_opaque(v.y), (_Float16)f32_opaque(v.z),
+              (_Float16)f32_opaque(v.w)};
   };
 
   const int prog = (b * p.H_KV + kvh) * p.n_qc + qc;

@@ -452,9 +452,21 @@ def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len, QPP=None, BLOC
         raise RuntimeError("paged_attention: head_dim must be contiguous")
     if block_tbl.dtype != torch.int32 or ctx_len.dtype != torch.int32:
         raise RuntimeError("paged_attention: block_tbl and ctx_len must be int32")
+    if out.shape != q.shape:
+        raise RuntimeError(f"paged_attention: out {tuple(out.shape)} must have q's shape {tuple(q.shape)}")
+    if kc.shape != vc.shape or kc.shape[3] != D or H % H_KV != 0:
+        raise RuntimeError(f"paged_attention: cache {tuple(kc.shape)} does not fit q {tuple(q.shape)}")
+    if tuple(ks.shape) != tuple(kc.shape[:3]) or ks.shape != vs.shape:
+        raise RuntimeError(f"paged_attention: scales {tuple(ks.shape)} must be [pages, PAGE, H_KV]")
+    if int(QPP) < 1:
+        raise RuntimeError(f"paged_attention: QPP={QPP} must be at least 1")
+    if plan is None and not (0 <= int(n_seqs) <= B and 0 <= int(q_len) <= QLMAX):
+        raise RuntimeError(f"paged_attention: need 0 <= n_seqs <= {B} and 0 <= q_len <= {QLMAX}")
     block_tbl = _rowmajor(block_tbl)
     ctx_len = ctx_len.contiguous()
     B_grid = B if plan is not None else int(n_seqs)
+    if block_tbl.dim() != 2 or block_tbl.shape[0] < B_grid or ctx_len.numel() < B_grid:
+        raise RuntimeError("paged_attention: block_tbl and ctx_len must cover every sequence of the grid")
     G = H // H_KV
     max_pages = block_tbl.shape[1]
     ws = workspace or _ws.shared(q.device)

@@ -9,12 +9,16 @@ only), so every oracle function is pinned by what the mathematics fixes:
                      torch restatement (library round)
   int4 pack/unpack   byte KATs 0x88 -> (0, 0), 0x0F -> (+7, -8); exhaustive round trips;
                      u8 <-> int32 layouts agree on every nibble
+  quantize_weight_int4  hand-worked packed bytes, fp16 scales and fp32-scale dequantised
+                     values (incl. half to even, the 1e-8 clamp, the j / j + K/2 pairing)
   dequant / w4a16    all-0x88 -> 0; single nonzero nibble -> a[:, k] * (q - 8) * s; torch
                      float64 matmul
   paged_attention    torch scaled_dot_product_attention in float64 (library) on a dense
                      gather; brute-force Python softmax; constant-V and single-key closed
                      forms; invariance under a consistent pool permutation
   silu_mul           torch.nn.functional.silu
+  cpu_baseline.*     the torch formulas bench.py times on the host: bit-exact (W8A8) or to
+                     tolerance (W4A16, attention) against the pinned numpy oracle above
 """
 import math
 
@@ -128,17 +132,34 @@ def test_int4_round_trips_exhaustive():
     assert words.view(np.uint32)[0, 0] == 0x76543210
 
 
-def test_int4_quantizer_matches_torch_restatement():
-    w = torch.randn(64, 512, generator=torch.Generator().manual_seed(4))
-    packed, sc, deq = O.quantize_weight_int4(w.numpy(), 128)
-    wg = w.float().view(64, 4, 128)
-    sct = wg.abs().amax(-1).clamp(min=1e-8) / 7.0
-    q = torch.round(wg / sct[..., None]).clamp(-8, 7).view(64, 512).to(torch.int16) + 8
-    ref_packed = (q[:, :256] | (q[:, 256:] << 4)).to(torch.uint8)
-    assert np.array_equal(packed, ref_packed.numpy())
-    assert np.array_equal(sc, sct.half().numpy())
-    ref_deq = ((q - 8).float().view(64, 4, 128) * sct[..., None]).view(64, 512).half()
-    assert np.array_equal(deq.view(np.uint16), ref_deq.numpy().view(np.uint16))
+def test_int4_quantizer_known_answers():
+    # Hand-worked case of kernels.py:138-147 with group 4 (K = 16, K/2 = 8 holds two groups).
+    #   row 0, group 0: amax 7 -> sc = 1 exactly; 7, 3.5, -2.5, 0.5 -> 7, 4, -2, 0 (half to even)
+    #   row 0, group 1: all zero -> sc = 1e-8 / 7 (fp16: 0), q = 0
+    #   row 0, group 2: amax 0.7 -> sc = fp32(0.1); -0.7, 0.12, 0.33, -0.04 -> -7, 1, 3, 0
+    #   row 0, group 3: amax 0.014 -> sc = fp32(0.002); 0, -0.0031, 0.0062, 0.014 -> 0, -2, 3, 7
+    #   row 1: amax 7 in every group, integer weights -> q = w
+    w = np.array([[7.0, 3.5, -2.5, 0.5, 0, 0, 0, 0, -0.7, 0.12, 0.33, -0.04, 0.0, -0.0031, 0.0062, 0.014],
+                  [-7, -6, -5, -4, 7, 6, 5, 4, 1, 2, 3, 7, -1, -2, -3, 7]], np.float32)
+    packed, sc, deq = O.quantize_weight_int4(w, 4)
+    # byte j holds k = j in its low nibble and k = j + 8 in its high nibble, each as q + 8
+    assert packed.tolist() == [[0x1F, 0x9C, 0xB6, 0x88, 0x88, 0x68, 0xB8, 0xF8],
+                               [0x91, 0xA2, 0xB3, 0xF4, 0x7F, 0x6E, 0x5D, 0xFC]]
+    # fp16 scales: 1, 1e-8/7 underflows to 0, fp16(0.1), fp16(0.002)
+    assert sc.astype(np.float64).tolist() == [[1.0, 0.0, 0.0999755859375, 0.0020008087158203125], [1.0] * 4]
+    # deq = fp16(q * sc) with the fp32 scale: -7 * fp32(0.1) -> -0.7001953125, where the fp16
+    # scale would give -0.69970703125 (and 3 -> 0.300048828125 against 0.2998046875)
+    assert deq[0].astype(np.float64).tolist() == [7.0, 4.0, -2.0, 0.0, 0.0, 0.0, 0.0, 0.0,
+                                                  -0.7001953125, 0.0999755859375, 0.300048828125, 0.0,
+                                                  0.0, -0.004001617431640625, 0.006000518798828125,
+                                                  0.01399993896484375]
+    assert deq[1].astype(np.float64).tolist() == w[1].astype(np.float64).tolist()
+    # |w / sc| <= 7 always, so nibbles stay in 1..15 (the -8 clamp is never reached)
+    big = np.random.default_rng(3).standard_normal((16, 256)).astype(np.float32)
+    nib = O.unpack_int4_u8(O.quantize_weight_int4(big, 128)[0])
+    assert nib.min() >= 1 and nib.max() <= 15
+    with pytest.raises(AssertionError):
+        O.quantize_weight_int4(np.zeros((1, 24), np.float32), 8)     # (K/2) % group != 0
 
 
 def test_w4a16_kats_and_torch():
@@ -236,6 +257,19 @@ def test_attention_pool_permutation_invariance():
     inv = np.argsort(perm)
     got = O.paged_attention(q, kc[perm], vc[perm], ks[perm], vs[perm], inv[bt].astype(np.int32), cl, 3)
     assert np.array_equal(base, got)
+
+
+def test_attention_magnitude_closed_forms():
+    # mag = sum_t p_t |v_t vs_t|: equals the output when every V entry is >= 0, bounds |out|
+    # always, and is the output of the same cache with |V|.
+    kc, vc, ks, vs, bt, cl = _small_cache(40)
+    q = rng(41).standard_normal((2, 3, 8, 16)).astype(np.float16)
+    out, mag = O.paged_attention(q, kc, vc, ks, vs, bt, cl, 3, magnitude=True)
+    assert (mag >= np.abs(out) - 1e-12).all()
+    absv = np.abs(vc.astype(np.int16)).astype(np.int8)
+    pos_out, pos_mag = O.paged_attention(q, kc, absv, ks, vs, bt, cl, 3, magnitude=True)
+    assert np.allclose(pos_out, pos_mag, rtol=1e-12, atol=0) and np.allclose(pos_mag, mag, rtol=1e-12, atol=0)
+    assert np.array_equal(out, O.paged_attention(q, kc, vc, ks, vs, bt, cl, 3))
 
 
 def test_silu_mul_matches_torch():
@@ -362,3 +396,51 @@ def test_w4a8_channel_quantizer_matches_torch_restatement():
     packed, tsc = K.quantize_weight_int4_channel(torch.from_numpy(w))
     assert np.array_equal(O.unpack_int4_u8(packed.numpy()), qu)
     assert np.array_equal(tsc.numpy().view(np.uint32), sc.view(np.uint32))
+
+
+# ---------------------------------------------------------------- CPU baseline formulas
+def test_cpu_baseline_w8a8_int_mm_is_bitexact():
+    from oracle import cpu_baseline as C
+    r = rng(30)
+    a = r.integers(-127, 128, (20, 4096), dtype=np.int8)
+    w = r.integers(-127, 128, (48, 4096), dtype=np.int8)
+    sa = r.uniform(0.005, 0.02, 20).astype(np.float32)
+    sw = r.uniform(0.001, 0.01, 48).astype(np.float32)
+    got = C.w8a8_int_mm(torch.from_numpy(a), torch.from_numpy(sa), torch.from_numpy(w).T.contiguous(),
+                        torch.from_numpy(sw)).numpy()
+    assert np.array_equal(got.view(np.uint16), O.w8a8(a, sa, w, sw).view(np.uint16))
+
+
+def test_cpu_baseline_fp32_formula_exact_below_2_24():
+    # With 127 * 127 * K < 2**24 every fp32 partial sum is exact, so the reference test's float
+    # formula equals the kernel's fp32 epilogue value and rounds to the same fp16.
+    from oracle import cpu_baseline as C
+    r = rng(31)
+    K = 1040
+    assert 127 * 127 * K < 2 ** 24
+    a = np.full((3, K), 127, np.int8); a[1] = -127; a[2] = r.integers(-127, 128, K, dtype=np.int8)
+    w = r.integers(-127, 128, (40, K), dtype=np.int8); w[0] = 127
+    sa = r.uniform(0.005, 0.02, 3).astype(np.float32)
+    sw = r.uniform(0.001, 0.01, 40).astype(np.float32)
+    got = C.w8a8_fp32_formula(torch.from_numpy(a), torch.from_numpy(sa), torch.from_numpy(w), torch.from_numpy(sw))
+    assert np.array_equal(got.half().numpy().view(np.uint16), O.w8a8(a, sa, w, sw).view(np.uint16))
+
+
+def test_cpu_baseline_w4a16_and_attention_match_oracle():
+    from oracle import cpu_baseline as C
+    r = rng(32)
+    N, K, G = 64, 512, 128
+    qu = r.integers(0, 16, (N, K)).astype(np.uint8)
+    sc = r.uniform(0.002, 0.02, (N, K // G)).astype(np.float16)
+    x = r.standard_normal((9, K)).astype(np.float16)
+    deq = O.dequant_int4(qu, sc, G)
+    got = C.w4a16_fp32(torch.from_numpy(x), torch.from_numpy(deq)).float().numpy()
+    ref = O.w4a16(x, qu, sc, G)
+    assert np.abs(got - ref).max() <= 2e-3 * np.abs(ref).max()
+    zero = C.w4a16_fp32(torch.from_numpy(x), torch.zeros((N, K), dtype=torch.float16))
+    assert (zero == 0).all()
+    kc, vc, ks, vs, bt, cl = _small_cache(33, B=2, ctx=(45, 19), H=8, H_KV=2, D=32)
+    q = rng(34).standard_normal((2, 4, 8, 32)).astype(np.float16)
+    got = C.paged_attention_fp32(*(torch.from_numpy(t) for t in (q, kc, vc, ks, vs, bt, cl)), 3).float().numpy()
+    ref = O.paged_attention(q, kc, vc, ks, vs, bt, cl, 3)
+    assert np.abs(got[:, :3] - ref[:, :3]).max() < 2e-3 and (got[:, 3:] == 0).all()
