@@ -94,6 +94,22 @@ int specq_w8a8_packed(const int8_t* a, int64_t lda, const void* w_packed,
                       int block_m, int block_n, int num_warps, int split_k,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* W8A8 on packed weights without a workspace argument: the same computation and tiles as
+ * specq_w8a8_packed (bit-identical results), with the split-K counters and INT32 partial tiles
+ * held in a static device array of SPECQ_NOALLOC_SCRATCH_BYTES bytes that each GPU keeps for the
+ * life of the process.  No reference counterpart: it is for callers that cannot allocate device
+ * memory (code under graph capture, serving loops that forbid allocation).  It allocates and
+ * frees nothing.  A call whose tiles need more scratch than the array holds returns
+ * SPECQ_ENOSPC before any launch (every config-1 shape at M <= 300 with the automatic tile fits).
+ * The counters a call uses are zeroed by a fill kernel on `stream` before the GEMM.  Every call
+ * on a GPU shares that GPU's array, so calls that may overlap on one GPU (different streams)
+ * race and must not be issued concurrently. */
+#define SPECQ_NOALLOC_SCRATCH_BYTES (32u * 1024u * 1024u)
+int specq_w8a8_packed_noalloc(const int8_t* a, int64_t lda, const void* w_packed,
+                              const float* sa, const float* sw, void* c, int64_t ldc,
+                              int M, int N, int K, int grid_m_max, const int32_t* plan,
+                              int block_m, int block_n, int num_warps, int split_k, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * W4A8 GEMM: C[m, n] = fp16( (float(sum_k A[m,k] * q[n,k]) * sa[m]) * sw[n] ) with q the
  * signed INT4 weight in [-8, 7] and a per-channel fp32 scale sw, so the INT4 weights run on

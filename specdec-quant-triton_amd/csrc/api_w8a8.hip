@@ -11,6 +11,8 @@
 // families with the same tiles.
 #include <algorithm>
 #include <atomic>
+#include <mutex>
+#include <vector>
 
 #include "api_common.hpp"
 #include "w8a8.hpp"
@@ -84,6 +86,41 @@ __global__ __launch_bounds__(256) void w4a8_pack_kernel(const uint8_t* __restric
     d[dd] = v;
   }
   *reinterpret_cast<v2i*>(out + frag * 512 + l * 8) = v2i{(int)d[0], (int)d[1]};
+}
+
+// Device scratch of the allocation-free entry point specq_w8a8_packed_noalloc: the split-K
+// counters (the first kCounterBytes) and the INT32 partial tiles.  Each GPU the library runs on
+// holds its own copy until the process ends.  In host code `scratch` is only a stand-in for
+// the symbol: its device address on a GPU comes from hipGetSymbolAddress with that GPU current.
+static __device__ __align__(256) uint8_t scratch[SPECQ_NOALLOC_SCRATCH_BYTES];
+static_assert(SPECQ_NOALLOC_SCRATCH_BYTES > kCounterBytes, "scratch holds the counter region");
+
+// Zeroes n int32 counters (a fill kernel, not a memset node, so the call may be captured).
+__global__ __launch_bounds__(256) void zero_i32_kernel(int32_t* __restrict__ p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// Device address of `scratch` on the current GPU, looked up once per GPU.
+static int noalloc_scratch(void** out) {
+  static std::mutex mu;
+  static std::vector<void*> ptrs;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return fail(SPECQ_EIO, "w8a8_packed_noalloc: no current device");
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)ptrs.size() <= dev) ptrs.resize(dev + 1, nullptr);
+  if (ptrs[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error("w8a8_packed_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return SPECQ_EIO;
+    }
+    ptrs[dev] = ptr;
+  }
+  *out = ptrs[dev];
+  return SPECQ_OK;
 }
 
 // Kernel family override (0 = automatic), set through specq_set_option("w8a8_path", v).
@@ -349,9 +386,13 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   return SPECQ_OK;
 }
 
+// With `static_scratch` the call runs on the device scratch array instead of a caller workspace:
+// it is refused when it needs more than that array holds, and the counters it uses are zeroed
+// (on the stream, before the GEMM) rather than assumed zero.
 int run_w8a8(int layout, const int8_t* a, int64_t lda, const void* w, int64_t ldw, const float* sa, const float* sw,
              void* c, int64_t ldc, int M, int N, int K, int grid_m_max, const int32_t* plan, int block_m, int block_n,
-             int num_warps, int split_k, void* workspace, size_t workspace_bytes, void* stream) {
+             int num_warps, int split_k, void* workspace, size_t workspace_bytes, void* stream,
+             bool static_scratch = false) {
   SPECQ_REQUIRE(M >= 0 && N > 0 && K > 0, SPECQ_EINVAL, "w8a8: bad sizes M=%d N=%d K=%d", M, N, K);
   SPECQ_REQUIRE(a && w && sa && sw && c, SPECQ_EINVAL, "w8a8: null tensor pointer");
   SPECQ_REQUIRE(lda >= K && (layout != 0 || ldw >= K) && ldc >= N, SPECQ_EINVAL,
@@ -370,6 +411,17 @@ int run_w8a8(int layout, const int8_t* a, int64_t lda, const void* w, int64_t ld
   int rc = w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, vec, plan != nullptr, &cfg);
   if (rc) return rc;
   const size_t need = cfg.ws_partials + cfg.ws_counters;
+  if (static_scratch) {
+    SPECQ_REQUIRE(need <= SPECQ_NOALLOC_SCRATCH_BYTES, SPECQ_ENOSPC,
+                  "w8a8_packed_noalloc: this call needs %zu bytes of scratch, the static scratch holds %zu "
+                  "(split_k=%d, BLOCK_M=%d); use specq_w8a8_packed with a workspace",
+                  need, (size_t)SPECQ_NOALLOC_SCRATCH_BYTES, cfg.splits, cfg.mt * 16);
+    if (need) {
+      rc = noalloc_scratch(&workspace);
+      if (rc) return rc;
+      workspace_bytes = SPECQ_NOALLOC_SCRATCH_BYTES;
+    }
+  }
   SPECQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), SPECQ_ENOSPC,
                 "w8a8: workspace of %zu bytes required, %zu given", need, workspace ? workspace_bytes : 0);
   rc = ensure_lds(cfg.fn, cfg.lds);
@@ -383,6 +435,17 @@ int run_w8a8(int layout, const int8_t* a, int64_t lda, const void* w, int64_t ld
   p.partials = need ? reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + kCounterBytes) : nullptr;
   p.vec_store = ((uintptr_t)c % 8 == 0) && (ldc % 4 == 0) && ((uintptr_t)sw % 16 == 0);
   const int grid = chunked_grid(cfg.n_tiles * cfg.splits, cfg.m_chunks);
+  if (static_scratch && need) {
+    int n_ctr = cfg.m_chunks * cfg.n_tiles;
+    int32_t* ctr = p.counters;
+    void* zargs[] = {(void*)&ctr, (void*)&n_ctr};
+    const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&zero_i32_kernel), dim3(ceil_div(n_ctr, 256)),
+                                         dim3(256), zargs, 0, reinterpret_cast<hipStream_t>(stream));
+    if (e != hipSuccess) {
+      set_error("w8a8_packed_noalloc: counter clear failed: %s", hipGetErrorString(e));
+      return SPECQ_EIO;
+    }
+  }
   return launch(cfg.fn, grid, cfg.nw * 64, cfg.lds, reinterpret_cast<hipStream_t>(stream), &p);
 }
 
@@ -488,6 +551,15 @@ extern "C" int specq_w8a8_packed(const int8_t* a, int64_t lda, const void* w_pac
   clear_error();
   return run_w8a8(1, a, lda, w_packed, 0, sa, sw, c, ldc, M, N, K, grid_m_max, plan, block_m, block_n, num_warps,
                   split_k, workspace, workspace_bytes, stream);
+}
+
+extern "C" int specq_w8a8_packed_noalloc(const int8_t* a, int64_t lda, const void* w_packed, const float* sa,
+                                         const float* sw, void* c, int64_t ldc, int M, int N, int K, int grid_m_max,
+                                         const int32_t* plan, int block_m, int block_n, int num_warps, int split_k,
+                                         void* stream) {
+  clear_error();
+  return run_w8a8(1, a, lda, w_packed, 0, sa, sw, c, ldc, M, N, K, grid_m_max, plan, block_m, block_n, num_warps,
+                  split_k, nullptr, 0, stream, /*static_scratch=*/true);
 }
 
 extern "C" int specq_set_option(const char* name, int value) {

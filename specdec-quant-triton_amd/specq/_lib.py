@@ -44,6 +44,9 @@ SIGNATURES = {
     "specq_w8a8_packed": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
                                    _c_int, _c_int, _c_int, _c_int, _c_vp,
                                    _c_int, _c_int, _c_int, _c_int, _c_vp, _c_size, _c_vp]),
+    "specq_w8a8_packed_noalloc": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
+                                           _c_int, _c_int, _c_int, _c_int, _c_vp,
+                                           _c_int, _c_int, _c_int, _c_int, _c_vp]),
     "specq_w4a8_packed_bytes": (_c_size, [_c_int, _c_int]),
     "specq_w4a8_pack_weight": (_c_int, [_c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp, _c_vp]),
     "specq_w4a8_packed_workspace_size": (_c_size, [_c_int] * 7),
