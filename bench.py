@@ -1,29 +1,30 @@
 """Benchmark of the quantized verification path on one MI355X (prints one JSON line).
 
-Workload: W8A8 GEMMs over the reference's per-layer Llama-3-8B linears (bench_matmul.py:16:
-qkv 6144x4096, o 4096x4096, gate_up 28672x4096, down 4096x14336; the config-1 shapes fused as
-the reference benchmarks them) at the verification batch M = B*(k+1) = 8*9 = 72.  One step is
-the linears of one verification forward: 32 layers x 4 GEMMs = 128 launches streaming 6.98 GB
-of distinct INT8 weights (far beyond the 256 MiB Infinity Cache, so every step reads its
-weights from HBM).  The step is captured once into a hipGraph (torch.cuda.graph over the
-C-ABI launches) and replayed; inputs are resident in HBM before the timed region starts.
-Weights are packed once, at load time, into the kernel's MFMA-fragment layout
-(pack_weight_int8; bit-identical results); the same step on row-major weights (the
-reference's w_q layout) and on the seven unfused config-1 linears (q, k, v, o, gate, up, down)
-are reported in `detail`.
+Workload: W8A8 GEMMs over the seven linears of a Llama-3-8B layer (N x K:
+q 4096x4096, k and v 1024x4096, o 4096x4096, gate and up 14336x4096, down 4096x14336) at the
+verification batch M = B*(k+1) = 8*9 = 72.  One step is the linears of one verification
+forward: 32 layers x 7 GEMMs streaming 6.98 GB of distinct INT8 weights (far beyond the
+256 MiB Infinity Cache, so every step reads its weights from HBM).  The GEMMs that share an
+activation in a model layer run as one grouped launch over their separate weight tensors
+(q|k|v and gate|up; w8a8_matmul_grouped), so a layer is 4 launches.  Weights are packed once at
+load time into the kernel's MFMA-fragment layout (pack_weight_int8; bit-identical results).
+The step is captured once into a hipGraph and replayed; inputs are resident in HBM before the
+timed region starts.
 
-  value        algorithmic HBM bytes of a step / step time, in GB/s (whole job, one GPU)
-  roofline     the dominant kernel (the gate_up GEMM, 54% of the bytes): algorithmic bytes per
-               launch / its mean launch duration, measured with HIP events around a graph of
-               back-to-back launches on the stream the kernels run on, against 8 TB/s
-  cpu_baseline the CPU oracle (oracle/oracle.py, numpy) on one layer's linears at the same M,
-               timed on the host cores for a bounded ~10 s sample
-  detail       the k=0 decode step (M=8) on the same weights and the verify/decode ratio
-               (target <= 1.1), W4A16 at M=72 and M=8 (load-time packed INT4, and the int32
-               packing as given at M=72), W4A8 at M=72 and M=8 (packed INT4 weights on the
-               INT8 MFMA path), INT8 paged verification attention at B=8, k=8, the paged
-               KV-cache append of the k+1 new tokens, and the plan-buffer graph replay of the
-               config-4 stack
+  value        algorithmic HBM bytes of a step / step time, in GB/s (whole job, one GPU): every
+               weight, channel scale and output once, and each launch's activations and token
+               scales once
+  roofline     the dominant kernel (the grouped gate|up launch, 54% of the bytes): algorithmic
+               bytes per launch / its mean launch duration, measured with HIP events around a
+               graph of back-to-back launches on the stream the kernels run on, against 8 TB/s
+  cpu_baseline the reference's PyTorch formulas on the host cores (oracle/cpu_baseline.py,
+               BASELINE.md section 3): torch._int_mm with the fp32 epilogue on one layer's seven
+               linears at M = 72 (the value), plus the fp32 formula, W4A16 and attention timings
+  detail       the k=0 decode step (M = 8) and the verify/decode ratio (target <= 1.1); the same
+               step as 7 separate launches per layer, on row-major weights, and on the fused
+               weights the reference benchmarks (bench_matmul.py:16); per-launch times; W4A16
+               and W4A8 steps; INT8 paged verification attention at B=8, k=8; the paged
+               KV-cache append; and the plan-buffer graph replay of the config-4 stack
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-detail]
 """
@@ -44,11 +45,14 @@ for _p in (ROOT, PKG):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
-# One layer's linears as the reference benchmarks them (bench_matmul.py:16), and unfused.
+# The seven linears of a Llama-3-8B layer, and how a layer launches them:
+# GEMMs that share an activation run as one grouped launch.
+CONFIG1 = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+           ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+LAUNCHES = [("qkv", ("q", "k", "v")), ("o", ("o",)), ("gate_up", ("gate", "up")), ("down", ("down",))]
+# The reference's own benchmark fuses the weights instead (bench_matmul.py:16).
 LINEARS = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 28672, 4096), ("down", 4096, 14336)]
-SPLIT_LINEARS = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
-                 ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
-DOMINANT = ("gate_up", 28672, 4096)
+DOMINANT = "gate_up"
 METRIC = "GEMM µs & HBM GB/s vs M=B·(k+1); INT8 verify-attn µs at k=8; graph replay µs"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -60,6 +64,18 @@ def log(msg: str) -> None:
 def w8a8_bytes(M: int, N: int, K: int) -> int:
     """Algorithmic HBM bytes of one W8A8 call: W, A, sa, sw read once, C written once."""
     return N * K + M * K + 4 * M + 4 * N + 2 * M * N
+
+
+def grouped_bytes(M: int, shapes) -> int:
+    """Algorithmic HBM bytes of one launch of GEMMs sharing an activation [M, K]: every weight,
+    channel scale and output once, the activation and token scales once."""
+    K = shapes[0][1]
+    return sum(N * Kd + 4 * N + 2 * M * N for N, Kd in shapes) + M * K + 4 * M
+
+
+def config1_step_bytes(M: int, layers: int) -> int:
+    shape = {n: (N, Kd) for n, N, Kd in CONFIG1}
+    return layers * sum(grouped_bytes(M, [shape[m] for m in mem]) for _, mem in LAUNCHES)
 
 
 def w4a16_bytes(M: int, N: int, K: int, group: int = 128) -> int:
@@ -133,66 +149,100 @@ def make_weights(K, L: int, seed: int = 0, packed: bool = True, linears=LINEARS)
 
 
 def w8a8_step_fn(K, layers, acts, M, outs, linears=LINEARS):
+    """One launch per linear (each on the activation of its K)."""
     a, sa, a_ff = acts[0][:M], acts[1][:M], acts[2][:M]
 
     def step():
         for lw in layers:
             for name, N, Kd in linears:
                 w, sw = lw[name]
-                K.w8a8_matmul(a if Kd == a.shape[1] else a_ff, sa, w, sw, out=outs[N][:M], BLOCK_M=None)
+                K.w8a8_matmul(a if Kd == a.shape[1] else a_ff, sa, w, sw, out=outs[name][:M], BLOCK_M=None)
     return step
+
+
+def config1_step_fn(K, layers, acts, M, outs):
+    """A layer's seven linears as 4 launches: q|k|v and gate|up grouped, o and down alone."""
+    a, sa, a_ff = acts[0][:M], acts[1][:M], acts[2][:M]
+    shape = {n: (N, Kd) for n, N, Kd in CONFIG1}
+
+    def step():
+        for lw in layers:
+            for _, mem in LAUNCHES:
+                x = a if shape[mem[0]][1] == a.shape[1] else a_ff
+                if len(mem) == 1:
+                    K.w8a8_matmul(x, sa, *lw[mem[0]], out=outs[mem[0]][:M], BLOCK_M=None)
+                else:
+                    K.w8a8_matmul_grouped(x, sa, [lw[m] for m in mem], outs=[outs[m][:M] for m in mem], BLOCK_M=None)
+    return step
+
+
+def per_launch_us(K, torch, layers, acts, M, outs, args):
+    """Mean duration of each of a layer's 4 launches at M: a graph of the launch over every
+    layer's weights, timed with events on the stream it runs on."""
+    shape = {n: (N, Kd) for n, N, Kd in CONFIG1}
+    res = {}
+    for lname, mem in LAUNCHES:
+        x = acts[0][:M] if shape[mem[0]][1] == acts[0].shape[1] else acts[2][:M]
+        sa = acts[1][:M]
+
+        def run(mem=mem, x=x, sa=sa):
+            for lw in layers:
+                K.w8a8_matmul_grouped(x, sa, [lw[m] for m in mem], outs=[outs[m][:M] for m in mem], BLOCK_M=None)
+        run()
+        torch.cuda.synchronize()
+        g = capture(run)
+        ms = time_replays(g, max(5, args.steps), 2)
+        us = ms * 1e3 / len(layers)
+        b = grouped_bytes(M, [shape[m] for m in mem])
+        _, ck = K.w8a8_matmul_grouped(x, sa, [layers[0][m] for m in mem], outs=[outs[m][:M] for m in mem],
+                                      BLOCK_M=None)
+        res[lname] = dict(us=us, bytes=b, GBps=b / (us * 1e-6) / 1e9, kernel=ck.name, config=ck.config)
+        del g
+    return res
 
 
 # ------------------------------------------------------------------------------------------
 # Parts of the run
 # ------------------------------------------------------------------------------------------
 def bench_w8a8(args, K, torch):
-    layers = make_weights(K, args.layers, seed=1, packed=True)
     g = torch.Generator(device="cuda").manual_seed(2)
     M_max = 300
     a = torch.randint(-127, 128, (M_max, 4096), dtype=torch.int8, device="cuda", generator=g)
     a_ff = torch.randint(-127, 128, (M_max, 14336), dtype=torch.int8, device="cuda", generator=g)
     sa = torch.rand((M_max,), device="cuda", generator=g) * 0.015 + 0.005
     acts = (a, sa, a_ff)
-    outs = {N: torch.empty((M_max, N), dtype=torch.float16, device="cuda")
-            for N in {n for _, n, _ in LINEARS + SPLIT_LINEARS}}
+    outs = {name: torch.empty((M_max, N), dtype=torch.float16, device="cuda")
+            for name, N, _ in CONFIG1 + LINEARS}
     res = {}
+    layers = make_weights(K, args.layers, seed=1, packed=True, linears=CONFIG1)
     for label, M in (("verify", args.B * (args.k + 1)), ("decode", args.B)):
-        step = w8a8_step_fn(K, layers, acts, M, outs)
+        step = config1_step_fn(K, layers, acts, M, outs)
         step()
         torch.cuda.synchronize()
         graph = capture(step)
-        bytes_step = args.layers * sum(w8a8_bytes(M, N, Kd) for _, N, Kd in LINEARS)
-        log(f"w8a8 {label} M={M}: warmup {args.warmup}, timing {args.steps} steps")
+        bytes_step = config1_step_bytes(M, args.layers)
+        log(f"w8a8 config-1 {label} M={M}: warmup {args.warmup}, timing {args.steps} steps")
         ms = time_replays(graph, args.steps, args.warmup)
         res[label] = dict(M=M, ms=ms, bytes=bytes_step, GBps=bytes_step / (ms * 1e-3) / 1e9)
         del graph
-
-    # Dominant kernel (gate_up shape): a graph of back-to-back launches over every layer's
-    # gate_up weights, timed with events on the stream the launches run on.
+        # The same step as 7 separate launches per layer.
+        step = w8a8_step_fn(K, layers, acts, M, outs, linears=CONFIG1)
+        step()
+        torch.cuda.synchronize()
+        graph = capture(step)
+        ms = time_replays(graph, args.steps, args.warmup)
+        res[label + "_7_launches"] = dict(M=M, ms=ms, GBps=args.layers * sum(w8a8_bytes(M, N, Kd) for _, N, Kd in CONFIG1)
+                                          / (ms * 1e-3) / 1e9)
+        del graph
+    # Per-launch durations at the verification M; the dominant one is the roofline kernel.
     M = res["verify"]["M"]
-    dname, N, Kd = DOMINANT
-    outg = outs[N][:M]
-
-    def dom():
-        for lw in layers:
-            K.w8a8_matmul(a[:M], sa[:M], *lw[dname], out=outg, BLOCK_M=None)
-    dom()
-    torch.cuda.synchronize()
-    gdom = capture(dom)
-    launches = args.layers
-    ms = time_replays(gdom, max(5, args.steps), 2)
-    us_launch = ms * 1e3 / launches
-    _, ck = K.w8a8_matmul(a[:M], sa[:M], *layers[0][dname], out=outg, BLOCK_M=None)
-    dom_bytes = w8a8_bytes(M, N, Kd)
-    res["dominant"] = dict(kernel=ck.name, M=M, N=N, K=Kd, us=us_launch, bytes=dom_bytes,
-                           GBps=dom_bytes / (us_launch * 1e-6) / 1e9, config=ck.config)
-    del gdom, layers
+    res["launches"] = per_launch_us(K, torch, layers, acts, M, outs, args)
+    res["launches_decode"] = per_launch_us(K, torch, layers, acts, args.B, outs, args)
+    del layers
     torch.cuda.empty_cache()
     # The same verification step on row-major weights (the reference's w_q layout).
-    layers = make_weights(K, args.layers, seed=1, packed=False)
-    M = res["verify"]["M"]
-    step = w8a8_step_fn(K, layers, acts, M, outs)
+    layers = make_weights(K, args.layers, seed=1, packed=False, linears=CONFIG1)
+    step = config1_step_fn(K, layers, acts, M, outs)
     step()
     torch.cuda.synchronize()
     graph = capture(step)
@@ -200,16 +250,16 @@ def bench_w8a8(args, K, torch):
     res["verify_rowmajor"] = dict(M=M, ms=ms, GBps=res["verify"]["bytes"] / (ms * 1e-3) / 1e9)
     del graph, layers
     torch.cuda.empty_cache()
-    # The seven unfused config-1 linears (packed weights), verification and decode.
-    layers = make_weights(K, args.layers, seed=1, packed=True, linears=SPLIT_LINEARS)
-    for label, M in (("verify_split", args.B * (args.k + 1)), ("decode_split", args.B)):
-        step = w8a8_step_fn(K, layers, acts, M, outs, linears=SPLIT_LINEARS)
+    # The reference's fused-weight shapes (bench_matmul.py:16), verification and decode.
+    layers = make_weights(K, args.layers, seed=1, packed=True, linears=LINEARS)
+    for label, Mx in (("verify_fused_weights", M), ("decode_fused_weights", args.B)):
+        step = w8a8_step_fn(K, layers, acts, Mx, outs, linears=LINEARS)
         step()
         torch.cuda.synchronize()
         graph = capture(step)
         ms = time_replays(graph, args.steps, args.warmup)
-        b = args.layers * sum(w8a8_bytes(M, N, Kd) for _, N, Kd in SPLIT_LINEARS)
-        res[label] = dict(M=M, ms=ms, GBps=b / (ms * 1e-3) / 1e9)
+        b = args.layers * sum(w8a8_bytes(Mx, N, Kd) for _, N, Kd in LINEARS)
+        res[label] = dict(M=Mx, ms=ms, GBps=b / (ms * 1e-3) / 1e9)
         del graph
     del layers
     torch.cuda.empty_cache()
@@ -217,14 +267,14 @@ def bench_w8a8(args, K, torch):
 
 
 def bench_w4a16(args, K, torch):
-    """W4A16 over the same per-layer linears, M = 72 and 8: INT4 weights (int32, 8 nibbles per word)
-    packed once at load into MFMA fragments (pack_weight_int4), and the int32 weights as given
-    for the verification step."""
+    """W4A16 (config 2) over the seven config-1 linears, M = 72 and 8: INT4 weights (int32, 8
+    nibbles per word) packed once at load into MFMA fragments (pack_weight_int4), and the int32
+    weights as given for the verification step; one launch per linear."""
     g = torch.Generator(device="cuda").manual_seed(3)
     layers, raw = [], []
     for _ in range(args.layers):
         lw, lr = {}, {}
-        for name, N, Kd in LINEARS:
+        for name, N, Kd in CONFIG1:
             wp = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, Kd // 8), dtype=torch.int32, device="cuda", generator=g)
             sc = (torch.rand((N, Kd // 128), device="cuda", generator=g) * 0.018 + 0.002).half()
             lw[name] = (K.pack_weight_int4(wp), sc)
@@ -233,21 +283,21 @@ def bench_w4a16(args, K, torch):
         raw.append(lr)
     x = torch.randn((300, 4096), device="cuda", generator=g).half()
     x_ff = torch.randn((300, 14336), device="cuda", generator=g).half()
-    outs = {N: torch.empty((300, N), dtype=torch.float16, device="cuda") for N in {n for _, n, _ in LINEARS}}
+    outs = {name: torch.empty((300, N), dtype=torch.float16, device="cuda") for name, N, _ in CONFIG1}
     res = {}
     for label, M, ls in (("verify", args.B * (args.k + 1), layers), ("decode", args.B, layers),
                          ("verify_int32", args.B * (args.k + 1), raw)):
         def step():
             for lw in ls:
-                for name, N, Kd in LINEARS:
-                    K.w4a16_matmul(x[:M] if Kd == 4096 else x_ff[:M], *lw[name], out=outs[N][:M], BLOCK_M=None)
+                for name, N, Kd in CONFIG1:
+                    K.w4a16_matmul(x[:M] if Kd == 4096 else x_ff[:M], *lw[name], out=outs[name][:M], BLOCK_M=None)
         step()
         torch.cuda.synchronize()
         graph = capture(step)
         log(f"w4a16 {label} M={M}")
         ms = time_replays(graph, args.steps, args.warmup)
-        b = args.layers * sum(w4a16_bytes(M, N, Kd) for _, N, Kd in LINEARS)
-        flops = args.layers * sum(2 * M * N * Kd for _, N, Kd in LINEARS)
+        b = args.layers * sum(w4a16_bytes(M, N, Kd) for _, N, Kd in CONFIG1)
+        flops = args.layers * sum(2 * M * N * Kd for _, N, Kd in CONFIG1)
         res[label] = dict(M=M, ms=ms, GBps=b / (ms * 1e-3) / 1e9, TFLOPs=flops / (ms * 1e-3) / 1e12)
         del graph
     del layers, raw
@@ -261,13 +311,14 @@ def w4a8_bytes(M: int, N: int, K: int) -> int:
 
 
 def bench_w4a8(args, K, torch):
-    """W4A8 (INT4 weights on the INT8 MFMA path, per-channel scale) over the same per-layer
-    linears, M = 72 and 8, weights packed once at load (pack_weight_w4a8)."""
+    """W4A8 (INT4 weights on the INT8 MFMA path, per-channel scale) over the seven config-1
+    linears, M = 72 and 8, weights packed once at load (pack_weight_w4a8), q|k|v and gate|up as
+    grouped launches like the W8A8 step."""
     g = torch.Generator(device="cuda").manual_seed(4)
     layers = []
     for _ in range(args.layers):
         lw = {}
-        for name, N, Kd in LINEARS:
+        for name, N, Kd in CONFIG1:
             wp = torch.randint(0, 256, (N, Kd // 2), dtype=torch.uint8, device="cuda", generator=g)
             sw = torch.rand((N,), device="cuda", generator=g) * 0.009 + 0.001
             lw[name] = (K.pack_weight_w4a8(wp), sw)
@@ -276,20 +327,22 @@ def bench_w4a8(args, K, torch):
     a = torch.randint(-127, 128, (300, 4096), dtype=torch.int8, device="cuda", generator=g)
     a_ff = torch.randint(-127, 128, (300, 14336), dtype=torch.int8, device="cuda", generator=g)
     sa = torch.rand((300,), device="cuda", generator=g) * 0.015 + 0.005
-    outs = {N: torch.empty((300, N), dtype=torch.float16, device="cuda") for N in {n for _, n, _ in LINEARS}}
+    outs = {name: torch.empty((300, N), dtype=torch.float16, device="cuda") for name, N, _ in CONFIG1}
+    shape = {n: (N, Kd) for n, N, Kd in CONFIG1}
     res = {}
     for label, M in (("verify", args.B * (args.k + 1)), ("decode", args.B)):
         def step():
             for lw in layers:
-                for name, N, Kd in LINEARS:
-                    K.w4a8_matmul(a[:M] if Kd == 4096 else a_ff[:M], sa[:M], *lw[name], out=outs[N][:M],
-                                  BLOCK_M=None)
+                for _, mem in LAUNCHES:
+                    x = a[:M] if shape[mem[0]][1] == 4096 else a_ff[:M]
+                    K.w8a8_matmul_grouped(x, sa[:M], [lw[m] for m in mem], outs=[outs[m][:M] for m in mem],
+                                          BLOCK_M=None)
         step()
         torch.cuda.synchronize()
         graph = capture(step)
         log(f"w4a8 {label} M={M}")
         ms = time_replays(graph, args.steps, args.warmup)
-        b = args.layers * sum(w4a8_bytes(M, N, Kd) for _, N, Kd in LINEARS)
+        b = args.layers * sum(w4a8_bytes(M, N, Kd) for _, N, Kd in CONFIG1)
         res[label] = dict(M=M, ms=ms, GBps=b / (ms * 1e-3) / 1e9)
         del graph
     del layers
@@ -332,7 +385,8 @@ def bench_attention(args, K, torch):
 
 
 def bench_plan_graph(args, K, torch):
-    """Config 4: a 4-layer INT8 stack (d_model 4096, weights packed at load) replayed over a
+    """Config 4: a 4-layer INT8 stack (d_model 4096, weights packed at load; gate and up as one
+    grouped launch over their separate weights) replayed over a
     seeded (B, k) trace, B in 1..32, k in {0, 2, 4, 8}, under five launch strategies:
       eager     every step launched with its exact shapes
       allshapes one graph per distinct (B, k) of the trace (captured before timing)
@@ -386,8 +440,8 @@ def bench_plan_graph(args, K, torch):
             K.paged_attention(q_buf[:Bg, :qg], kc, vc, ks, vs, bt[:Bg], cl[:Bg], qg, QPP=qg,
                               plan=plan.attn if plan is not None else None, out=o_buf[:Bg, :qg])
             K.w8a8_matmul(aa, ss, *lw["o"], out=bufs["o"][:Mg], BLOCK_M=None, **gk)
-            K.w8a8_matmul(aa, ss, *lw["gate"], out=bufs["gate"][:Mg], BLOCK_M=None, **gk)
-            K.w8a8_matmul(aa, ss, *lw["up"], out=bufs["up"][:Mg], BLOCK_M=None, **gk)
+            K.w8a8_matmul_grouped(aa, ss, [lw["gate"], lw["up"]], outs=[bufs["gate"][:Mg], bufs["up"][:Mg]],
+                                  BLOCK_M=None, **gk)
             K.silu_mul_quant_int8(bufs["gate"][:Mg], bufs["up"][:Mg], q=hq[:Mg], s=hs[:Mg], **kw)
             K.w8a8_matmul(hq[:Mg], hs[:Mg], *lw["down"], out=bufs["down"][:Mg], BLOCK_M=None, **gk)
 
@@ -474,43 +528,91 @@ def bench_plan_graph(args, K, torch):
 
 
 def cpu_baseline(args, M: int, seconds: float):
-    """The CPU oracle (numpy) on one layer's linears at M, repeated for about `seconds`."""
-    import numpy as np
+    """The reference's PyTorch formulas on the host cores (oracle/cpu_baseline.py, the plan of
+    BASELINE.md section 3), each on a bounded sample of the same workload:
+      value   torch._int_mm + the fp32 epilogue over one layer's seven config-1 linears at M
+      also    the reference test's fp32 formula on the same layer (correctness.py:37), W4A16
+              x.float() @ deq.float().T on the same shapes (correctness.py:76), and dense fp32
+              attention at B=8, k=8, ctx 4096 (kernels.py:289-309)
+    Threads: torch's intra-op pool as configured for the process (OMP_NUM_THREADS)."""
+    import statistics as st
 
-    from oracle import oracle as O
+    import torch
 
+    from oracle import cpu_baseline as C
+
+    cores = torch.get_num_threads()
+    model = "unknown CPU"
     try:
-        from threadpoolctl import threadpool_info
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # noqa: BLE001
-        cores = os.cpu_count() or 1
-    rng = np.random.default_rng(0)
-    ws = [(rng.integers(-127, 128, (N, Kd), dtype=np.int8), rng.uniform(0.001, 0.01, N).astype(np.float32))
-          for _, N, Kd in LINEARS]
-    a = rng.integers(-127, 128, (M, 14336), dtype=np.int8)
-    sa = rng.uniform(0.005, 0.02, M).astype(np.float32)
-    b_layer = sum(w8a8_bytes(M, N, Kd) for _, N, Kd in LINEARS)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        for (w, sw), (_, N, Kd) in zip(ws, LINEARS):
-            O.w8a8(a[:, :Kd], sa, w, sw)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or reps >= 50:
-            break
-    return dict(value=round(reps * b_layer / el / 1e9, 3), unit="GB/s", cores=int(cores), kind="port",
-                sample=f"oracle.w8a8 (numpy) on one layer's Llama-3-8B linears (qkv, o, gate_up, down) at M={M}, {reps} reps "
-                       f"in {el:.1f} s ({reps * b_layer / 1e9:.2f} GB of weights)")
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), model)
+    except OSError:
+        pass
+    g = torch.Generator().manual_seed(0)
+    a4 = torch.randint(-127, 128, (M, 4096), dtype=torch.int8, generator=g)
+    a14 = torch.randint(-127, 128, (M, 14336), dtype=torch.int8, generator=g)
+    sa = torch.rand(M, generator=g) * 0.015 + 0.005
+    ws = {}
+    for name, N, Kd in CONFIG1:
+        w = torch.randint(-127, 128, (N, Kd), dtype=torch.int8, generator=g)
+        ws[name] = (w, w.T.contiguous(), torch.rand(N, generator=g) * 0.009 + 0.001)
+
+    def timed(fn, budget):
+        t_end, times = time.perf_counter() + budget, []
+        fn()  # warm-up
+        while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return st.median(times), len(times)
+
+    def layer_int_mm():
+        for name, N, Kd in CONFIG1:
+            C.w8a8_int_mm(a4 if Kd == 4096 else a14, sa, ws[name][1], ws[name][2])
+
+    def layer_fp32():
+        for name, N, Kd in CONFIG1:
+            C.w8a8_fp32_formula(a4 if Kd == 4096 else a14, sa, ws[name][0], ws[name][2])
+
+    b_layer = config1_step_bytes(M, 1)
+    t_int, n_int = timed(layer_int_mm, seconds * 0.45)
+    t_f32, n_f32 = timed(layer_fp32, seconds * 0.2)
+    del ws
+    # W4A16 on the same shapes: fp16 activations against the dequantised fp16 weights.
+    x4 = torch.randn(M, 4096, generator=g).half()
+    x14 = torch.randn(M, 14336, generator=g).half()
+    deq = {name: (torch.randn(N, Kd, generator=g) * 0.05).half() for name, N, Kd in CONFIG1}
+
+    def layer_w4a16():
+        for name, N, Kd in CONFIG1:
+            C.w4a16_fp32(x4 if Kd == 4096 else x14, deq[name])
+    t_w4, n_w4 = timed(layer_w4a16, seconds * 0.2)
+    del deq
+    from specq import gen
+    kc, vc, ks, vs, bt, cl = gen.paged_kv(8, [4096 + 9] * 8, 8, 128, seed=5)
+    q = gen.queries(8, 9, 32, 128, seed=6)
+    t_at, n_at = timed(lambda: C.paged_attention_fp32(q, kc, vc, ks, vs, bt, cl, 9), seconds * 0.15)
+    b_att = attn_bytes(8, 4096 + 9, 9, 32, 8, 128, 4)
+    return dict(
+        value=round(b_layer / t_int / 1e9, 3), unit="GB/s", cores=int(cores), kind="port",
+        cpu=model,
+        sample=(f"torch._int_mm + fp32 epilogue (oracle/cpu_baseline.py) over one Llama-3-8B layer's seven "
+                f"linears at M={M}: median {t_int * 1e3:.1f} ms of {n_int} reps; bytes counted as for the GPU step"),
+        fp32_formula_layer_ms=round(t_f32 * 1e3, 2), fp32_formula_reps=n_f32,
+        w4a16_layer_ms=round(t_w4 * 1e3, 2), w4a16_reps=n_w4,
+        attention_B8_k8_ctx4096_ms=round(t_at * 1e3, 2), attention_GBps=round(b_att / t_at / 1e9, 3),
+        attention_reps=n_at)
 
 
-def read_traffic(kernel: str, M: int):
-    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary."""
+def read_traffic(key: str):
+    """HBM bytes per launch of the dominant kernel ("kernel@workload") from the committed
+    rocprofv3 --pmc summary (profiles/traffic.json, written by specq/profiling.py traffic)."""
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None
-    e = t.get(f"{kernel}@M={M}")
+    e = t.get(key)
     return None if e is None else e.get("bytes_per_launch")
 
 
@@ -544,15 +646,22 @@ def main() -> int:
     M = args.B * (args.k + 1)
     torch.cuda.synchronize()
     w = bench_w8a8(args, K, torch)
-    v, d, dom = w["verify"], w["decode"], w["dominant"]
-    vr = w["verify_rowmajor"]
+    v, d = w["verify"], w["decode"]
+    dom = w["launches"][DOMINANT]
+    rnd = lambda r: {k: (round(x, 4) if isinstance(x, float) else x) for k, x in r.items()}  # noqa: E731
     detail = {"w8a8_verify": dict(M=v["M"], ms=round(v["ms"], 4), GBps=round(v["GBps"], 1)),
-              "w8a8_verify_rowmajor_weights": dict(M=vr["M"], ms=round(vr["ms"], 4), GBps=round(vr["GBps"], 1)),
               "w8a8_decode": dict(M=d["M"], ms=round(d["ms"], 4), GBps=round(d["GBps"], 1)),
               "w8a8_verify_over_decode": round(v["ms"] / d["ms"], 4),
-              "w8a8_verify_7_linears": {k: round(x, 4) for k, x in w["verify_split"].items()},
-              "w8a8_decode_7_linears": {k: round(x, 4) for k, x in w["decode_split"].items()},
-              "w8a8_verify_over_decode_7_linears": round(w["verify_split"]["ms"] / w["decode_split"]["ms"], 4),
+              "w8a8_verify_7_launches": rnd(w["verify_7_launches"]),
+              "w8a8_decode_7_launches": rnd(w["decode_7_launches"]),
+              "w8a8_verify_rowmajor_weights": rnd(w["verify_rowmajor"]),
+              "w8a8_verify_fused_weights": rnd(w["verify_fused_weights"]),
+              "w8a8_decode_fused_weights": rnd(w["decode_fused_weights"]),
+              "w8a8_launch_us_M%d" % M: {k: dict(us=round(r["us"], 3), GBps=round(r["GBps"], 1),
+                                                 frac=round(r["GBps"] / HBM_PEAK_GBS, 4))
+                                         for k, r in w["launches"].items()},
+              "w8a8_launch_us_M%d" % args.B: {k: dict(us=round(r["us"], 3), GBps=round(r["GBps"], 1))
+                                              for k, r in w["launches_decode"].items()},
               "dominant_kernel": dict(name=dom["kernel"], us=round(dom["us"], 3), **dom["config"])}
     if not args.no_detail:
         w4 = bench_w4a16(args, K, torch)
@@ -590,14 +699,16 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic",
-        "config": {"workload": f"W8A8 verification linears of Llama-3-8B: {args.layers} layers x 4 "
-                               f"(qkv, o, gate_up, down as in bench_matmul.py), M=B*(k+1)={M} (B={args.B}, k={args.k}), "
-                               f"weights packed at load, one hipGraph replay per step",
+        "config": {"workload": f"BASELINE config 1: W8A8 over the seven Llama-3-8B linears (q, k, v, o, gate, up, "
+                               f"down) x {args.layers} layers at M=B*(k+1)={M} (B={args.B}, k={args.k}); q|k|v and "
+                               f"gate|up as grouped launches over separate weights (4 launches per layer); weights "
+                               f"packed at load; one hipGraph replay per step",
                    "M": M, "layers": args.layers, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(dom["GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic(dom["kernel"], M),
-                     "kernel": dom["kernel"], "algorithmic_bytes": dom["bytes"], "us_per_launch": round(dom["us"], 3)},
+                     "traffic": read_traffic(f'{dom["kernel"]}@W8A8 grouped gate|up 2x14336x4096 M={M}'),
+                     "kernel": dom["kernel"] + " (grouped gate|up launch)", "algorithmic_bytes": dom["bytes"],
+                     "us_per_launch": round(dom["us"], 3)},
         "cpu_baseline": cpu,
         "detail": detail,
     }

@@ -94,6 +94,27 @@ int specq_w8a8_packed(const int8_t* a, int64_t lda, const void* w_packed,
                       int block_m, int block_n, int num_warps, int split_k,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* Grouped W8A8: up to 4 GEMMs that share one activation (a, sa, M, K) -- q, k and v, or gate and
+ * up -- in one launch, each with its own weight, channel scale, output and N:
+ *   C_g[m, n] = fp16( (float(sum_k A[m,k] * W_g[n,k]) * sa[m]) * sw_g[n] ),  n < N[g]
+ * Results are bit-identical to one specq_w8a8 / specq_w8a8_packed / specq_w4a8_packed call per
+ * member.  The tiles are those of one GEMM of width sum(N), so the launch costs what the fused
+ * weight of bench_matmul.py:16 (qkv 6144, gate_up 28672) costs, while the weights and outputs
+ * stay separate tensors as in a model's layers.  No reference counterpart (the reference fuses
+ * the weights instead).
+ *   layout   0 row-major int8 weights (ldw[g] row strides), 1 packed int8 (specq_w8a8_pack_weight),
+ *            2 packed INT4 (specq_w4a8_pack_weight); ldw may be NULL unless layout is 0
+ *   w, sw, c, ldc, N  arrays of n_members entries (host memory)
+ *   Activations must have 16-byte aligned rows and K % 16 == 0.  Other arguments as specq_w8a8. */
+size_t specq_w8a8_grouped_workspace_size(int layout, int m_grid, int n_members, const int* N, int K,
+                                         int block_m, int block_n, int num_warps, int split_k);
+int specq_w8a8_grouped(int layout, const int8_t* a, int64_t lda, const float* sa, int n_members,
+                       const void* const* w, const int64_t* ldw, const float* const* sw,
+                       void* const* c, const int64_t* ldc, const int* N,
+                       int M, int K, int grid_m_max, const int32_t* plan,
+                       int block_m, int block_n, int num_warps, int split_k,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* W8A8 on packed weights without a workspace argument: the same computation and tiles as
  * specq_w8a8_packed (bit-identical results), with the split-K counters and INT32 partial tiles
  * held in a static device array of SPECQ_NOALLOC_SCRATCH_BYTES bytes that each GPU keeps for the

@@ -386,29 +386,75 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   return SPECQ_OK;
 }
 
+// The GEMMs of one launch: one, or up to kW8A8MaxGroup sharing the activation (a grouped launch).
+struct W8A8Group {
+  int n;
+  const void* w[kW8A8MaxGroup];
+  int64_t ldw[kW8A8MaxGroup];
+  const float* sw[kW8A8MaxGroup];
+  void* c[kW8A8MaxGroup];
+  int64_t ldc[kW8A8MaxGroup];
+  int N[kW8A8MaxGroup];
+  int n_total() const {
+    int t = 0;
+    for (int g = 0; g < n; ++g) t += N[g];
+    return t;
+  }
+};
+
+W8A8Group single(const void* w, int64_t ldw, const float* sw, void* c, int64_t ldc, int N) {
+  W8A8Group g;
+  g.n = 1; g.w[0] = w; g.ldw[0] = ldw; g.sw[0] = sw; g.c[0] = c; g.ldc[0] = ldc; g.N[0] = N;
+  return g;
+}
+
+// Tiles of a grouped launch: chosen as for one GEMM of the members' total width, then every
+// member gets whole channel blocks of its own (its last block may be partial).
+int w8a8_group_config(int layout, int m_grid, const W8A8Group& grp, int K, int block_m, int block_n, int num_warps,
+                      int split_k, int vec, bool plan_mode, W8A8Cfg* cfg) {
+  int rc = w8a8_config(layout, m_grid, grp.n_total(), K, block_m, block_n, num_warps, split_k, vec, plan_mode, cfg);
+  if (rc || grp.n == 1) return rc;
+  SPECQ_REQUIRE(cfg->family != kLegacy, SPECQ_ENOTSUP,
+                "w8a8 grouped: needs 16-byte aligned operands and K %% 16 == 0 (the streaming kernels)");
+  int tiles = 0;
+  for (int g = 0; g < grp.n; ++g) tiles += ceil_div(grp.N[g], cfg->bn);
+  cfg->n_tiles = tiles;
+  cfg->ws_partials =
+      cfg->splits > 1 ? align_up((size_t)cfg->m_chunks * tiles * cfg->splits * (cfg->mt * 16) * cfg->bn * 4, 256) : 0;
+  SPECQ_REQUIRE((int64_t)cfg->m_chunks * tiles <= kMaxCounters, SPECQ_ENOTSUP,
+                "w8a8: %d x %d tiles exceed the counter region", cfg->m_chunks, tiles);
+  return SPECQ_OK;
+}
+
 // With `static_scratch` the call runs on the device scratch array instead of a caller workspace:
 // it is refused when it needs more than that array holds, and the counters it uses are zeroed
 // (on the stream, before the GEMM) rather than assumed zero.
-int run_w8a8(int layout, const int8_t* a, int64_t lda, const void* w, int64_t ldw, const float* sa, const float* sw,
-             void* c, int64_t ldc, int M, int N, int K, int grid_m_max, const int32_t* plan, int block_m, int block_n,
-             int num_warps, int split_k, void* workspace, size_t workspace_bytes, void* stream,
-             bool static_scratch = false) {
-  SPECQ_REQUIRE(M >= 0 && N > 0 && K > 0, SPECQ_EINVAL, "w8a8: bad sizes M=%d N=%d K=%d", M, N, K);
-  SPECQ_REQUIRE(a && w && sa && sw && c, SPECQ_EINVAL, "w8a8: null tensor pointer");
-  SPECQ_REQUIRE(lda >= K && (layout != 0 || ldw >= K) && ldc >= N, SPECQ_EINVAL,
-                "w8a8: row strides must cover a row (lda=%lld ldw=%lld ldc=%lld)", (long long)lda, (long long)ldw,
-                (long long)ldc);
+int run_w8a8(int layout, const int8_t* a, int64_t lda, const W8A8Group& grp, const float* sa, int M, int K,
+             int grid_m_max, const int32_t* plan, int block_m, int block_n, int num_warps, int split_k,
+             void* workspace, size_t workspace_bytes, void* stream, bool static_scratch = false) {
+  SPECQ_REQUIRE(grp.n >= 1 && grp.n <= kW8A8MaxGroup, SPECQ_EINVAL, "w8a8: %d GEMMs in a group (1..%d)", grp.n,
+                kW8A8MaxGroup);
+  SPECQ_REQUIRE(M >= 0 && K > 0, SPECQ_EINVAL, "w8a8: bad sizes M=%d K=%d", M, K);
+  SPECQ_REQUIRE(a && sa && lda >= K, SPECQ_EINVAL, "w8a8: null activation pointer or lda=%lld < K", (long long)lda);
+  int vec = common_vec({(uint64_t)(uintptr_t)a, (uint64_t)lda, (uint64_t)K});
+  for (int g = 0; g < grp.n; ++g) {
+    const int N = grp.N[g];
+    SPECQ_REQUIRE(N > 0, SPECQ_EINVAL, "w8a8: bad sizes M=%d N=%d K=%d", M, N, K);
+    SPECQ_REQUIRE(grp.w[g] && grp.sw[g] && grp.c[g], SPECQ_EINVAL, "w8a8: null tensor pointer");
+    SPECQ_REQUIRE((layout != 0 || grp.ldw[g] >= K) && grp.ldc[g] >= N, SPECQ_EINVAL,
+                  "w8a8: row strides must cover a row (lda=%lld ldw=%lld ldc=%lld)", (long long)lda,
+                  (long long)grp.ldw[g], (long long)grp.ldc[g]);
+    if (layout == 0) vec = std::min(vec, common_vec({(uint64_t)(uintptr_t)grp.w[g], (uint64_t)grp.ldw[g]}));
+    SPECQ_REQUIRE(layout == 0 || (uintptr_t)grp.w[g] % 16 == 0, SPECQ_EINVAL, "w8a8: misaligned packed weight");
+  }
   SPECQ_REQUIRE(grid_m_max == 0 || grid_m_max >= M, SPECQ_EINVAL, "w8a8: grid_m_max=%d < M=%d", grid_m_max, M);
   const int m_grid = grid_m_max > 0 ? grid_m_max : M;
   if (m_grid == 0) return SPECQ_OK;
-  int vec = common_vec({(uint64_t)(uintptr_t)a, (uint64_t)lda, (uint64_t)K});
-  if (layout == 0) vec = std::min(vec, common_vec({(uint64_t)(uintptr_t)w, (uint64_t)ldw}));
   SPECQ_REQUIRE(layout == 0 || vec == 16, SPECQ_ENOTSUP,
                 "w8a8: packed weights need 16-byte aligned activations and K %% 16 == 0");
-  SPECQ_REQUIRE(layout == 0 || (uintptr_t)w % 16 == 0, SPECQ_EINVAL, "w8a8: misaligned packed weight");
   SPECQ_REQUIRE(layout != 2 || K <= 131072, SPECQ_ENOTSUP, "w4a8: K=%d exceeds 131072 (INT32 range of 16*sum)", K);
   W8A8Cfg cfg;
-  int rc = w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, vec, plan != nullptr, &cfg);
+  int rc = w8a8_group_config(layout, m_grid, grp, K, block_m, block_n, num_warps, split_k, vec, plan != nullptr, &cfg);
   if (rc) return rc;
   const size_t need = cfg.ws_partials + cfg.ws_counters;
   if (static_scratch) {
@@ -426,14 +472,29 @@ int run_w8a8(int layout, const int8_t* a, int64_t lda, const void* w, int64_t ld
                 "w8a8: workspace of %zu bytes required, %zu given", need, workspace ? workspace_bytes : 0);
   rc = ensure_lds(cfg.fn, cfg.lds);
   if (rc) return rc;
+  auto vec_store = [](const void* c, int64_t ldc, const float* sw) {
+    return (int)(((uintptr_t)c % 8 == 0) && (ldc % 4 == 0) && ((uintptr_t)sw % 16 == 0));
+  };
   W8A8Params p;
-  p.A = a; p.lda = lda; p.W = (const int8_t*)w; p.ldw = ldw; p.sa = sa; p.sw = sw;
-  p.C = reinterpret_cast<__half*>(c); p.ldc = ldc; p.plan = plan;
-  p.M = M; p.N = N; p.K = K; p.m_grid = m_grid;
+  memset(&p, 0, sizeof(p));
+  p.A = a; p.lda = lda; p.W = (const int8_t*)grp.w[0]; p.ldw = grp.ldw[0]; p.sa = sa; p.sw = grp.sw[0];
+  p.C = reinterpret_cast<__half*>(grp.c[0]); p.ldc = grp.ldc[0]; p.plan = plan;
+  p.M = M; p.N = grp.N[0]; p.K = K; p.m_grid = m_grid;
   p.n_tiles = cfg.n_tiles; p.m_chunks = cfg.m_chunks; p.splits = cfg.splits; p.k_range = cfg.k_range;
   p.counters = need ? reinterpret_cast<int32_t*>(workspace) : nullptr;
   p.partials = need ? reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + kCounterBytes) : nullptr;
-  p.vec_store = ((uintptr_t)c % 8 == 0) && (ldc % 4 == 0) && ((uintptr_t)sw % 16 == 0);
+  p.vec_store = vec_store(grp.c[0], grp.ldc[0], grp.sw[0]);
+  p.n_grp = grp.n;
+  int tile_end = 0;
+  for (int g = 0; g < grp.n; ++g) {
+    tile_end += ceil_div(grp.N[g], cfg.bn);
+    if (g + 1 < grp.n) p.grp_tile_end[g] = tile_end;
+    if (g > 0) {
+      p.grp_W[g - 1] = (const int8_t*)grp.w[g]; p.grp_ldw[g - 1] = grp.ldw[g]; p.grp_sw[g - 1] = grp.sw[g];
+      p.grp_C[g - 1] = reinterpret_cast<__half*>(grp.c[g]); p.grp_ldc[g - 1] = grp.ldc[g]; p.grp_N[g - 1] = grp.N[g];
+      p.grp_vec_store[g - 1] = vec_store(grp.c[g], grp.ldc[g], grp.sw[g]);
+    }
+  }
   const int grid = chunked_grid(cfg.n_tiles * cfg.splits, cfg.m_chunks);
   if (static_scratch && need) {
     int n_ctr = cfg.m_chunks * cfg.n_tiles;
@@ -449,14 +510,24 @@ int run_w8a8(int layout, const int8_t* a, int64_t lda, const void* w, int64_t ld
   return launch(cfg.fn, grid, cfg.nw * 64, cfg.lds, reinterpret_cast<hipStream_t>(stream), &p);
 }
 
-size_t workspace_size(int layout, int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k) {
+int run_w8a8(int layout, const int8_t* a, int64_t lda, const void* w, int64_t ldw, const float* sa, const float* sw,
+             void* c, int64_t ldc, int M, int N, int K, int grid_m_max, const int32_t* plan, int block_m, int block_n,
+             int num_warps, int split_k, void* workspace, size_t workspace_bytes, void* stream,
+             bool static_scratch = false) {
+  return run_w8a8(layout, a, lda, single(w, ldw, sw, c, ldc, N), sa, M, K, grid_m_max, plan, block_m, block_n,
+                  num_warps, split_k, workspace, workspace_bytes, stream, static_scratch);
+}
+
+size_t workspace_size(int layout, int m_grid, const W8A8Group& grp, int K, int block_m, int block_n, int num_warps,
+                      int split_k) {
   W8A8Cfg cfg;
   size_t best = 0;
   // Size for every alignment class and mode (eager or plan) the call could resolve to.
   for (int vec : {16, 1}) {
-    if (layout != 0 && vec != 16) continue;
+    if ((layout != 0 || grp.n > 1) && vec != 16) continue;
     for (bool plan_mode : {false, true}) {
-      if (w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, vec, plan_mode, &cfg) == SPECQ_OK) {
+      if (w8a8_group_config(layout, m_grid, grp, K, block_m, block_n, num_warps, split_k, vec, plan_mode, &cfg) ==
+          SPECQ_OK) {
         const size_t s = cfg.ws_partials + cfg.ws_counters;
         if (s > best) best = s;
       }
@@ -464,6 +535,11 @@ size_t workspace_size(int layout, int m_grid, int N, int K, int block_m, int blo
   }
   clear_error();
   return best;
+}
+
+size_t workspace_size(int layout, int m_grid, int N, int K, int block_m, int block_n, int num_warps, int split_k) {
+  return workspace_size(layout, m_grid, single(nullptr, 0, nullptr, nullptr, 0, N), K, block_m, block_n, num_warps,
+                        split_k);
 }
 
 }  // namespace
@@ -560,6 +636,52 @@ extern "C" int specq_w8a8_packed_noalloc(const int8_t* a, int64_t lda, const voi
   clear_error();
   return run_w8a8(1, a, lda, w_packed, 0, sa, sw, c, ldc, M, N, K, grid_m_max, plan, block_m, block_n, num_warps,
                   split_k, nullptr, 0, stream, /*static_scratch=*/true);
+}
+
+namespace {
+int make_group(int n_members, const void* const* w, const int64_t* ldw, const float* const* sw, void* const* c,
+               const int64_t* ldc, const int* N, W8A8Group* grp) {
+  SPECQ_REQUIRE(n_members >= 1 && n_members <= kW8A8MaxGroup, SPECQ_EINVAL,
+                "w8a8_grouped: %d GEMMs (1..%d supported)", n_members, kW8A8MaxGroup);
+  SPECQ_REQUIRE(N != nullptr, SPECQ_EINVAL, "w8a8_grouped: null N array");
+  grp->n = n_members;
+  for (int g = 0; g < n_members; ++g) {
+    grp->w[g] = w ? w[g] : nullptr;
+    grp->ldw[g] = ldw ? ldw[g] : 0;
+    grp->sw[g] = sw ? sw[g] : nullptr;
+    grp->c[g] = c ? c[g] : nullptr;
+    grp->ldc[g] = ldc ? ldc[g] : 0;
+    grp->N[g] = N[g];
+  }
+  return SPECQ_OK;
+}
+}  // namespace
+
+extern "C" size_t specq_w8a8_grouped_workspace_size(int layout, int m_grid, int n_members, const int* N, int K,
+                                                    int block_m, int block_n, int num_warps, int split_k) {
+  W8A8Group grp;
+  if (layout < 0 || layout > 2 || make_group(n_members, nullptr, nullptr, nullptr, nullptr, nullptr, N, &grp)) {
+    clear_error();
+    return 0;
+  }
+  for (int g = 0; g < n_members; ++g)
+    if (N[g] <= 0) return 0;
+  return workspace_size(layout, m_grid, grp, K, block_m, block_n, num_warps, split_k);
+}
+
+extern "C" int specq_w8a8_grouped(int layout, const int8_t* a, int64_t lda, const float* sa, int n_members,
+                                  const void* const* w, const int64_t* ldw, const float* const* sw, void* const* c,
+                                  const int64_t* ldc, const int* N, int M, int K, int grid_m_max, const int32_t* plan,
+                                  int block_m, int block_n, int num_warps, int split_k, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  clear_error();
+  SPECQ_REQUIRE(layout >= 0 && layout <= 2, SPECQ_EINVAL, "w8a8_grouped: weight layout %d (0, 1 or 2)", layout);
+  SPECQ_REQUIRE(w && sw && c && ldc && N && (layout != 0 || ldw), SPECQ_EINVAL, "w8a8_grouped: null member array");
+  W8A8Group grp;
+  int rc = make_group(n_members, w, ldw, sw, c, ldc, N, &grp);
+  if (rc) return rc;
+  return run_w8a8(layout, a, lda, grp, sa, M, K, grid_m_max, plan, block_m, block_n, num_warps, split_k, workspace,
+                  workspace_bytes, stream);
 }
 
 extern "C" int specq_set_option(const char* name, int value) {

@@ -40,7 +40,40 @@ struct W8A8Params {
   int32_t* partials;   // [m_chunks][n_tiles][splits][BM*BN] when splits > 1
   int32_t* counters;   // [m_chunks][n_tiles], zero between calls
   int vec_store;       // 1 when C rows allow 8-byte aligned stores of 4 halves
+  // Grouped launch: n_grp GEMMs that share A, sa, M and K (q, k and v; gate and up), each with
+  // its own weight, channel scales, output and N.  Member 0 is W / ldw / sw / C / ldc / N above;
+  // members 1.. are the grp_* entries.  n_tiles counts the tiles of every member, and tile t
+  // belongs to member g when grp_tile_end[g-1] <= t < grp_tile_end[g].
+  int n_grp;
+  int grp_tile_end[3];
+  const int8_t* grp_W[3];
+  int64_t grp_ldw[3];
+  const float* grp_sw[3];
+  __half* grp_C[3];
+  int64_t grp_ldc[3];
+  int grp_N[3];
+  int grp_vec_store[3];
 };
+constexpr int kW8A8MaxGroup = 4;
+
+// Points W, ldw, sw, C, ldc and N at the GEMM of a grouped launch that owns launch-wide tile
+// `tile`, and returns the tile's index within that GEMM.  The member is picked with scalar
+// selects (the parameter block is never indexed dynamically).  Counters and split-K partials
+// stay indexed by the launch-wide tile.
+__device__ __forceinline__ int w8a8_select_member(W8A8Params& p, int tile) {
+  if (p.n_grp <= 1) return tile;
+  int first = 0;
+#pragma unroll
+  for (int g = 1; g < kW8A8MaxGroup; ++g) {
+    if (g < p.n_grp && tile >= p.grp_tile_end[g - 1]) {  // g is a constant once unrolled
+      first = p.grp_tile_end[g - 1];
+      p.W = p.grp_W[g - 1]; p.ldw = p.grp_ldw[g - 1]; p.sw = p.grp_sw[g - 1];
+      p.C = p.grp_C[g - 1]; p.ldc = p.grp_ldc[g - 1]; p.N = p.grp_N[g - 1];
+      p.vec_store = p.grp_vec_store[g - 1];
+    }
+  }
+  return tile - first;
+}
 
 constexpr int kW8A8Pad = 4;  // int32 padding per LDS row
 

@@ -58,7 +58,8 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
   int mc, unit;
   if (!chunked_unit(p.m_chunks, p.n_tiles * p.splits, mc, unit)) return;
   const int split = unit % p.splits;
-  const int tile = unit / p.splits;
+  const int tile = unit / p.splits;          // launch-wide tile (counters, partials)
+  const int ltile = w8a8_select_member(p, tile);  // tile within its GEMM (weights, outputs)
 
   int M = p.M;
   if (p.plan != nullptr) M = min(max(p.plan[0], 0), p.m_grid);
@@ -68,7 +69,7 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
 
   const int lane = lane_id(), w = uniform(wave_id()), g = lane >> 4, r = lane & 15;
   const int cw = w % CW, kw = w / CW;
-  const int n0 = tile * BN + cw * BNW;  // first channel of this wave
+  const int n0 = ltile * BN + cw * BNW;  // first channel of this wave
   const int kb = split * p.k_range;
   const int ke = min(p.K, kb + p.k_range);
   const int nsteps = (ke - kb + 63) / 64;
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
         w8a8_publish_quad<BM, BN>(prs, split, j * 16 + r, cw * BNW + a * 16 + 4 * g, acc[a][j]);
   }
   __shared__ int s_last_rk;
-  w8a8_splitk_finish<BM, BN, NW * 64>(p, prs, cidx, m0, tile * BN, M, &s_last_rk);
+  w8a8_splitk_finish<BM, BN, NW * 64>(p, prs, cidx, m0, ltile * BN, M, &s_last_rk);
 }
 
 }  // namespace specq

@@ -48,6 +48,7 @@ Differences a caller may notice:
 """
 from __future__ import annotations
 
+import ctypes
 import math
 import os
 import sys
@@ -69,6 +70,7 @@ __all__ = [
     "silu_mul", "quantize_act_int8_gpu", "silu_mul_quant_int8", "paged_kv_append",
     "pack_int4_i32", "KernelInfo", "PackedWeightInt8", "pack_weight_int8", "PackedWeightInt4", "pack_weight_int4",
     "w4a8_matmul", "quantize_weight_int4_channel", "PackedWeightW4A8", "pack_weight_w4a8",
+    "w8a8_matmul_grouped",
 ]
 
 
@@ -282,6 +284,83 @@ def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK_K=12
                   wptr, wbytes, _stream_ptr(a_q))
     _w8a8_kernel._note(a_q.device.index or 0, (bm, bn, nw))
     return out, KernelInfo(0, (1 if packed else 0) | (16 if plan is not None else 0), m_grid, N, K, bm, bn, nw, split_k)
+
+
+def w8a8_matmul_grouped(a_q, sa, weights, outs=None, BLOCK_M=16, BLOCK_N=None, num_warps=4, plan=None,
+                        grid_m_max=None, split_k=0, workspace=None, plan_tiles=None):
+    """Up to four W8A8 GEMMs that share one activation (q, k and v; gate and up) in one launch.
+
+    outs[g] = fp16((int32(a_q @ W_g.T) * sa[:, None]) * sw_g[None, :]) for weights[g] = (W_g, sw_g),
+    bit-identical to one w8a8_matmul (or w4a8_matmul) call per GEMM.  The W_g are all int8 [N_g, K]
+    tensors, all PackedWeightInt8 or all PackedWeightW4A8.  The launch uses the tiles of one GEMM
+    of width sum(N_g), as the reference's fused qkv / gate_up weights do (bench_matmul.py:16),
+    while the weights and outputs stay separate.  Other arguments as w8a8_matmul.  Returns
+    (outs, ck).
+    """
+    n = len(weights)
+    if not 1 <= n <= 4:
+        raise RuntimeError(f"w8a8_matmul_grouped: {n} GEMMs (1..4 supported)")
+    ws_ = [w for w, _ in weights]
+    if all(isinstance(w, PackedWeightInt8) for w in ws_):
+        layout = 1
+    elif all(isinstance(w, PackedWeightW4A8) for w in ws_):
+        layout = 2
+    elif all(isinstance(w, torch.Tensor) and w.dtype == torch.int8 for w in ws_):
+        layout = 0
+    else:
+        raise RuntimeError("w8a8_matmul_grouped: weights must all be int8 tensors, all PackedWeightInt8 "
+                           "or all PackedWeightW4A8")
+    _require_gpu(a_q, sa, *(sw for _, sw in weights))
+    if layout == 0:
+        _require_gpu(*ws_)
+        ws_ = [_rowmajor(w) for w in ws_]
+    if a_q.dtype != torch.int8:
+        raise RuntimeError("w8a8_matmul_grouped expects int8 activations")
+    M, K = a_q.shape
+    Ns = [int(w.shape[0]) if layout == 0 else int(w.N) for w in ws_]
+    for w in ws_:
+        if (w.shape[1] if layout == 0 else w.K) != K:
+            raise RuntimeError(f"w8a8_matmul_grouped: K mismatch {tuple(a_q.shape)} vs {tuple(w.shape)}")
+    a_q = _rowmajor(a_q)
+    sa = sa.float().contiguous()
+    sws = [sw.float().contiguous() for _, sw in weights]
+    for sw, N in zip(sws, Ns):
+        if sw.numel() != N:
+            raise RuntimeError(f"w8a8_matmul_grouped: channel scale of {sw.numel()} entries for N={N}")
+    if outs is None:
+        outs = [torch.empty((M, N), device=a_q.device, dtype=torch.float16) for N in Ns]
+    if len(outs) != n:
+        raise RuntimeError("w8a8_matmul_grouped: one output per GEMM")
+    for o, N in zip(outs, Ns):
+        if o.dtype != torch.float16 or o.stride(-1) != 1 or tuple(o.shape) != (M, N):
+            raise RuntimeError(f"w8a8_matmul_grouped: outputs must be fp16 [M, N] with unit inner stride, got "
+                               f"{tuple(o.shape)} for N={N}")
+    m_grid = int(grid_m_max) if grid_m_max is not None else M
+    N_total = sum(Ns)
+    bm = BLOCK_M if BLOCK_M else pick_block_m("w8a8", m_grid, N_total, K)
+    bn = _w8a8_block_n(BLOCK_N)
+    nw = int(num_warps) if num_warps else 4
+    if plan is not None and plan_tiles is not None:
+        if plan_tiles != "grid":
+            raise RuntimeError(f"w8a8_matmul_grouped: plan_tiles={plan_tiles!r} (None or 'grid')")
+        if not bm:
+            cfg = KernelInfo(0, layout, m_grid, N_total, K, 0, bn, nw, split_k).config
+            bm, bn, split_k = cfg["block_m"], cfg["block_n"], cfg["split_k"]
+    arr = lambda ct, vals: (ct * n)(*vals)  # noqa: E731
+    n_arr = arr(ctypes.c_int, Ns)
+    w_arr = arr(ctypes.c_void_p, [w.data_ptr() if layout == 0 else w.data.data_ptr() for w in ws_])
+    ldw_arr = arr(ctypes.c_int64, [w.stride(0) if layout == 0 else 0 for w in ws_])
+    sw_arr = arr(ctypes.c_void_p, [sw.data_ptr() for sw in sws])
+    c_arr = arr(ctypes.c_void_p, [o.data_ptr() for o in outs])
+    ldc_arr = arr(ctypes.c_int64, [o.stride(0) for o in outs])
+    ws = workspace or _ws.shared(a_q.device)
+    need = _lib.lib().specq_w8a8_grouped_workspace_size(layout, m_grid, n, n_arr, K, bm, bn, nw, split_k)
+    wptr, wbytes = ws.ensure(need)
+    _lib.call("specq_w8a8_grouped", layout, a_q.data_ptr(), a_q.stride(0), sa.data_ptr(), n, w_arr, ldw_arr, sw_arr,
+              c_arr, ldc_arr, n_arr, M, K, int(grid_m_max or 0), _plan_ptr(plan), bm, bn, nw, split_k,
+              wptr, wbytes, _stream_ptr(a_q))
+    _w8a8_kernel._note(a_q.device.index or 0, (bm, bn, nw, "grouped", layout))
+    return outs, KernelInfo(0, layout | (16 if plan is not None else 0), m_grid, N_total, K, bm, bn, nw, split_k)
 
 
 def quantize_act_int8(x):

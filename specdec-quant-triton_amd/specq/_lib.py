@@ -44,6 +44,11 @@ SIGNATURES = {
     "specq_w8a8_packed": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
                                    _c_int, _c_int, _c_int, _c_int, _c_vp,
                                    _c_int, _c_int, _c_int, _c_int, _c_vp, _c_size, _c_vp]),
+    "specq_w8a8_grouped_workspace_size": (_c_size, [_c_int, _c_int, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int,
+                                                    _c_int]),
+    "specq_w8a8_grouped": (_c_int, [_c_int, _c_vp, _c_i64, _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                    _c_int, _c_int, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_size,
+                                    _c_vp]),
     "specq_w8a8_packed_noalloc": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
                                            _c_int, _c_int, _c_int, _c_int, _c_vp,
                                            _c_int, _c_int, _c_int, _c_int, _c_vp]),

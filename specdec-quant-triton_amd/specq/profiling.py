@@ -6,6 +6,8 @@ Subcommands (run from the repository root):
             enough distinct weights / KV caches that every launch reads HBM (more than the
             256 MiB Infinity Cache between two uses of one buffer):
               w8a8:M    the fused gate_up W8A8 GEMM (N=28672, K=4096, packed weights)
+              w8a8g:M   gate and up (14336 x 4096 each) as one grouped launch over separate
+                        packed weights (the headline's dominant launch)
               w4a16:M   the same shape in W4A16 (load-time packed INT4, group 128)
               attn:B:k:ctx  INT8 paged verification attention (32/8 heads, D=128, fp32
                         scales, fused QPP=k+1)
@@ -105,6 +107,29 @@ def probe(args) -> int:
             _, ck = K.w8a8_matmul(a, sa, *layers[0], out=out, BLOCK_M=None)
             bytes_, ops = N * Kd + M * Kd + 4 * M + 4 * N + 2 * M * N, 2 * M * N * Kd
             wl = f"W8A8 N={N} K={Kd} M={M}"
+        elif f[0] == "w8a8g":
+            # The headline's dominant launch: gate and up (14336 x 4096 each, separate packed
+            # weights) as one grouped launch.
+            M, Ng = int(f[1]), 14336
+            layers = []
+            for _ in range(args.layers):
+                pair = []
+                for _ in range(2):
+                    w = torch.randint(-127, 128, (Ng, Kd), dtype=torch.int8, device="cuda", generator=g)
+                    pair.append((K.pack_weight_int8(w), torch.rand((Ng,), device="cuda", generator=g) * 0.009 + 0.001))
+                    del w
+                layers.append(pair)
+            a = torch.randint(-127, 128, (M, Kd), dtype=torch.int8, device="cuda", generator=g)
+            sa = torch.rand((M,), device="cuda", generator=g) * 0.015 + 0.005
+            outs = [torch.empty((M, Ng), dtype=torch.float16, device="cuda") for _ in range(2)]
+
+            def run(layers=layers, a=a, sa=sa, outs=outs):
+                for pair in layers:
+                    K.w8a8_matmul_grouped(a, sa, pair, outs=outs, BLOCK_M=None)
+            _, ck = K.w8a8_matmul_grouped(a, sa, layers[0], outs=outs, BLOCK_M=None)
+            bytes_ = 2 * (Ng * Kd + 4 * Ng + 2 * M * Ng) + M * Kd + 4 * M
+            ops = 2 * 2 * M * Ng * Kd
+            wl = f"W8A8 grouped gate|up 2x{Ng}x{Kd} M={M}"
         elif f[0] == "w4a16":
             M = int(f[1])
             layers = []

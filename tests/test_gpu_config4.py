@@ -1,7 +1,7 @@
 """Config 4 at its real size: the 4-layer INT8 stack with d_model 4096 (qkv N=6144, o 4096x4096,
-gate and up 14336x4096 each, SiLU*mul fused with the INT8 quantisation, down 4096x14336) and
-paged attention at context 1024 (H=32, H_KV=8, D=128, fp32 scales), B <= 32, k in {0, 2, 4, 8},
-M_MAX = 288 -- the stack bench.py times.
+gate and up 14336x4096 each as one grouped launch, SiLU*mul fused with the INT8 quantisation,
+down 4096x14336) and paged attention at context 1024 (H=32, H_KV=8, D=128, fp32 scales),
+B <= 32, k in {0, 2, 4, 8}, M_MAX = 288 -- the stack bench.py times.
 
 One plan-buffer graph captured at B=32, k=8 and the bucketed PlanGraphSet each replay a
 seeded trace holding every distinct (B, k) once (random.Random(0) order) plus (32, 8) and
@@ -61,8 +61,8 @@ class Stack:
             K.paged_attention(self.q[:Bg, :qg], kc, vc, ks, vs, bt[:Bg], cl[:Bg], qg, QPP=qg,
                               plan=plan.attn if plan is not None else None, out=self.o[:Bg, :qg])
             K.w8a8_matmul(a, sa, *lw["o"], out=b["o"][:Mg], BLOCK_M=None, **gk)
-            K.w8a8_matmul(a, sa, *lw["gate"], out=b["gate"][:Mg], BLOCK_M=None, **gk)
-            K.w8a8_matmul(a, sa, *lw["up"], out=b["up"][:Mg], BLOCK_M=None, **gk)
+            K.w8a8_matmul_grouped(a, sa, [lw["gate"], lw["up"]], outs=[b["gate"][:Mg], b["up"][:Mg]], BLOCK_M=None,
+                                  **gk)
             K.silu_mul_quant_int8(b["gate"][:Mg], b["up"][:Mg], q=self.hq[:Mg], s=self.hs[:Mg], **kw)
             K.w8a8_matmul(self.hq[:Mg], self.hs[:Mg], *lw["down"], out=b["down"][:Mg], BLOCK_M=None, **gk)
 
