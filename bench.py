@@ -386,18 +386,22 @@ def bench_attention(args, K, torch):
 
 def bench_plan_graph(args, K, torch):
     """Config 4: a 4-layer INT8 stack (d_model 4096, weights packed at load; gate and up as one
-    grouped launch over their separate weights) replayed over a
-    seeded (B, k) trace, B in 1..32, k in {0, 2, 4, 8}, under five launch strategies:
-      eager     every step launched with its exact shapes
+    grouped launch over their separate weights) replayed over a seeded 1000-step (B, k) trace,
+    B in 1..32, k in {0, 2, 4, 8}, under the strategies of bench_graphs.py:109-114 and two more:
+      eager     every step launched with its exact shapes (a fifth of the trace)
       allshapes one graph per distinct (B, k) of the trace (captured before timing)
-      maxpad    one graph at B=32, k=8 (M=288) without a plan: every step computes M=288
+      maxpad    one graph per B with k padded to 8, no plan: every step computes B * 9 rows
+      maxgrid   one graph at B=32, k=8 (M=288), no plan: every step computes 288 rows
       plan      one plan-buffer graph captured at B=32, k=8, the active (B, k) read on device
       bucketed  plan-buffer graphs per (B bucket 1/2/3/4/6/8/12/16/24/32, k): the GEMMs of each
                 bucket run the tiles an eager call of its row count would pick (PlanGraphSet,
                 plan_tiles="grid")
-    Host perf_counter around plan write + replay + sync per step (bench_graphs.py:126-136).
-    Padding waste is the token rows the GEMMs compute beyond M, per step (the tile the library
-    resolved for that strategy's grid, chunks past the active M skipped in plan mode)."""
+    Host perf_counter around plan write + replay + sync per step (bench_graphs.py:126-136); fixed-k
+    traces (bench_graphs.py:141-142) give the mean step per k.  Padding waste is reported in
+    M-tiles (REPORT.md:147): per step, the BLOCK_M-row tiles a strategy's GEMMs compute beyond the
+    ceil(M / BLOCK_M) the active rows need, for BLOCK_M in {16, 32, 64, 128}; plan-mode tiles past
+    the active M exit at once and are not counted.  The library's own tiles are reported as rows
+    computed beyond M."""
     import random
 
     from specq import gen
@@ -456,11 +460,16 @@ def bench_plan_graph(args, K, torch):
     shapes = sorted(set(trace))
     for B, k in shapes:  # warm every exact shape (also sizes the shared workspace)
         step(B, k + 1)
+    for B in range(1, B_MAX + 1):
+        step(B, QL_MAX)
     torch.cuda.synchronize()
 
-    def timed(run):
+    def timed(run, tr):
+        for B, k in tr[:20]:
+            run(B, k + 1)
+        torch.cuda.synchronize()
         lat = []
-        for B, k in trace:
+        for B, k in tr:
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             run(B, k + 1)
@@ -468,53 +477,72 @@ def bench_plan_graph(args, K, torch):
             lat.append((time.perf_counter() - t0) * 1e3)
         return lat
 
-    res = {}
-    # eager (a fifth of the trace: launch-bound on the host)
-    lat = []
-    for B, k in trace[: max(20, args.trace // 5)]:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        step(B, k + 1)
-        torch.cuda.synchronize()
-        lat.append((time.perf_counter() - t0) * 1e3)
-    res["eager"] = lat
-    # allshapes
+    t_build = {}
+    t0 = time.perf_counter()
     per_shape = {bk: capture(lambda bk=bk: step(bk[0], bk[1] + 1)) for bk in shapes}
-    res["allshapes"] = timed(lambda B, ql: per_shape[(B, ql - 1)].replay())
-    del per_shape
-    # maxpad
+    t_build["allshapes"] = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    per_b = {B: capture(lambda B=B: step(B, QL_MAX)) for B in range(1, B_MAX + 1)}
+    t_build["maxpad"] = time.perf_counter() - t0
     gmax = capture(lambda: step(B_MAX, QL_MAX))
-    res["maxpad"] = timed(lambda B, ql: gmax.replay())
-    del gmax
-    # one plan graph at the maximum grid
     plan1 = Plan("cuda")
     plan1.set(B_MAX, QL_MAX)
+    t0 = time.perf_counter()
     gplan = capture(lambda: step(B_MAX, QL_MAX, plan1))
+    t_build["plan"] = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    gset = PlanGraphSet(step, B_MAX, [k + 1 for k in KS])
+    t_build["bucketed"] = time.perf_counter() - t0
 
     def run_plan(B, ql):
         plan1.set(B, ql)
         gplan.replay()
-    res["plan"] = timed(run_plan)
-    # bucketed plan graphs
-    t0 = time.perf_counter()
-    gset = PlanGraphSet(step, B_MAX, [k + 1 for k in KS])
-    build_s = time.perf_counter() - t0
-    res["bucketed"] = timed(gset.replay)
+    runs = {"allshapes": lambda B, ql: per_shape[(B, ql - 1)].replay(),
+            "maxpad": lambda B, ql: per_b[B].replay(),
+            "maxgrid": lambda B, ql: gmax.replay(),
+            "plan": run_plan,
+            "bucketed": gset.replay}
+    res = {"eager": timed(lambda B, ql: step(B, ql), trace[: max(40, args.trace // 5)])}
+    for name, fn in runs.items():
+        res[name] = timed(fn, trace)
 
     tokens = sum(B * (k + 1) for B, k in trace)
-    out = dict(steps=len(trace), bucketed_graphs=len(gset.graphs), bucketed_build_s=build_s,
-               allshapes_graphs=len(shapes))
+    out = dict(steps=len(trace), allshapes_graphs=len(shapes), maxpad_graphs=len(per_b),
+               bucketed_graphs=len(gset.graphs))
+    for name, tb in t_build.items():
+        out[f"{name}_build_s"] = tb
     for name, lat in res.items():
         out[f"{name}_p50_ms"] = statistics.median(lat)
         out[f"{name}_p99_ms"] = sorted(lat)[int(0.99 * (len(lat) - 1))]
         if name != "eager":
             out[f"{name}_tokens_per_s"] = tokens / (sum(lat) * 1e-3)
-    # padding waste in token rows per step (qkv GEMM; every GEMM of a step shares its grid)
-    waste = dict(eager=0.0, maxpad=0.0, plan=0.0, bucketed=0.0)
+    for name in ("plan", "bucketed", "maxpad"):
+        out[f"{name}_p50_over_allshapes"] = out[f"{name}_p50_ms"] / out["allshapes_p50_ms"]
+        out[f"{name}_p99_over_allshapes"] = out[f"{name}_p99_ms"] / out["allshapes_p99_ms"]
+    # fixed-k traces (bench_graphs.py:141-142): mean ms per step
+    for k in KS:
+        rk = random.Random(10 + k)
+        tr = [(rk.randint(1, B_MAX), k) for _ in range(max(50, args.trace // 10))]
+        for name in ("allshapes", "maxpad", "plan", "bucketed"):
+            fn = runs[name]
+            if name == "allshapes":
+                tr_ok = [(B, kk) for B, kk in tr if (B, kk) in per_shape]
+                lat = timed(fn, tr_ok) if tr_ok else [float("nan")]
+            else:
+                lat = timed(fn, tr)
+            out[f"fixed_k{k}_{name}_mean_ms"] = statistics.fmean(lat)
+    # padding waste in M-tiles per step at each BLOCK_M (REPORT.md:147), and the library's rows
+    for bm in (16, 32, 64, 128):
+        need = [-(-(B * (k + 1)) // bm) for B, k in trace]
+        out[f"pad_tiles_bm{bm}_maxpad"] = statistics.fmean(-(-(B * QL_MAX) // bm) - n for (B, k), n in zip(trace, need))
+        out[f"pad_tiles_bm{bm}_maxgrid"] = statistics.fmean(-(-M_MAX // bm) - n for n in need)
+        out[f"pad_tiles_bm{bm}_eager_allshapes_plan"] = 0.0
+    waste = dict(eager=0.0, maxpad=0.0, maxgrid=0.0, plan=0.0, bucketed=0.0)
     for B, k in trace:
         M = B * (k + 1)
         waste["eager"] += rows_computed(M, M, False) - M
-        waste["maxpad"] += rows_computed(M_MAX, M, False) - M
+        waste["maxpad"] += rows_computed(B * QL_MAX, M, False) - M
+        waste["maxgrid"] += rows_computed(M_MAX, M, False) - M
         waste["plan"] += rows_computed(M_MAX, M, True) - M
         waste["bucketed"] += rows_computed(gset.bucket(B) * (k + 1), M, True, grid_tiles=True) - M
     torch.cuda.synchronize()
@@ -523,7 +551,8 @@ def bench_plan_graph(args, K, torch):
     out["allshapes_pad_rows_per_step"] = out["eager_pad_rows_per_step"]
     log(f"plan graphs: P50 plan {out['plan_p50_ms']:.3f} / bucketed {out['bucketed_p50_ms']:.3f} / "
         f"allshapes {out['allshapes_p50_ms']:.3f} / maxpad {out['maxpad_p50_ms']:.3f} / "
-        f"eager {out['eager_p50_ms']:.3f} ms")
+        f"maxgrid {out['maxgrid_p50_ms']:.3f} / eager {out['eager_p50_ms']:.3f} ms")
+    del per_shape, per_b, gmax, gplan, gset
     return out
 
 
@@ -624,7 +653,7 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--B", type=int, default=8)
     ap.add_argument("--k", type=int, default=8)
-    ap.add_argument("--trace", type=int, default=200, help="steps of the plan-graph (B, k) trace")
+    ap.add_argument("--trace", type=int, default=1000, help="steps of the plan-graph (B, k) trace")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-detail", action="store_true")

@@ -61,7 +61,6 @@ if _HERE not in sys.path:
 
 from specq import _lib  # noqa: E402
 from specq import workspace as _ws  # noqa: E402
-from specq.tiles import pick_block_m  # noqa: E402
 
 __all__ = [
     "w8a8_matmul", "w4a16_matmul", "paged_attention",
@@ -258,7 +257,7 @@ def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK_K=12
     if out.dtype != torch.float16 or out.stride(-1) != 1:
         raise RuntimeError("w8a8_matmul: out must be fp16 with unit inner stride")
     m_grid = int(grid_m_max) if grid_m_max is not None else M
-    bm = BLOCK_M if BLOCK_M else pick_block_m("w8a8", m_grid, N, K)
+    bm = int(BLOCK_M) if BLOCK_M else 0  # 0: the library picks the tile (cost model over M, N, K)
     bn = _w8a8_block_n(BLOCK_N)
     nw = int(num_warps) if num_warps else 4
     if plan is not None and plan_tiles is not None:
@@ -337,7 +336,7 @@ def w8a8_matmul_grouped(a_q, sa, weights, outs=None, BLOCK_M=16, BLOCK_N=None, n
                                f"{tuple(o.shape)} for N={N}")
     m_grid = int(grid_m_max) if grid_m_max is not None else M
     N_total = sum(Ns)
-    bm = BLOCK_M if BLOCK_M else pick_block_m("w8a8", m_grid, N_total, K)
+    bm = int(BLOCK_M) if BLOCK_M else 0
     bn = _w8a8_block_n(BLOCK_N)
     nw = int(num_warps) if num_warps else 4
     if plan is not None and plan_tiles is not None:
@@ -485,7 +484,7 @@ def w4a16_matmul(a, wp, sc, group=128, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK
     if out.dtype != torch.float16 or out.stride(-1) != 1:
         raise RuntimeError("w4a16_matmul: out must be fp16 with unit inner stride")
     m_grid = int(grid_m_max) if grid_m_max is not None else M
-    bm = BLOCK_M if BLOCK_M else pick_block_m("w4a16", m_grid, N, K)
+    bm = int(BLOCK_M) if BLOCK_M else 0
     bn = 0 if not BLOCK_N else (64 if BLOCK_N <= 64 else 128)
     ws = workspace or _ws.shared(a.device)
     need = _lib.lib().specq_w4a16_workspace_size(m_grid, N, K, bm, bn, 4, split_k)
@@ -783,7 +782,7 @@ def w4a8_matmul(a_q, sa, wq, sw, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK_K=128
     if out.dtype != torch.float16 or out.stride(-1) != 1:
         raise RuntimeError("w4a8_matmul: out must be fp16 with unit inner stride")
     m_grid = int(grid_m_max) if grid_m_max is not None else M
-    bm = BLOCK_M if BLOCK_M else pick_block_m("w8a8", m_grid, N, K)
+    bm = int(BLOCK_M) if BLOCK_M else 0  # 0: the library picks the tile (cost model over M, N, K)
     bn = _w8a8_block_n(BLOCK_N)
     nw = int(num_warps) if num_warps else 4
     ws = workspace or _ws.shared(a_q.device)

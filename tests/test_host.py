@@ -192,11 +192,21 @@ def test_make_paged_kv_invariants():
     assert (kc.abs().amax(-1) == 127).float().mean() > 0.99       # per-(page,slot,head) amax hits 127
 
 
-def test_tile_staircase_default():
-    from specq.tiles import default_block_m, pick_block_m
-    assert default_block_m("w8a8", 1) == 16 and default_block_m("w8a8", 72) == 80
-    assert default_block_m("w8a8", 300) == 304 and default_block_m("w8a8", 321) <= 320
-    assert pick_block_m("w4a16", 300, 4096, 4096) <= 256
+def test_automatic_tiles_split_k_only_where_the_model_prices_it(built_lib):
+    # The library's tile choice (host-side cost model, no device needed): decode tiles (M <= 16)
+    # never split K, so they need no workspace; down (K = 14336) at the verification batch
+    # does; and a grouped launch sizes its workspace like the fused width.
+    from specq import _lib
+    L = _lib.lib()
+    assert L.specq_w8a8_packed_workspace_size(8, 4096, 4096, 0, 0, 4, 0) == 0
+    assert L.specq_w8a8_packed_workspace_size(8, 28672, 4096, 0, 0, 4, 0) == 0
+    assert L.specq_w8a8_packed_workspace_size(72, 4096, 14336, 0, 0, 4, 0) > 256 * 1024
+    import ctypes
+    Ns = (ctypes.c_int * 2)(14336, 14336)
+    assert L.specq_w8a8_grouped_workspace_size(1, 72, 2, Ns, 4096, 0, 0, 4, 0) == \
+        L.specq_w8a8_packed_workspace_size(72, 28672, 4096, 0, 0, 4, 0)
+    bad = (ctypes.c_int * 2)(14336, 0)
+    assert L.specq_w8a8_grouped_workspace_size(1, 72, 2, bad, 4096, 0, 0, 4, 0) == 0
 
 
 def test_gpu_entry_points_refuse_cpu_tensors():
