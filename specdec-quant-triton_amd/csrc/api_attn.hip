@@ -118,6 +118,8 @@ extern "C" int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64
   SPECQ_REQUIRE((uintptr_t)kc % 16 == 0 && (uintptr_t)vc % 16 == 0 && s_kp % 16 == 0 && s_ko % 16 == 0 &&
                     s_kh % 16 == 0,
                 SPECQ_ENOTSUP, "paged_attn: K/V cache rows must be 16-byte aligned");
+  SPECQ_REQUIRE(s_ko > 0 && 16 * s_ko + D < ((int64_t)1 << 31), SPECQ_ENOTSUP,
+                "paged_attn: token stride %lld of the K/V cache outside (0, 2^27)", (long long)s_ko);
   if (B_grid == 0) return SPECQ_OK;
   const int rb = ceil_div(QPP * G, 16);
   const void* fn = attn_fn(D, rb, scale_fp32 ? 1 : 0);

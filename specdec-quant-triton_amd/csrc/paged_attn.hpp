@@ -81,6 +81,10 @@ constexpr int kAttnMinUnits = 2;                    // shortest split: 256 token
 constexpr int kAttnMaxUnits = 32;                   // longest split: 4096 tokens (32 page ids per wave)
 constexpr int kAttnMergeMax = 64;                   // most splits one program merges
 constexpr int kAttnRing = 4;                        // LDS chunk slots per wave
+// Largest unnormalised probability p = exp2(s - m) the lazy running max lets through (2^6):
+// p * vs stays at most 64 * 65504 / 127 < 65504, inside fp16, for the V scale of any fp16 row
+// quantised to int8 (vs <= 65504 / 127).
+constexpr float kAttnLazyP = 64.f;
 constexpr int64_t kAttnMaxTokens = (int64_t)kAttnUnit * kAttnMaxUnits * kAttnMergeMax;  // 262144
 
 // 128-token units per split for a sequence of L tokens when `pairs` (sequence, KV head) pairs
@@ -131,22 +135,48 @@ __device__ __forceinline__ float group_max4(float x) {
   return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
 }
 
-// LDS DMA from 64-bit per-lane addresses (lds wave-uniform): lane l's 16 bytes land at
-// lds + 16 l (dwordx4), its dword at lds + 4 l (dword), its 16-bit value in the low half of the
-// dword at lds + 4 l (ushort).  Issued as inline asm: the compiler then neither counts these
-// loads nor makes LDS accesses wait for them, and every dependence on them is an explicit
-// wait_vmcnt of the kernel (its own loads only ever get stricter waits, which stays correct).
+// Unsigned max over the four 16-lane rows of a lane's column (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ uint32_t group_umax4(uint32_t u) {
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const uint32_t m1 = max((uint32_t)a[0], (uint32_t)a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(m1, m1, false, false);
+  return max((uint32_t)b[0], (uint32_t)b[1]);
+}
+
+// LDS DMA (lds wave-uniform): lane l's 16 bytes land at lds + 16 l (dwordx4), its dword at
+// lds + 4 l (dword), its 16-bit value in the low half of the dword at lds + 4 l (ushort).  The
+// K/V DMAs are buffer loads: the chunk's page sub-tile is the resource base (scalar), the lane's
+// granule offset within it the VGPR offset, which is the same for every chunk, so a chunk's
+// addresses cost no vector arithmetic; an offset with bit 31 set is out of range and writes
+// zeros.  The scale DMA reads from 64-bit per-lane addresses (lanes read K or V scales).
+// Issued as inline asm: the compiler then neither counts these loads nor makes LDS accesses
+// wait for them, and every dependence on them is an explicit wait_vmcnt of the kernel (its own
+// loads only ever get stricter waits, which stays correct).  An LDS DMA reads M0 one wait state
+// after it is written, hence the s_nop.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(lds_ptr_t)p;
 }
-__device__ __forceinline__ void dma16_global(const void* src, uint8_t* lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr(lds)) : "memory", "m0");
+// Raw buffer resource over [base, base + 2^31): offsets with bit 31 set are out of range.
+__device__ __forceinline__ v4i attn_rsrc(const void* base) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  return v4i{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xFFFFu), (int)kOOB, kRsrcWord3};
+}
+__device__ __forceinline__ void dma16_rs(v4i rs, uint32_t voff, uint8_t* lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs),
+               "s"(lds_addr(lds))
+               : "memory", "m0");
 }
 __device__ __forceinline__ void dma4_global(const void* src, uint8_t* lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds_addr(lds)) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds_addr(lds)) : "memory", "m0");
 }
 __device__ __forceinline__ void dma2_global(const void* src, uint8_t* lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_ushort %0, off" ::"v"(src), "s"(lds_addr(lds)) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_ushort %0, off" ::"v"(src), "s"(lds_addr(lds)) : "memory", "m0");
+}
+// 64-bit value of lane `l` (wave-uniform l).
+__device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 template <int D, int RB, typename ST>
@@ -273,54 +303,62 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
     if (f < RB * NU * 64) (&q_lds[0][0][0])[f] = qtmp[i];
   }
 
-  const int64_t head_k = (int64_t)kvh * p.s_kh;
-  const int64_t head_s = (int64_t)kvh * p.s_sh;
   // Chunk-invariant per-lane parts of the DMA addresses: the byte offset of the lane's K/V
-  // granule within the chunk's page sub-tile (DMA i covers chunk tokens 64 i / GR ..), and the
-  // element offset of its scale.  Lanes l < 16 fetch ks of token perm(l), 16 <= l < 32 vs of
-  // token perm(l - 16), lanes 32.. repeat lanes 0..31.
-  int64_t kvoff[NDMA];
+  // granule within the chunk's page sub-tile (DMA i covers chunk tokens 64 i / GR ..; below
+  // 2^31, which the host checks), and the address of its scale within the chunk's first token.
+  // Lanes l < 16 fetch ks of token perm(l), 16 <= l < 32 vs of token perm(l - 16), lanes 32..
+  // repeat lanes 0..31.
+  uint32_t kvoff[NDMA];
 #pragma unroll
   for (int i = 0; i < NDMA; ++i) {
     const int gi = 64 * i + lane, T = gi / GR, s = gi % GR;
-    kvoff[i] = (int64_t)T * p.s_ko + 16 * (s ^ attn_key<GR>(T));
+    kvoff[i] = (uint32_t)((int64_t)T * p.s_ko + 16 * (s ^ attn_key<GR>(T)));
   }
   const int sc_T = attn_perm(lane & 15);
-  const int64_t sc_off = (int64_t)sc_T * p.s_so * (int64_t)sizeof(ST);
   const uint8_t* sc_src = reinterpret_cast<const uint8_t*>((lane & 16) ? p.vs : p.ks);
-  // Issue the DMAs of chunk `it` into ring slot SL.  Chunks past the wave's last, and tokens at
-  // or past kv_end, read a fixed valid address instead.
+  const uint8_t* sc_lane = sc_src + (int64_t)sc_T * p.s_so * (int64_t)sizeof(ST);
+  // Per-chunk bases, lane c holding the wave's chunk c: the byte offset of the chunk's page
+  // sub-tile of this KV head in the K/V cache, and that of its first token's scales.  Chunks
+  // at or past the wave's last use page 0 (their DMAs read nothing or a fixed valid address).
+  int64_t kv_base_v, sc_base_v;
+  {
+    const int pg = lane < n_it ? page_v : 0;
+    const int tk = chunk_t0(lane) % p.PAGE;
+    kv_base_v = (int64_t)pg * p.s_kp + (int64_t)tk * p.s_ko + (int64_t)kvh * p.s_kh;
+    sc_base_v = ((int64_t)pg * p.s_sp + (int64_t)tk * p.s_so + (int64_t)kvh * p.s_sh) * (int64_t)sizeof(ST);
+  }
+  // Issue the DMAs of chunk `it` into ring slot SL.  K/V granules of chunks past the wave's
+  // last, and of tokens at or past kv_end, are out of range (zeros); their scales read a fixed
+  // valid address.
   auto issue = [&](auto slc, int it) __attribute__((always_inline)) {
     uint8_t* dst = ring_of(slc, w);
     const bool real = it < n_it;
     const int t0 = chunk_t0(it);
-    const int pg = real ? __builtin_amdgcn_readlane(page_v, min(it, 63)) : 0;
-    const int tk = t0 % p.PAGE;
-    const int64_t pb = (int64_t)pg * p.s_kp + (int64_t)tk * p.s_ko + head_k;
-    const int64_t sb = ((int64_t)pg * p.s_sp + (int64_t)tk * p.s_so + head_s) * (int64_t)sizeof(ST);
+    const int li = min(it, 63);
+    const int64_t kb = readlane64(kv_base_v, li);
+    const int64_t sb = readlane64(sc_base_v, li);
+    const v4i rk = attn_rsrc(p.kc + kb), rv = attn_rsrc(p.vc + kb);
     if (real && t0 + kAttnChunk <= kv_end) {
 #pragma unroll
-      for (int i = 0; i < NDMA; ++i) dma16_global(p.kc + pb + kvoff[i], dst + 1024 * i);
+      for (int i = 0; i < NDMA; ++i) dma16_rs(rk, kvoff[i], dst + 1024 * i);
 #pragma unroll
-      for (int i = 0; i < NDMA; ++i) dma16_global(p.vc + pb + kvoff[i], dst + KB + 1024 * i);
-      const uint8_t* src = sc_src + sb + sc_off;
+      for (int i = 0; i < NDMA; ++i) dma16_rs(rv, kvoff[i], dst + KB + 1024 * i);
+      const uint8_t* src = sc_lane + sb;
       if constexpr (sizeof(ST) == 4) dma4_global(src, dst + SC);
       else dma2_global(src, dst + SC);
     } else {
 #pragma unroll
       for (int i = 0; i < NDMA; ++i) {
-        const int gi = 64 * i + lane;
-        const bool ok = real && t0 + gi / GR < kv_end;
-        dma16_global(p.kc + (ok ? pb + kvoff[i] : 16 * (gi % GR)), dst + 1024 * i);
+        const bool ok = real && t0 + (64 * i + lane) / GR < kv_end;
+        dma16_rs(rk, oob_unless(ok, kvoff[i]), dst + 1024 * i);
       }
 #pragma unroll
       for (int i = 0; i < NDMA; ++i) {
-        const int gi = 64 * i + lane;
-        const bool ok = real && t0 + gi / GR < kv_end;
-        dma16_global(p.vc + (ok ? pb + kvoff[i] : 16 * (gi % GR)), dst + KB + 1024 * i);
+        const bool ok = real && t0 + (64 * i + lane) / GR < kv_end;
+        dma16_rs(rv, oob_unless(ok, kvoff[i]), dst + KB + 1024 * i);
       }
       const bool ok = real && t0 + sc_T < kv_end;
-      const uint8_t* src = sc_src + (ok ? sb + sc_off : 0);
+      const uint8_t* src = ok ? sc_lane + sb : sc_src;
       if constexpr (sizeof(ST) == 4) dma4_global(src, dst + SC);
       else dma2_global(src, dst + SC);
     }
@@ -334,11 +372,20 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
     if constexpr (QREG) return qreg[rb][u];
     else return q_lds[rb][u][lane];
   };
-  // One chunk from ring slot SL: S^T, online softmax, O^T += V^T . P^T.
-  auto compute = [&](auto slc, int it) __attribute__((always_inline)) {
+  // One chunk in two stages.  Stage A reads the chunk's K, V and scales from its ring slot,
+  // converts K to fp16 and computes S^T = K . Q^T; stage B applies the scales and the causal
+  // mask, runs the online softmax and accumulates O^T += V^T . P^T.  A wave issues stage A of
+  // chunk it + 1 before stage B of chunk it, so the S^T MFMAs of one chunk are in flight
+  // while the other's softmax runs.  Each chunk's arithmetic is unchanged, so the results do
+  // not depend on the pipelining.
+  struct Staged {
+    v4f cs[RB];                // S^T of the chunk before the scales
+    float ksc[4], vsc[4];      // K scale * sm_scale * log2(e), V scale, in operand order
+    uint32_t vx[4][ND / 4];    // V bytes of operand slots 4g..4g+3
+  };
+  auto stage_a = [&](auto slc, Staged& st) __attribute__((always_inline)) {
     const uint8_t* kb = ring_of(slc, w);
     const uint8_t* vb = kb + KB;
-    const int t0 = chunk_t0(it);
     // K operands: lane (r, g) holds head-dim bytes [DS*g, DS*g + DS) of token perm(r).
     v8h kf[NU];
     {
@@ -352,23 +399,20 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
     }
     // V^T operands: lane (r, g) reads bytes [ND*r, ND*r + ND) of tokens perm(4g + e), operand
     // slot 4g + e of the 16x16x16 product.
-    uint32_t vx[4][ND / 4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int T = attn_perm(4 * g + e);
       const uint8_t* src = vb + T * D + 16 * (((ND * r) >> 4) ^ attn_key<GR>(T)) + ((ND * r) & 15);
       if constexpr (ND == 8) {
         const v2i x = *reinterpret_cast<const v2i*>(src);
-        vx[e][0] = (uint32_t)x.x;
-        vx[e][1] = (uint32_t)x.y;
+        st.vx[e][0] = (uint32_t)x.x;
+        st.vx[e][1] = (uint32_t)x.y;
       } else {
-        vx[e][0] = *reinterpret_cast<const uint32_t*>(src);
+        st.vx[e][0] = *reinterpret_cast<const uint32_t*>(src);
       }
     }
     // Scales in operand order: dword 4g + e holds ks of token perm(4g + e), dword 16 + 4g + e
-    // its vs (an fp16 scale in the low half); zero V scale for tokens at or past kv_end (their
-    // scale slots hold the dummy address's scale).
-    float ksc[4], vsc[4];
+    // its vs (an fp16 scale in the low half).
     {
       const v4i kr = *reinterpret_cast<const v4i*>(kb + SC + 16 * g);
       const v4i vr = *reinterpret_cast<const v4i*>(kb + SC + 64 + 16 * g);
@@ -385,76 +429,98 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
           kv = (float)__builtin_bit_cast(_Float16, (uint16_t)(ki & 0xFFFF));
           vv = (float)__builtin_bit_cast(_Float16, (uint16_t)(vi & 0xFFFF));
         }
-        ksc[e] = kv * p.scale_log2;
-        vsc[e] = vv;
+        st.ksc[e] = kv * p.scale_log2;
+        st.vsc[e] = vv;
       }
     }
-
-    if (t0 + kAttnChunk > kv_end) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (t0 + attn_perm(4 * g + e) >= kv_end) vsc[e] = 0.f;
-    }
-    // S^T of every row block first (RB independent MFMA chains), then the softmax of every
-    // row block, so the chains and the softmax arithmetic of different row blocks interleave.
-    v4f cs[RB];
+    // S^T of every row block (RB independent MFMA chains).
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       v4f c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int u = 0; u < NU; ++u) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[u], qfrag(rb, u), c, 0, 0, 0);
-      cs[rb] = c;
+      st.cs[rb] = c;
+    }
+  };
+  auto stage_b = [&](int it, const Staged& st) __attribute__((always_inline)) {
+    const int t0 = chunk_t0(it);
+    // Zero V scale for tokens at or past kv_end (their scale slots hold the dummy address's).
+    float vsc[4] = {st.vsc[0], st.vsc[1], st.vsc[2], st.vsc[3]};
+    if (t0 + kAttnChunk > kv_end) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (t0 + attn_perm(4 * g + e) >= kv_end) vsc[e] = 0.f;
     }
     // Every row of the program sees every token of the chunk: no causal mask needed.
     const bool full = t0 + kAttnChunk - 1 <= L - q_len + qc * p.QPP;
-    v4h pf[RB];
-    float alpha[RB];
-    bool grew = false;
+    // Unnormalised probabilities against the row's running max m: p = exp2(s_raw * ksc - m)
+    // (one fma; masked tokens 0).  While m = -inf every visible p is +inf.  The row max of p is
+    // taken on the bit patterns (p >= 0, so their integer order is the numeric order).
+    float pr[RB][4];
+    uint32_t pbig = 0;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      float s[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) s[e] = cs[rb][e] * ksc[e];
+      for (int e = 0; e < 4; ++e) pr[rb][e] = fast_exp2(fmaf(st.cs[rb][e], st.ksc[e], -m_run[rb]));
       if (!full) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (t0 + attn_perm(4 * g + e) > qpos[rb]) s[e] = -INFINITY;
+          if (t0 + attn_perm(4 * g + e) > qpos[rb]) pr[rb][e] = 0.f;
       }
-      // The running max is the same in the four lanes of a row, so the row max only needs the
-      // cross-lane reduction (and alpha its exp) when some lane's own max exceeds it; after the
-      // first chunks that is rare, and the result is the same either way.
-      const float lmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-      float m_new = m_run[rb];
-      alpha[rb] = 1.f;
-      if (__builtin_amdgcn_ballot_w64(lmax > m_run[rb]) != 0) {
-        m_new = fmaxf(m_run[rb], group_max4(lmax));
-        const float m_safe0 = (m_new == -INFINITY) ? 0.f : m_new;
-        alpha[rb] = fast_exp2(m_run[rb] - m_safe0);
-        grew |= m_new > m_run[rb];
-      }
-      const float m_safe = (m_new == -INFINITY) ? 0.f : m_new;
-      float psum = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float pv = fast_exp2(s[e] - m_safe);
-        psum += pv;
-        pf[rb][e] = (_Float16)f32_opaque(pv * vsc[e]);  // fp32 product, then fp16 (kernels.py:232)
-      }
-      l_run[rb] = l_run[rb] * alpha[rb] + psum;
-      m_run[rb] = m_new;
+      const uint32_t b0 = __builtin_bit_cast(uint32_t, pr[rb][0]), b1 = __builtin_bit_cast(uint32_t, pr[rb][1]);
+      const uint32_t b2 = __builtin_bit_cast(uint32_t, pr[rb][2]), b3 = __builtin_bit_cast(uint32_t, pr[rb][3]);
+      pbig = max(pbig, max(max(b0, b1), max(b2, b3)));
     }
-    // alpha is exactly 1 for every row whose running max did not grow, so the O rescale is
-    // skipped (bit-identically) unless some row grew, which after the first chunks is rare.
-    if (__builtin_amdgcn_ballot_w64(grew) != 0) {
+    // Lazy running max: a row's m moves only when one of its p exceeds kAttnLazyP, i.e. a
+    // score exceeds m by more than 6; m then becomes the row's exact max score and the
+    // row's p, l and O are rescaled.  After a row's first chunk that is rare, so one wave-wide
+    // test guards it.  The decision is the row's own (its four lanes see the same row max of p),
+    // so each row's result does not depend on the rows packed with it.
+    float alpha[RB];
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
+    for (int rb = 0; rb < RB; ++rb) alpha[rb] = 1.f;
+    if (__builtin_amdgcn_ballot_w64(pbig > __builtin_bit_cast(uint32_t, kAttnLazyP)) != 0) {
+      bool grew = false;
 #pragma unroll
-        for (int db = 0; db < ND; ++db) acc[rb][db] *= alpha[rb];
+      for (int rb = 0; rb < RB; ++rb) {
+        const uint32_t b0 = __builtin_bit_cast(uint32_t, pr[rb][0]), b1 = __builtin_bit_cast(uint32_t, pr[rb][1]);
+        const uint32_t b2 = __builtin_bit_cast(uint32_t, pr[rb][2]), b3 = __builtin_bit_cast(uint32_t, pr[rb][3]);
+        const uint32_t rowp = group_umax4(max(max(b0, b1), max(b2, b3)));
+        float s[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[e] = st.cs[rb][e] * st.ksc[e];
+          if (!full && t0 + attn_perm(4 * g + e) > qpos[rb]) s[e] = -INFINITY;
+        }
+        const float rmax = group_max4(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+        if (rowp > __builtin_bit_cast(uint32_t, kAttnLazyP)) {
+          alpha[rb] = fast_exp2(m_run[rb] - rmax);  // 0 from m = -inf
+          m_run[rb] = rmax;
+          grew = true;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            pr[rb][e] = s[e] == -INFINITY ? 0.f : fast_exp2(fmaf(st.cs[rb][e], st.ksc[e], -rmax));
+        }
+      }
+      // alpha is exactly 1 for every row whose m did not move.
+      if (__builtin_amdgcn_ballot_w64(grew) != 0) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int db = 0; db < ND; ++db) acc[rb][db] *= alpha[rb];
+      }
+    }
+    v4h pf[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      l_run[rb] = l_run[rb] * alpha[rb] + ((pr[rb][0] + pr[rb][1]) + (pr[rb][2] + pr[rb][3]));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pf[rb][e] = (_Float16)f32_opaque(pr[rb][e] * vsc[e]);  // fp32 product, then fp16 (kernels.py:232)
     }
     // V bytes to d-major: vt[db] = the 4 token bytes (operand slots 4g..4g+3) of d = ND*r + db.
 #pragma unroll
     for (int c = 0; c < ND / 4; ++c) {
-      const uint32_t x[4] = {vx[0][c], vx[1][c], vx[2][c], vx[3][c]};
+      const uint32_t x[4] = {st.vx[0][c], st.vx[1][c], st.vx[2][c], st.vx[3][c]};
       uint32_t y[4];
       transpose4x4(x, y);
 #pragma unroll
@@ -483,16 +549,42 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
 #pragma unroll
       for (int u = 0; u < NU; ++u) qreg[rb][u] = q_lds[rb][u][lane];
   }
-  // Steady state: issue chunk it + NS - 1 into the slot chunk it - 1 left, wait for chunk it
-  // (NS - 1 chunks may stay in flight), multiply it.
-  for (int base = 0; base < n_it; base += NS) {
-    static_for<0, NS>([&](auto ic) __attribute__((always_inline)) {
-      constexpr int i = decltype(ic)::value;
-      const int it = base + i;
-      issue(ic, it + NS - 1);
-      wait_vmcnt<(NS - 1) * NVM>();
-      if (it < n_it) compute(std::integral_constant<int, (i + 1) % NS>{}, it);
-    });
+  // Steady state, step it: issue chunk it + NS - 1 into the slot chunk it - 1 left (both its
+  // stages have run), wait for chunk it + 1 (NS - 2 chunks may stay in flight), run stage A of
+  // chunk it + 1, then stage B of chunk it.  Chunk it's staged state lives in st[it % 2]; NS is
+  // even, so the index is a compile-time constant in the unrolled body.
+  // The 64-row program at D = 128 has no registers for a second staged state and runs the two
+  // stages of a chunk back to back (waiting for chunk it itself, NS - 1 chunks in flight).
+  constexpr bool PIPE = !(RB == 4 && D == 128);
+  static_assert(NS % 2 == 0, "staged state ping-pong");
+  if constexpr (PIPE) {
+    Staged st[2];
+    wait_vmcnt<(NS - 2) * NVM>();  // chunk 0 has landed
+    if (n_it > 0) stage_a(std::integral_constant<int, 1 % NS>{}, st[0]);
+    for (int base = 0; base < n_it; base += NS) {
+      static_for<0, NS>([&](auto ic) __attribute__((always_inline)) {
+        constexpr int i = decltype(ic)::value;
+        const int it = base + i;
+        issue(ic, it + NS - 1);
+        wait_vmcnt<(NS - 2) * NVM>();
+        if (it + 1 < n_it) stage_a(std::integral_constant<int, (i + 2) % NS>{}, st[(i + 1) & 1]);
+        if (it < n_it) stage_b(it, st[i & 1]);
+      });
+    }
+  } else {
+    for (int base = 0; base < n_it; base += NS) {
+      static_for<0, NS>([&](auto ic) __attribute__((always_inline)) {
+        constexpr int i = decltype(ic)::value;
+        const int it = base + i;
+        issue(ic, it + NS - 1);
+        wait_vmcnt<(NS - 1) * NVM>();
+        if (it < n_it) {
+          Staged st;
+          stage_a(std::integral_constant<int, (i + 1) % NS>{}, st);
+          stage_b(it, st);
+        }
+      });
+    }
   }
   // Every DMA has landed before the ring is reused for the merge.
   wait_vmcnt<0>();

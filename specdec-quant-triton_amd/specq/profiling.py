@@ -21,6 +21,10 @@ Subcommands (run from the repository root):
   traffic   reads the FETCH_SIZE and WRITE_SIZE `--pmc` csv files of two probe runs and writes
             the HBM bytes per launch of each probed kernel, scaled by what the same counters
             read for the copy kernel (bytes = counter KiB * 1024 * copy_bytes / copy_counter).
+  sq        reads one or more `--pmc` runs of SQ_* (and GRBM_GUI_ACTIVE) counters: per kernel the
+            median per dispatch of each counter, instructions per wave (SQ_INSTS_* / SQ_WAVES),
+            and the share of wave cycles spent issuing each instruction class
+            (SQ_ACTIVE_INST_* / SQ_WAVE_CYCLES, both counted per wave in the same units).
   mfma      reads a `--pmc SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_INSTS_VALU_MFMA_MOPS_F16` run: the
             MFMA ops issued (512 per MOPS unit) against the algorithmic 2*M*N*K, and achieved
             TOP/s from an unprofiled probe's timing (`--map`) against the dense peak.
@@ -261,6 +265,45 @@ def traffic(args) -> int:
     return 0
 
 
+def _all_counters(dirname: str):
+    """{kernel short name: {counter: [value per dispatch]}} of every specq kernel in a run."""
+    vals = collections.defaultdict(lambda: collections.defaultdict(list))
+    files = glob.glob(os.path.join(dirname, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {dirname}")
+    for f in files:
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                if "specq::" in r["Kernel_Name"]:
+                    vals[_short(r["Kernel_Name"])][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    return vals
+
+
+def sq(args) -> int:
+    """Per-kernel SQ counter medians and per-wave ratios from one or more --pmc runs."""
+    merged = collections.defaultdict(dict)
+    for d in args.dirs:
+        for name, cs in _all_counters(d).items():
+            for c, v in cs.items():
+                merged[name][c] = statistics.median(v)
+    wmap = json.load(open(args.map)) if args.map else {}
+    for name, cs in sorted(merged.items()):
+        wl = wmap.get(name, {}).get("workload", "")
+        print(f"\n### `{name}` {wl}\n")
+        print("| counter | median per dispatch | per wave |")
+        print("|---|---|---|")
+        waves = cs.get("SQ_WAVES")
+        for c in sorted(cs):
+            pw = f"{cs[c] / waves:.1f}" if waves and c.startswith("SQ_INSTS") else ""
+            print(f"| {c} | {cs[c]:.0f} | {pw} |")
+        wc = cs.get("SQ_WAVE_CYCLES")
+        if wc:
+            shares = [(c[len("SQ_ACTIVE_INST_"):], cs[c] / wc) for c in sorted(cs) if c.startswith("SQ_ACTIVE_INST_")]
+            shares += [(c[len("SQ_"):], cs[c] / wc) for c in ("SQ_WAIT_ANY", "SQ_WAIT_INST_ANY") if c in cs]
+            print("\nshare of wave cycles: " + ", ".join(f"{k} {100 * v:.1f} %" for k, v in shares))
+    return 0
+
+
 def mfma(args) -> int:
     """Issued MFMA ops (from the MOPS counters) against 2*M*N*K, and achieved TOP/s per kernel."""
     wmap = json.load(open(args.map))
@@ -339,6 +382,9 @@ def staircase(args) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
+    p = sub.add_parser("sq")
+    p.add_argument("dirs", nargs="+")
+    p.add_argument("--map", default=None)
     p = sub.add_parser("probe")
     p.add_argument("--kinds", default="w8a8:72,copy")
     p.add_argument("--layers", type=int, default=16)
@@ -366,7 +412,7 @@ def main() -> int:
     c.add_argument("--out", required=True)
     args = ap.parse_args()
     return {"probe": probe, "stats": stats, "traffic": traffic, "mfma": mfma, "staircase": staircase,
-            "staircase-md": staircase_md}[args.cmd](args)
+            "staircase-md": staircase_md, "sq": sq}[args.cmd](args)
 
 
 if __name__ == "__main__":
