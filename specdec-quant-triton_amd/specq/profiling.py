@@ -202,7 +202,9 @@ def stats(args) -> int:
                 name = r["Kernel_Name"]
                 if args.filter and args.filter not in name:
                     continue
-                wgs = int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"]))
+                wgs = 1
+                for ax in "XYZ":
+                    wgs *= int(r.get(f"Grid_Size_{ax}", 1) or 1) // max(1, int(r.get(f"Workgroup_Size_{ax}", 1) or 1))
                 dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
                 rows[(_short(name), wgs)].append(dur)
     table = sorted(rows.items(), key=lambda kv: -sum(kv[1]))[: args.top]
