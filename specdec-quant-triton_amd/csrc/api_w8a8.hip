@@ -250,7 +250,11 @@ void w8a8_auto_tiles(int M, int N, int K, double wb, int bnsel_fixed, int splits
         const double rounds = (double)ceil_div((int)wgs, cus);
         double t = std::max(rounds * (bn * wb + rows) * K / s / 45e3, N * wb * K / 6e6) + 1.0;
         if (s > 1) t += 2.0 + (double)s * rows * chunks * N * 8 / 2e6;
-        if (best_mt < 0 || t < best_t) { best_t = t; best_mt = mt; best_sel = sel; best_s = s; }
+        // Equal prices go to the shallower token tile (fewer activation rows per workgroup).
+        const bool tie = best_mt >= 0 && std::fabs(t - best_t) <= 1e-9 * best_t;
+        if (best_mt < 0 || (t < best_t && !tie) || (tie && mt < best_mt)) {
+          best_t = t; best_mt = mt; best_sel = sel; best_s = s;
+        }
       }
     }
   }
