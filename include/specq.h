@@ -225,9 +225,13 @@ int specq_w4a16_pack_weight(const void* wq, int64_t ldq, int wq_layout, int N, i
  *            (rows packed per program = QPP * H/H_KV, at most 64)
  *   plan     NULL, or device int32*: plan[0] = n_seqs, plan[1] = q_len (the reference passes
  *            plan[1:] of its [M, B, q_len] buffer, bench_graphs.py:58)
- *   D must be 64 or 128; PAGE a multiple of 16.  sm_scale is the softmax scale (1/sqrt(D)).
- *   The KV split across workgroups is a fixed function of token position (512 tokens per
- *   split), so results do not depend on B, QPP or the plan.
+ *   D must be 64 or 128; PAGE a multiple of 16; K/V rows 16-byte aligned with a token stride
+ *   s_ko below 2^27 bytes (SPECQ_ENOTSUP otherwise).  sm_scale is the softmax scale
+ *   (1/sqrt(D)).
+ *   A sequence's KV range is cut into splits of whole 128-token units, their length chosen
+ *   from the block table's capacity and the number of active (sequence, KV head) pairs, so a
+ *   QPP=1 and a fused call, and an eager and a plan-mode call, cut a sequence at the same
+ *   tokens and give bit-identical results.
  * ------------------------------------------------------------------------------------- */
 size_t specq_paged_attn_workspace_size(int B_grid, int H, int H_KV, int ql_grid, int QPP,
                                        int max_pages, int PAGE);
