@@ -71,7 +71,6 @@ struct AttnParams {
   int32_t* counters;   // [progs]
 };
 
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 constexpr int kAttnChunk = 16;                      // tokens per wave iteration (one page sub-tile)
 constexpr int kAttnWaves = 8;                       // two per SIMD

@@ -47,7 +47,6 @@ struct W4A16Params {
   int vec_store;
 };
 
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 // Two unsigned nibbles (bytes of y selected by sel) -> half2 of (nibble + 1024).
 __device__ __forceinline__ v2h nib_pair(uint32_t y, uint32_t sel) {

@@ -137,21 +137,24 @@ __device__ __forceinline__ void w8a8_unscale16(v4i (&acc)[RW][MT]) {
 
 // Epilogue for 4 consecutive output channels of one token row, with the token scale `a` and
 // the channel scales `w` already in registers (entries past N are not stored).
+// The fp16 outputs of 4 INT32 sums: each value is rounded to fp32 after `* a`, again after
+// `* w`, and then to fp16 (RNE), as in the reference (f32_opaque keeps the compiler from
+// fusing the last multiply into the fp16 conversion).
+__device__ __forceinline__ v4h w8a8_cvt4(v4i s, float a, const float (&w)[4]) {
+  v4h o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = (_Float16)f32_opaque(((float)s[i] * a) * w[i]);
+  return o;
+}
 __device__ __forceinline__ void w8a8_store4s(const W8A8Params& p, int m, int n, v4i s, float a, const float (&w)[4]) {
   __half* dst = p.C + (int64_t)m * p.ldc + n;
-  // Each value is rounded to fp32 and then to fp16, as in the reference (f32_opaque keeps the
-  // compiler from fusing the last multiply into the fp16 conversion).
-  float v[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = f32_opaque(((float)s[i] * a) * w[i]);
+  const v4h o = w8a8_cvt4(s, a, w);
   if (p.vec_store && n + 3 < p.N) {
-    typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-    const v4h o = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
     *reinterpret_cast<v4h*>(dst) = o;
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (n + i < p.N) dst[i] = __float2half_rn(v[i]);
+      if (n + i < p.N) reinterpret_cast<_Float16*>(dst)[i] = o[i];
   }
 }
 
@@ -218,8 +221,10 @@ __device__ __forceinline__ void w8a8_splitk_finish(const W8A8Params& p, rsrc_t p
   if (!arrive_last(p.counters + cidx, p.splits, s_last)) return;
   constexpr int QUADS = BM * BN / 4;
   constexpr int QPT = (QUADS + NT - 1) / NT;                   // quads per thread
-  constexpr int QG = QPT < 4 ? QPT : 4;                        // quads summed together
-  constexpr int SB = 16 / QG > 8 ? 8 : 16 / QG;                // splits loaded together
+  // Up to 8 quads per thread are summed in one round of loads (up to 32 loads in flight);
+  // the deepest tiles, whose main loops need every register, take 4 quads per round.
+  constexpr int QG = QPT <= 8 ? QPT : 4;                       // quads summed together
+  constexpr int SB = (QPT <= 8 ? 32 : 16) / QG > 8 ? 8 : (QPT <= 8 ? 32 : 16) / QG;  // splits loaded together
 #pragma unroll
   for (int g0 = 0; g0 < QPT; g0 += QG) {
     int ml[QG], nl[QG];

@@ -275,14 +275,43 @@ __global__ __launch_bounds__(NW * 64) void w8a8_ws_kernel(W8A8Params p) {
 
   const int cidx = mc * p.n_tiles + tile;
   if (p.splits == 1) {
+    // The fp16 tile goes through LDS (row-major, 16-byte pieces XOR-swizzled by row), so that
+    // each lane then stores 16 contiguous bytes of an output row and a wave's store covers
+    // whole rows of the tile instead of 32-byte pieces of 16 rows.
+    constexpr int PIECES = BN / 8;  // 16-byte pieces per tile row
+    static_assert(BM * BN * 2 <= SLOT, "the fp16 tile fits one activation slot");
+    uint8_t* ctile = slot_ptr(std::integral_constant<int, 0>{});
+    if constexpr (KW > 1) wg_barrier_lds();  // the owners have read the reduction slices
     if (owner) {
 #pragma unroll
       for (int a = 0; a < RW; ++a)
 #pragma unroll
         for (int u = 0; u < MT; ++u) {
-          const int m = m0 + u * 16 + r, n = n0 + a * 16 + 4 * g;
-          if (m < M && n < p.N) w8a8_store4s(p, m, n, acc[a][u], es.a[u], es.w[a]);
+          const int row = u * 16 + r, nl = cw * BNW + a * 16 + 4 * g;
+          const int pc = (nl >> 3) ^ (row & (PIECES - 1));
+          *reinterpret_cast<v4h*>(ctile + row * (BN * 2) + pc * 16 + (nl & 4) * 2) = w8a8_cvt4(acc[a][u], es.a[u], es.w[a]);
         }
+    }
+    wg_barrier_lds();
+    const int nt0 = ltile * BN;
+    const bool v16 = ((uintptr_t)p.C % 16 == 0) & (p.ldc % 8 == 0);
+    constexpr int NT = NW * 64, QN = BM * PIECES;
+#pragma unroll
+    for (int i = 0; i < (QN + NT - 1) / NT; ++i) {
+      const int q = (int)threadIdx.x + i * NT;
+      const int row = q / PIECES, pc = q % PIECES;
+      const int m = m0 + row, n = nt0 + pc * 8;
+      if ((QN % NT == 0 || q < QN) && m < M && n < p.N) {
+        const v8h v = *reinterpret_cast<const v8h*>(ctile + row * (BN * 2) + ((pc ^ (row & (PIECES - 1))) * 16));
+        _Float16* dst = reinterpret_cast<_Float16*>(p.C + (int64_t)m * p.ldc + n);
+        if (v16 && n + 7 < p.N) {
+          *reinterpret_cast<v8h*>(dst) = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (n + e < p.N) dst[e] = v[e];
+        }
+      }
     }
     return;
   }
