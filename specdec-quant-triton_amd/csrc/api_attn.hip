@@ -139,7 +139,16 @@ extern "C" int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64
   }
   SPECQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), SPECQ_ENOSPC,
                 "paged_attn: workspace of %zu bytes required, %zu given", need, workspace ? workspace_bytes : 0);
-  SPECQ_REQUIRE((int64_t)H_KV * n_qc <= 65535 && B_grid <= 65535, SPECQ_ENOTSUP, "paged_attn: grid too large");
+  // One-dimensional grid of program x split (the kernel derives both from the active count):
+  // the exact count for an eager call, the most any active count needs in plan mode.
+  int64_t wgs = (int64_t)(plan ? B_grid : n_seqs) * H_KV * n_qc * ns;
+  if (plan) {
+    wgs = 0;
+    for (int s = 1; s <= B_grid; ++s)
+      wgs = std::max(wgs, (int64_t)s * H_KV * n_qc * n_splits_for(max_pages, PAGE, s * H_KV, target));
+  }
+  if (wgs == 0) return SPECQ_OK;
+  SPECQ_REQUIRE(wgs <= INT32_MAX, SPECQ_ENOTSUP, "paged_attn: grid too large");
   AttnParams p;
   p.q = (const _Float16*)q; p.s_qb = s_qb; p.s_qt = s_qt; p.s_qh = s_qh;
   p.kc = kc; p.vc = vc; p.s_kp = s_kp; p.s_ko = s_ko; p.s_kh = s_kh;
@@ -153,8 +162,7 @@ extern "C" int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64
   p.counters = need ? (int32_t*)workspace : nullptr;
   p.part = need ? (float*)((char*)workspace + kCounterBytes) : nullptr;
   void* args[] = {&p};
-  hipError_t e = hipLaunchKernel(fn, dim3(ns, H_KV * n_qc, B_grid), dim3(kAttnThreads), args, 0,
-                                 (hipStream_t)stream);
+  hipError_t e = hipLaunchKernel(fn, dim3((unsigned)wgs), dim3(kAttnThreads), args, 0, (hipStream_t)stream);
   if (e != hipSuccess) {
     set_error("paged_attn: hipLaunchKernel failed: %s", hipGetErrorString(e));
     return SPECQ_EIO;

@@ -64,7 +64,7 @@ struct AttnParams {
   const int32_t* plan;
   int B_grid, n_seqs, q_len, ql_grid;
   int G, QPP, n_qc, H_KV, PAGE;
-  int n_splits;        // grid.x: the most splits any active sequence can have
+  int n_splits;        // the most splits any active count of sequences gives (workspace stride)
   int target_wgs;      // workgroups the split length aims at (the device's CUs)
   float scale_log2;    // sm_scale * log2(e)
   float* part;         // [progs][n_splits][rows][D] unnormalised O, then [progs][n_splits][rows][2] (m, l)
@@ -208,9 +208,6 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
   __shared__ int s_last;
   static_assert(NS == 4, "four ring variables");
 
-  const int split = blockIdx.x;
-  const int kvh = blockIdx.y / p.n_qc, qc = blockIdx.y % p.n_qc;
-  const int b = blockIdx.z;
   int n_seqs = p.n_seqs, q_len = p.q_len;
   if (p.plan != nullptr) {
     n_seqs = min(max(p.plan[0], 0), p.B_grid);
@@ -218,14 +215,21 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
   }
   n_seqs = uniform(n_seqs);
   q_len = uniform(q_len);
-  if (b >= n_seqs || qc * p.QPP >= q_len) return;
   // Splits are sized from the block table's capacity (not the sequence's own length), so the
   // page ids of the split can be fetched together with the context length and Q: one memory
   // round trip before the first K/V DMA.
   const int cap = p.max_pages * p.PAGE;
   const int split_tokens = kAttnUnit * attn_split_units(cap, n_seqs * p.H_KV, p.target_wgs);
+  // The grid is one-dimensional: workgroup id = program * splits + split, with the split count
+  // of the active sequences, so the workgroups that have work are the first ones dispatched and
+  // a plan-mode grid (sized for the worst active count) carries few idle workgroups.
+  const int ns_act = (cap + split_tokens - 1) / split_tokens;
+  const int prog = (int)blockIdx.x / ns_act;
+  const int split = (int)blockIdx.x - prog * ns_act;
+  if (prog >= n_seqs * p.H_KV * p.n_qc) return;
+  const int qc = prog % p.n_qc, kvh = (prog / p.n_qc) % p.H_KV, b = prog / (p.n_qc * p.H_KV);
+  if (qc * p.QPP >= q_len) return;
   const int s0 = split * split_tokens;
-  if (split > 0 && s0 >= cap) return;
   const int L_raw = p.ctx_len[b];
 
   const int lane = lane_id(), w = uniform(wave_id()), g = lane >> 4, r = lane & 15;
@@ -689,7 +693,6 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
               (_Float16)f32_opaque(v.w)};
   };
 
-  const int prog = (b * p.H_KV + kvh) * p.n_qc + qc;
   if (n_active == 1) {
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
@@ -706,7 +709,7 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
   // ---- Cross-split merge: publish this split's valid rows (16 bytes per lane), the last to
   // arrive combines the splits in split order.
   const int64_t prog_base = (int64_t)prog * p.n_splits;
-  const int64_t n_o = (int64_t)gridDim.y * gridDim.z * p.n_splits * ROWS * D;  // floats of the O region
+  const int64_t n_o = (int64_t)p.B_grid * p.H_KV * p.n_qc * p.n_splits * ROWS * D;  // floats of the O region
   const rsrc_t ors = make_rsrc(p.part + prog_base * ROWS * D, (uint32_t)(p.n_splits * ROWS * D * 4));
   float* mlpart = p.part + n_o;
 #pragma unroll
