@@ -16,11 +16,15 @@
 
 #include "api_common.hpp"
 #include "w8a8.hpp"
+#include "w8a8_plan.hpp"
 #include "w8a8_tiles.hpp"
 
 namespace specq {
 
 const void* w8a8_kernel_rw1(int mt, int vec);
+const void* w8a8_plan_fn_l0();
+const void* w8a8_plan_fn_l1();
+const void* w8a8_plan_fn_l2();
 const void* w8a8_kernel_rw2(int mt, int vec);
 const void* w8a8_kernel_rw4(int mt, int vec);
 
@@ -130,7 +134,9 @@ extern std::atomic<int> g_attn_target;  // api_attn.hip
 
 namespace {
 
-enum Family { kRk = 1, kWs = 2, kLegacy = 3 };
+// kPlan: plan-mode launch holding the menu of RK / WS tilings (w8a8_plan.hpp), one per 16 rows
+// of the active M.
+enum Family { kRk = 1, kWs = 2, kLegacy = 3, kPlan = 4 };
 
 struct W8A8Cfg {
   int family, layout;
@@ -139,6 +145,10 @@ struct W8A8Cfg {
   int bnsel;      // RK/WS channel-width variant (0..3 for 16/32/64/128)
   size_t lds, ws_partials, ws_counters;
   const void* fn;
+  // kPlan: the tiling of each 16-row step of M, the grid (the largest tiling's) and the
+  // counters the largest tiling uses; mt / bn / splits above describe the entry of M = m_grid.
+  W8A8PlanTile plan_t[kW8A8PlanRows];
+  int plan_grid, n_counters;
 };
 
 int round_mt_for_vec(int mt, int vec, int rw) {
@@ -225,11 +235,28 @@ static_assert(W8A8BnSel<0>::KW == 4 && W8A8BnSel<1>::KW == 2 && W8A8BnSel<2>::KW
 // weight tiles at ~45 GB/s, and the weight re-reads of later M chunks come from L2 / MALL.
 // 16-row chunks run on the direct-activation kernel, measured fast only with 16-channel
 // blocks, no split and one round of workgroups.
+// Modelled time of one tiling (token-tile depth mt, channel block sel, requested split count)
+// of `rows16` 16-row token tiles, from the model above; negative when the tiling is not one the
+// model allows.  *s_eff is the split count after whole-chunk boundaries.
+double w8a8_model_time(int rows16, int N, int K, double wb, int mt, int sel, int s_req, int* s_eff) {
+  const int cus = device_cus();
+  const int ksteps = ceil_div(K, 64), kq = ceil_div(ksteps, 4);
+  const int chunks = ceil_div(rows16, mt), rows = mt * 16;
+  const int bn = bn_of_sel(sel);
+  int s = std::min(s_req, kq);
+  s = ceil_div(K, ceil_div(kq, s) * 256);  // split count after whole-chunk boundaries
+  const int64_t wgs = (int64_t)ceil_div(N, bn) * s * chunks;
+  if (mt == 1 && (sel != 0 || s != 1 || wgs > cus)) return -1.0;
+  const double rounds = (double)ceil_div((int)wgs, cus);
+  double t = std::max(rounds * (bn * wb + rows) * K / s / 45e3, N * wb * K / 6e6) + 1.0;
+  if (s > 1) t += 2.0 + (double)s * rows * chunks * N * 8 / 2e6;
+  *s_eff = s;
+  return t;
+}
+
 void w8a8_auto_tiles(int M, int N, int K, double wb, int bnsel_fixed, int splits_fixed, int* mt_out, int* bnsel,
                      int* splits) {
-  const int cus = device_cus();
   const int rows16 = ceil_div(std::max(M, 1), 16);
-  const int ksteps = ceil_div(K, 64), kq = ceil_div(ksteps, 4);
   double best_t = 0;
   int best_mt = -1, best_sel = 2, best_s = 1, last_mt = -1;
   const int max_c = std::max(6, ceil_div(rows16, kW8A8MaxMt));  // past 6 chunks only when M needs it
@@ -237,19 +264,13 @@ void w8a8_auto_tiles(int M, int N, int K, double wb, int bnsel_fixed, int splits
     const int mt = ceil_div(rows16, c);
     if (mt == last_mt || mt > kW8A8MaxMt) continue;
     last_mt = mt;
-    const int chunks = ceil_div(rows16, mt), rows = mt * 16;
     for (int sel = 0; sel < 4; ++sel) {
       if (bnsel_fixed >= 0 && sel != bnsel_fixed) continue;
-      const int bn = bn_of_sel(sel);
       const int cand[3] = {splits_fixed > 0 ? splits_fixed : 1, 2, 4};
       for (int ci = 0; ci < (splits_fixed > 0 ? 1 : 3); ++ci) {
-        int s = std::min(cand[ci], kq);
-        s = ceil_div(K, ceil_div(kq, s) * 256);  // split count after whole-chunk boundaries
-        const int64_t wgs = (int64_t)ceil_div(N, bn) * s * chunks;
-        if (mt == 1 && (sel != 0 || s != 1 || wgs > cus)) continue;
-        const double rounds = (double)ceil_div((int)wgs, cus);
-        double t = std::max(rounds * (bn * wb + rows) * K / s / 45e3, N * wb * K / 6e6) + 1.0;
-        if (s > 1) t += 2.0 + (double)s * rows * chunks * N * 8 / 2e6;
+        int s = 1;
+        const double t = w8a8_model_time(rows16, N, K, wb, mt, sel, cand[ci], &s);
+        if (t < 0) continue;
         // Equal prices go to the shallower token tile (fewer activation rows per workgroup).
         const bool tie = best_mt >= 0 && std::fabs(t - best_t) <= 1e-9 * best_t;
         if (best_mt < 0 || (t < best_t && !tie) || (tie && mt < best_mt)) {
@@ -273,6 +294,13 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   const int rows16 = ceil_div(m_grid > 0 ? m_grid : 1, 16);
   const int want = block_n > 0 ? (block_n == 16 ? 0 : (block_n == 32 ? 1 : (block_n == 64 ? 2 : 3))) : -1;
   const int path = g_w8a8_path.load();
+  // Plan-mode calls with automatic tiles get the launch that picks a tiling per 16 rows of the
+  // active M on the device (its table is filled by w8a8_plan_table for the launch's GEMMs).
+  if (plan_mode && block_m <= 0 && block_n <= 0 && split_k <= 0 && vec == 16 && path == 0) {
+    cfg->family = kPlan; cfg->layout = layout; cfg->vec = vec; cfg->nw = 4; cfg->rw = 1;
+    cfg->fn = layout == 0 ? w8a8_plan_fn_l0() : (layout == 1 ? w8a8_plan_fn_l1() : w8a8_plan_fn_l2());
+    return SPECQ_OK;
+  }
   // Eager calls with an automatic BLOCK_M on the streaming kernels choose the token-tile depth,
   // channel block and split count together.
   const bool joint = block_m <= 0 && !plan_mode && vec == 16 && path == 0 && rows16 > 1;
@@ -412,12 +440,84 @@ W8A8Group single(const void* w, int64_t ldw, const float* sw, void* c, int64_t l
   return g;
 }
 
+// The per-16-row table of the plan-mode launch: for each step of the active M, the menu
+// tiling and split count the eager cost model prices lowest at the step's largest M (the
+// decode rule of eager calls at M <= 16), with its channel tiles counted per GEMM of the group.
+int w8a8_plan_table(int m_grid, const W8A8Group& grp, int K, W8A8Cfg* cfg) {
+  const int N = grp.n_total();
+  const double wb = cfg->layout == 2 ? 0.5 : 1.0;
+  const int R = ceil_div(std::max(m_grid, 1), 16);
+  const int ksteps = ceil_div(K, 64), kq = ceil_div(ksteps, 4);
+  size_t ws = 0;
+  int grid = 0, n_ctr = 0;
+  size_t lds = 0;
+  for (int e = 0; e < kW8A8PlanRows; ++e) {
+    const int r = e == kW8A8PlanRows - 1 ? R : std::min(e + 1, R);
+    int path = -1, s = 1;
+    if (r == 1) {
+      int sel = 3;
+      for (int c = 0; c < 3; ++c)
+        if (ceil_div(N, bn_of_sel(c)) <= device_cus()) { sel = c; break; }
+      path = sel;  // menu entries 0..3: the direct-activation tile of channel block sel
+    } else {
+      double best = 0;
+      for (int i = 0; i < kW8A8PlanMenu; ++i) {
+        for (int s_req : {1, 2, 4}) {
+          int se = 1;
+          const double t = w8a8_model_time(r, N, K, wb, kW8A8PlanMenuMt[i], kW8A8PlanMenuSel[i], s_req, &se);
+          if (t < 0) continue;
+          const bool tie = path >= 0 && std::fabs(t - best) <= 1e-9 * best;
+          if (path < 0 || (t < best && !tie) || (tie && kW8A8PlanMenuMt[i] < kW8A8PlanMenuMt[path])) {
+            best = t; path = i; s = se;
+          }
+        }
+      }
+    }
+    SPECQ_REQUIRE(path >= 0, SPECQ_ENOTSUP, "w8a8 plan: no tiling for M=%d N=%d K=%d", 16 * r, N, K);
+    const int mt = kW8A8PlanMenuMt[path], bn = bn_of_sel(kW8A8PlanMenuSel[path]);
+    W8A8PlanTile& t = cfg->plan_t[e];
+    t.path = path;
+    t.m_chunks = ceil_div(r, mt);
+    int tiles = 0;
+    for (int g = 0; g < grp.n; ++g) {
+      tiles += ceil_div(grp.N[g], bn);
+      if (g + 1 < grp.n) t.grp_tile_end[g] = tiles;
+    }
+    for (int g = grp.n - 1; g < 3; ++g) t.grp_tile_end[g] = tiles;
+    t.n_tiles = tiles;
+    s = std::min(std::max(s, 1), kq);
+    t.k_range = ceil_div(kq, s) * 4 * 64;
+    t.splits = ceil_div(K, t.k_range);
+    SPECQ_REQUIRE((int64_t)t.m_chunks * tiles <= kMaxCounters, SPECQ_ENOTSUP,
+                  "w8a8 plan: %d x %d tiles exceed the counter region", t.m_chunks, tiles);
+    if (t.splits > 1) {
+      ws = std::max(ws, align_up((size_t)t.m_chunks * tiles * t.splits * (mt * 16) * bn * 4, 256));
+      n_ctr = std::max(n_ctr, t.m_chunks * tiles);
+    }
+    grid = std::max(grid, chunked_grid(tiles * t.splits, t.m_chunks));
+    if (mt == 1) lds = std::max(lds, (size_t)(kw_of_sel(kW8A8PlanMenuSel[path]) - 1) * 16 * bn * 4);
+  }
+  const W8A8PlanTile& top = cfg->plan_t[std::min(R, kW8A8PlanRows) - 1];
+  cfg->mt = kW8A8PlanMenuMt[top.path];
+  cfg->bnsel = kW8A8PlanMenuSel[top.path];
+  cfg->bn = bn_of_sel(cfg->bnsel);
+  cfg->n_tiles = top.n_tiles; cfg->m_chunks = top.m_chunks; cfg->splits = top.splits; cfg->k_range = top.k_range;
+  cfg->ws_partials = ws;
+  cfg->ws_counters = n_ctr > 0 ? kCounterBytes : 0;
+  cfg->n_counters = n_ctr;
+  cfg->plan_grid = grid;
+  cfg->lds = lds;
+  return SPECQ_OK;
+}
+
 // Tiles of a grouped launch: chosen as for one GEMM of the members' total width, then every
 // member gets whole channel blocks of its own (its last block may be partial).
 int w8a8_group_config(int layout, int m_grid, const W8A8Group& grp, int K, int block_m, int block_n, int num_warps,
                       int split_k, int vec, bool plan_mode, W8A8Cfg* cfg) {
   int rc = w8a8_config(layout, m_grid, grp.n_total(), K, block_m, block_n, num_warps, split_k, vec, plan_mode, cfg);
-  if (rc || grp.n == 1) return rc;
+  if (rc) return rc;
+  if (cfg->family == kPlan) return w8a8_plan_table(m_grid, grp, K, cfg);
+  if (grp.n == 1) return rc;
   SPECQ_REQUIRE(cfg->family != kLegacy, SPECQ_ENOTSUP,
                 "w8a8 grouped: needs 16-byte aligned operands and K %% 16 == 0 (the streaming kernels)");
   int tiles = 0;
@@ -499,9 +599,9 @@ int run_w8a8(int layout, const int8_t* a, int64_t lda, const W8A8Group& grp, con
       p.grp_vec_store[g - 1] = vec_store(grp.c[g], grp.ldc[g], grp.sw[g]);
     }
   }
-  const int grid = chunked_grid(cfg.n_tiles * cfg.splits, cfg.m_chunks);
+  const int grid = cfg.family == kPlan ? cfg.plan_grid : chunked_grid(cfg.n_tiles * cfg.splits, cfg.m_chunks);
   if (static_scratch && need) {
-    int n_ctr = cfg.m_chunks * cfg.n_tiles;
+    int n_ctr = cfg.family == kPlan ? cfg.n_counters : cfg.m_chunks * cfg.n_tiles;
     int32_t* ctr = p.counters;
     void* zargs[] = {(void*)&ctr, (void*)&n_ctr};
     const hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&zero_i32_kernel), dim3(ceil_div(n_ctr, 256)),
@@ -510,6 +610,12 @@ int run_w8a8(int layout, const int8_t* a, int64_t lda, const W8A8Group& grp, con
       set_error("w8a8_packed_noalloc: counter clear failed: %s", hipGetErrorString(e));
       return SPECQ_EIO;
     }
+  }
+  if (cfg.family == kPlan) {
+    W8A8PlanParams pp;
+    pp.p = p;
+    for (int e = 0; e < kW8A8PlanRows; ++e) pp.t[e] = cfg.plan_t[e];
+    return launch(cfg.fn, grid, 256, cfg.lds, reinterpret_cast<hipStream_t>(stream), &pp);
   }
   return launch(cfg.fn, grid, cfg.nw * 64, cfg.lds, reinterpret_cast<hipStream_t>(stream), &p);
 }
@@ -554,13 +660,17 @@ int w8a8_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, i
   const bool plan_mode = (layout & kAttrsPlan) != 0;
   layout &= ~kAttrsPlan;
   SPECQ_REQUIRE(layout >= 0 && layout <= 2, SPECQ_EINVAL, "w8a8 attrs: layout %d", layout);
-  int rc = w8a8_config(layout, m_grid, N, K, block_m, block_n, num_warps, split_k, 16, plan_mode, &cfg);
+  int rc = w8a8_group_config(layout, m_grid, single(nullptr, 0, nullptr, nullptr, 0, N), K, block_m, block_n,
+                             num_warps, split_k, 16, plan_mode, &cfg);
   if (rc) return rc;
   hipFuncAttributes fa;
   if (hipFuncGetAttributes(&fa, cfg.fn) != hipSuccess) return fail(SPECQ_EIO, "w8a8: hipFuncGetAttributes failed");
   // The name carries the template arguments exactly as profilers print the kernel symbol.
   const int kw = cfg.bn == 16 ? 4 : (cfg.bn == 32 ? 2 : 1), rw = cfg.bn == 128 ? 2 : 1, s = 4 / kw;
-  if (cfg.family == kRk) {
+  // A plan-mode launch with automatic tiles reports its tiling for M = m_grid.
+  if (cfg.family == kPlan) {
+    snprintf(out->name, sizeof(out->name), "specq::w8a8_plan_kernel<%d>", cfg.layout);
+  } else if (cfg.family == kRk) {
     snprintf(out->name, sizeof(out->name), "specq::w8a8_rk_kernel<1, %d, %d, 4, %d>", rw, kw, cfg.layout);
   } else if (cfg.family == kWs) {
     const int nslot = w8a8_ws_nslot(cfg.mt, kw);
@@ -573,7 +683,7 @@ int w8a8_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, i
   out->lds_bytes = (int)(fa.sharedSizeBytes + cfg.lds);
   out->scratch_bytes = (int)fa.localSizeBytes;
   out->threads = cfg.nw * 64;
-  out->grid = chunked_grid(cfg.n_tiles * cfg.splits, cfg.m_chunks);
+  out->grid = cfg.family == kPlan ? cfg.plan_grid : chunked_grid(cfg.n_tiles * cfg.splits, cfg.m_chunks);
   out->block_m = cfg.mt * 16; out->block_n = cfg.bn; out->num_warps = cfg.nw; out->split_k = cfg.splits;
   return SPECQ_OK;
 }

@@ -1,0 +1,97 @@
+// Plan-mode W8A8 launch that holds several compiled tilings and picks one on the device.
+//
+// A graph captured at the largest grid replays every active M = plan[0].  No single token-tile
+// depth serves M = 1 and M = 288 alike (a 16-row direct-activation tile is fastest at decode,
+// 144-row tiles at the top of the range), and a streaming kernel's per-chunk costs are fixed
+// by its compiled depth.  So this launch inlines a menu of the library's own tilings (the RK and
+// WS kernel bodies) and takes, per 16 rows of M, a tiling chosen on the host by the same cost
+// model as eager calls: workgroup w reads M, looks up the entry of ceil(M / 16) in the
+// parameter block, and runs that tiling's body with that entry's channel tiles, M-chunks and
+// split count (workgroups past the tiling's own grid exit at once).  INT32 sums are exact, so
+// every entry gives the bit-identical result of an eager call.
+//
+// The menu (index: token-tile depth x channel block):
+//   0..3   direct-activation 16-row tile, 16 / 32 / 64 / 128 channels
+//   4..6   32-row  streaming tile, 16 / 32 / 64 channels
+//   7..9   48-row  streaming tile, 32 / 64 / 128 channels
+//   10..12 80-row  streaming tile, 32 / 64 / 128 channels
+//   13..14 144-row streaming tile, 64 / 128 channels
+// The streaming tilings share four LDS slots sized for the largest of them (two of 144 rows x
+// 256 bytes, two of 80 x 256 for the 4-slot rings of the K-splitting tiles): 112 KB.
+#pragma once
+#include "w8a8_tiles.hpp"
+
+namespace specq {
+
+constexpr int kW8A8PlanRows = 19;   // entries: M in (16 e, 16 (e + 1)]; the last also beyond
+constexpr int kW8A8PlanMenu = 15;
+// (token tiles of 16 rows, channel-width selector) of each menu entry; depth 1 = direct-activation.
+constexpr int kW8A8PlanMenuMt[kW8A8PlanMenu] = {1, 1, 1, 1, 2, 2, 2, 3, 3, 3, 5, 5, 5, 9, 9};
+constexpr int kW8A8PlanMenuSel[kW8A8PlanMenu] = {0, 1, 2, 3, 0, 1, 2, 1, 2, 3, 1, 2, 3, 2, 3};
+
+struct W8A8PlanTile {
+  int path;                           // menu index
+  int n_tiles, m_chunks, splits, k_range;
+  int grp_tile_end[3];                // grouped launches: member boundaries in this tiling's tiles
+};
+struct W8A8PlanParams {
+  W8A8Params p;
+  W8A8PlanTile t[kW8A8PlanRows];
+};
+
+template <int I, int WL, class SlotPtr>
+__device__ __forceinline__ void w8a8_plan_path(const W8A8Params& p, SlotPtr slots) {
+  constexpr int MT = kW8A8PlanMenuMt[I], SEL = kW8A8PlanMenuSel[I];
+  using B = W8A8BnSel<SEL>;
+  if constexpr (MT == 1) {
+    w8a8_rk_body<1, B::RW, B::KW, 4, WL>(p);
+  } else {
+    using P = W8A8WsPick<MT, SEL>;
+    static_assert(P::Cfg::SLOT <= 9 * 16 * 256 && (P::NSLOT <= 2 || P::Cfg::SLOT <= 5 * 16 * 256),
+                  "menu tiling fits the shared slots");
+    w8a8_ws_body<MT, B::RW, B::KW, B::S, P::NSLOT, 4, WL>(p, slots);
+  }
+}
+
+template <int WL>
+__global__ __launch_bounds__(256) void w8a8_plan_kernel(W8A8PlanParams pp) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s0[9 * 16 * 256], lds_s1[9 * 16 * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s2[5 * 16 * 256], lds_s3[5 * 16 * 256];
+  auto slots = [&](auto ic) -> uint8_t* {
+    constexpr int i = decltype(ic)::value;
+    static_assert(i < 4, "menu tilings use at most four slots");
+    if constexpr (i == 0) return lds_s0;
+    else if constexpr (i == 1) return lds_s1;
+    else if constexpr (i == 2) return lds_s2;
+    else return lds_s3;
+  };
+  int M = min(max(pp.p.plan[0], 0), pp.p.m_grid);
+  M = uniform(M);
+  const int e = uniform(min(max((M + 15) / 16, 1), kW8A8PlanRows) - 1);
+  W8A8Params p = pp.p;
+  const W8A8PlanTile& t = pp.t[e];
+  p.n_tiles = t.n_tiles; p.m_chunks = t.m_chunks; p.splits = t.splits; p.k_range = t.k_range;
+  p.grp_tile_end[0] = t.grp_tile_end[0]; p.grp_tile_end[1] = t.grp_tile_end[1]; p.grp_tile_end[2] = t.grp_tile_end[2];
+  switch (uniform(t.path)) {
+    case 0: w8a8_plan_path<0, WL>(p, slots); break;
+    case 1: w8a8_plan_path<1, WL>(p, slots); break;
+    case 2: w8a8_plan_path<2, WL>(p, slots); break;
+    case 3: w8a8_plan_path<3, WL>(p, slots); break;
+    case 4: w8a8_plan_path<4, WL>(p, slots); break;
+    case 5: w8a8_plan_path<5, WL>(p, slots); break;
+    case 6: w8a8_plan_path<6, WL>(p, slots); break;
+    case 7: w8a8_plan_path<7, WL>(p, slots); break;
+    case 8: w8a8_plan_path<8, WL>(p, slots); break;
+    case 9: w8a8_plan_path<9, WL>(p, slots); break;
+    case 10: w8a8_plan_path<10, WL>(p, slots); break;
+    case 11: w8a8_plan_path<11, WL>(p, slots); break;
+    case 12: w8a8_plan_path<12, WL>(p, slots); break;
+    case 13: w8a8_plan_path<13, WL>(p, slots); break;
+    case 14: w8a8_plan_path<14, WL>(p, slots); break;
+    default: break;
+  }
+}
+
+const void* w8a8_plan_fn(int layout);  // instantiation units
+
+}  // namespace specq

@@ -1,0 +1,8 @@
+// Instantiation of the plan-mode W8A8 launch with several tilings, weight layout 2.
+#include "w8a8_plan.hpp"
+
+namespace specq {
+
+const void* w8a8_plan_fn_l2() { return reinterpret_cast<const void*>(&w8a8_plan_kernel<2>); }
+
+}  // namespace specq

@@ -49,8 +49,10 @@ struct W8A8RkCfg {
   static constexpr int RED_BYTES = (KW - 1) * BM * BN * 4;     // one slice per non-owner wave
 };
 
+// The kernel body, also inlined into the plan-mode launch that holds several tilings
+// (w8a8_plan.hpp).
 template <int MT, int RW, int KW, int NW, int LAYOUT>
-__global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
+__device__ __forceinline__ void w8a8_rk_body(W8A8Params p) {
   using C = W8A8RkCfg<MT, RW, KW, NW>;
   constexpr int CW = C::CW, BM = C::BM, BNW = C::BNW, BN = C::BN, NS = C::NS, D = C::D, PER = C::PER;
   extern __shared__ __attribute__((aligned(16))) int32_t smem_rk[];
@@ -212,6 +214,11 @@ __global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
   }
   __shared__ int s_last_rk;
   w8a8_splitk_finish<BM, BN, NW * 64>(p, prs, cidx, m0, ltile * BN, M, &s_last_rk);
+}
+
+template <int MT, int RW, int KW, int NW, int LAYOUT>
+__global__ __launch_bounds__(NW * 64) void w8a8_rk_kernel(W8A8Params p) {
+  w8a8_rk_body<MT, RW, KW, NW, LAYOUT>(p);
 }
 
 }  // namespace specq

@@ -53,26 +53,17 @@ struct W8A8WsCfg {
                              NSLOT * SLOT + 64 <= 160 * 1024 && (KW == 1 || RED <= SLOT);
 };
 
-template <int MT, int RW, int KW, int S, int NSLOT, int NW, int WL>
-__global__ __launch_bounds__(NW * 64) void w8a8_ws_kernel(W8A8Params p) {
+// The kernel body.  `slot_ptr(std::integral_constant<int, i>)` returns activation slot i
+// (i < NSLOT, at least SLOT bytes each, 16-byte aligned).  The slots are separate LDS
+// variables: the compiler's wait-count pass can then tell that reads of one slot do not
+// depend on the DMA still filling another.  Also inlined into the plan-mode launch that holds
+// several tilings (w8a8_plan.hpp), which passes slots sized for its largest tiling.
+template <int MT, int RW, int KW, int S, int NSLOT, int NW, int WL, class SlotPtr>
+__device__ __forceinline__ void w8a8_ws_body(W8A8Params p, SlotPtr slot_ptr) {
   using C = W8A8WsCfg<MT, RW, KW, S, NSLOT, NW>;
   static_assert(C::OK, "unsupported W8A8 weight-stream tile");
   constexpr int CW = C::CW, BM = C::BM, BNW = C::BNW, BN = C::BN, KC = C::KC, A_L = C::A_L;
   constexpr int NS = C::NS, D = C::D, P = C::P, SLOT = C::SLOT;
-  // The activation slots are separate LDS variables: the compiler's wait-count pass can then
-  // tell that reads of one slot do not depend on the DMA still filling another.
-  __shared__ __attribute__((aligned(16))) uint8_t lds_s0[SLOT], lds_s1[SLOT];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_s2[NSLOT > 2 ? SLOT : 16], lds_s3[NSLOT > 3 ? SLOT : 16];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_s4[NSLOT > 4 ? SLOT : 16], lds_s5[NSLOT > 5 ? SLOT : 16];
-  auto slot_ptr = [&](auto ic) -> uint8_t* {
-    constexpr int i = decltype(ic)::value;
-    if constexpr (i == 0) return lds_s0;
-    else if constexpr (i == 1) return lds_s1;
-    else if constexpr (i == 2) return lds_s2;
-    else if constexpr (i == 3) return lds_s3;
-    else if constexpr (i == 4) return lds_s4;
-    else return lds_s5;
-  };
 
   int mc, unit;
   if (!chunked_unit(p.m_chunks, p.n_tiles * p.splits, mc, unit)) return;
@@ -325,6 +316,23 @@ __global__ __launch_bounds__(NW * 64) void w8a8_ws_kernel(W8A8Params p) {
   }
   __shared__ int s_last_ws;
   w8a8_splitk_finish<BM, BN, NW * 64>(p, prs, cidx, m0, ltile * BN, M, &s_last_ws);
+}
+
+template <int MT, int RW, int KW, int S, int NSLOT, int NW, int WL>
+__global__ __launch_bounds__(NW * 64) void w8a8_ws_kernel(W8A8Params p) {
+  constexpr int SLOT = W8A8WsCfg<MT, RW, KW, S, NSLOT, NW>::SLOT;
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s0[SLOT], lds_s1[SLOT];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s2[NSLOT > 2 ? SLOT : 16], lds_s3[NSLOT > 3 ? SLOT : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s4[NSLOT > 4 ? SLOT : 16], lds_s5[NSLOT > 5 ? SLOT : 16];
+  w8a8_ws_body<MT, RW, KW, S, NSLOT, NW, WL>(p, [&](auto ic) -> uint8_t* {
+    constexpr int i = decltype(ic)::value;
+    if constexpr (i == 0) return lds_s0;
+    else if constexpr (i == 1) return lds_s1;
+    else if constexpr (i == 2) return lds_s2;
+    else if constexpr (i == 3) return lds_s3;
+    else if constexpr (i == 4) return lds_s4;
+    else return lds_s5;
+  });
 }
 
 }  // namespace specq
