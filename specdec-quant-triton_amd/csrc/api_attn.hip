@@ -12,6 +12,9 @@ namespace specq {
 // bit must run with the same value.
 std::atomic<int> g_attn_target{0};
 
+const void* attn_plan_fn_d64(int rb_max, int fp32);   // attn_plan_d64.hip
+const void* attn_plan_fn_d128(int rb_max, int fp32);  // attn_plan_d128.hip
+
 namespace {
 
 template <int D>
@@ -122,7 +125,11 @@ extern "C" int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64
                 "paged_attn: token stride %lld of the K/V cache outside (0, 2^27)", (long long)s_ko);
   if (B_grid == 0) return SPECQ_OK;
   const int rb = ceil_div(QPP * G, 16);
-  const void* fn = attn_fn(D, rb, scale_fp32 ? 1 : 0);
+  // Plan mode with more than one row block runs the launch that sizes its programs to the
+  // active q_len on the device (the rows of a program whose queries are inactive do nothing).
+  const void* fn = plan != nullptr && rb > 1
+                       ? (D == 128 ? attn_plan_fn_d128(rb, scale_fp32 ? 1 : 0) : attn_plan_fn_d64(rb, scale_fp32 ? 1 : 0))
+                       : attn_fn(D, rb, scale_fp32 ? 1 : 0);
   SPECQ_REQUIRE(fn != nullptr, SPECQ_ENOTSUP, "paged_attn: no kernel for D=%d rows=%d", D, QPP * G);
   const int n_qc = ceil_div(plan ? ql_grid : q_len, QPP);
   if (n_qc == 0) return SPECQ_OK;

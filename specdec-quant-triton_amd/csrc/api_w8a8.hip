@@ -11,6 +11,7 @@
 // families with the same tiles.
 #include <algorithm>
 #include <atomic>
+#include <map>
 #include <mutex>
 #include <vector>
 
@@ -22,9 +23,9 @@
 namespace specq {
 
 const void* w8a8_kernel_rw1(int mt, int vec);
-const void* w8a8_plan_fn_l0();
-const void* w8a8_plan_fn_l1();
-const void* w8a8_plan_fn_l2();
+const void* w8a8_plan_fn_l0(int variant);
+const void* w8a8_plan_fn_l1(int variant);
+const void* w8a8_plan_fn_l2(int variant);
 const void* w8a8_kernel_rw2(int mt, int vec);
 const void* w8a8_kernel_rw4(int mt, int vec);
 
@@ -236,10 +237,9 @@ static_assert(W8A8BnSel<0>::KW == 4 && W8A8BnSel<1>::KW == 2 && W8A8BnSel<2>::KW
 // 16-row chunks run on the direct-activation kernel, measured fast only with 16-channel
 // blocks, no split and one round of workgroups.
 // Modelled time of one tiling (token-tile depth mt, channel block sel, requested split count)
-// of `rows16` 16-row token tiles, from the model above; negative when the tiling is not one the
-// model allows.  *s_eff is the split count after whole-chunk boundaries.
-double w8a8_model_time(int rows16, int N, int K, double wb, int mt, int sel, int s_req, int* s_eff) {
-  const int cus = device_cus();
+// of `rows16` 16-row token tiles on `cus` CUs, from the model above; negative when the tiling
+// is not one the model allows.  *s_eff is the split count after whole-chunk boundaries.
+double w8a8_model_time(int rows16, int N, int K, double wb, int mt, int sel, int s_req, int cus, int* s_eff) {
   const int ksteps = ceil_div(K, 64), kq = ceil_div(ksteps, 4);
   const int chunks = ceil_div(rows16, mt), rows = mt * 16;
   const int bn = bn_of_sel(sel);
@@ -257,6 +257,7 @@ double w8a8_model_time(int rows16, int N, int K, double wb, int mt, int sel, int
 void w8a8_auto_tiles(int M, int N, int K, double wb, int bnsel_fixed, int splits_fixed, int* mt_out, int* bnsel,
                      int* splits) {
   const int rows16 = ceil_div(std::max(M, 1), 16);
+  const int cus = device_cus();
   double best_t = 0;
   int best_mt = -1, best_sel = 2, best_s = 1, last_mt = -1;
   const int max_c = std::max(6, ceil_div(rows16, kW8A8MaxMt));  // past 6 chunks only when M needs it
@@ -269,7 +270,7 @@ void w8a8_auto_tiles(int M, int N, int K, double wb, int bnsel_fixed, int splits
       const int cand[3] = {splits_fixed > 0 ? splits_fixed : 1, 2, 4};
       for (int ci = 0; ci < (splits_fixed > 0 ? 1 : 3); ++ci) {
         int s = 1;
-        const double t = w8a8_model_time(rows16, N, K, wb, mt, sel, cand[ci], &s);
+        const double t = w8a8_model_time(rows16, N, K, wb, mt, sel, cand[ci], cus, &s);
         if (t < 0) continue;
         // Equal prices go to the shallower token tile (fewer activation rows per workgroup).
         const bool tie = best_mt >= 0 && std::fabs(t - best_t) <= 1e-9 * best_t;
@@ -298,7 +299,6 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   // active M on the device (its table is filled by w8a8_plan_table for the launch's GEMMs).
   if (plan_mode && block_m <= 0 && block_n <= 0 && split_k <= 0 && vec == 16 && path == 0) {
     cfg->family = kPlan; cfg->layout = layout; cfg->vec = vec; cfg->nw = 4; cfg->rw = 1;
-    cfg->fn = layout == 0 ? w8a8_plan_fn_l0() : (layout == 1 ? w8a8_plan_fn_l1() : w8a8_plan_fn_l2());
     return SPECQ_OK;
   }
   // Eager calls with an automatic BLOCK_M on the streaming kernels choose the token-tile depth,
@@ -444,37 +444,73 @@ W8A8Group single(const void* w, int64_t ldw, const float* sw, void* c, int64_t l
 // tiling and split count the eager cost model prices lowest at the step's largest M (the
 // decode rule of eager calls at M <= 16), with its channel tiles counted per GEMM of the group.
 int w8a8_plan_table(int m_grid, const W8A8Group& grp, int K, W8A8Cfg* cfg) {
+  // Tables are cached per (device CUs, layout, grid, K, member widths): building one prices
+  // a few thousand tilings, and plan-mode calls repeat the same shapes.
+  const int cus = device_cus();
+  struct Key {
+    int v[9];
+    bool operator<(const Key& o) const { return std::lexicographical_compare(v, v + 9, o.v, o.v + 9); }
+  };
+  Key key{{cus, cfg->layout, m_grid, K, grp.n, grp.N[0], grp.n > 1 ? grp.N[1] : 0, grp.n > 2 ? grp.N[2] : 0,
+           grp.n > 3 ? grp.N[3] : 0}};
+  static std::mutex mu;
+  static std::map<Key, W8A8Cfg> cache;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) {
+      *cfg = it->second;
+      return SPECQ_OK;
+    }
+  }
   const int N = grp.n_total();
   const double wb = cfg->layout == 2 ? 0.5 : 1.0;
   const int R = ceil_div(std::max(m_grid, 1), 16);
   const int ksteps = ceil_div(K, 64), kq = ceil_div(ksteps, 4);
+  // Menu entry and split count of each step, per launch variant, and the variant whose steps
+  // the model prices lower in total (ties to variant 0, the smaller LDS footprint).
+  int pick[2][kW8A8PlanRows], split_of[2][kW8A8PlanRows];
+  double total[2] = {0, 0};
+  for (int v = 0; v < 2; ++v) {
+    for (int e = 0; e < kW8A8PlanRows; ++e) {
+      const int r = e == kW8A8PlanRows - 1 ? R : std::min(e + 1, R);
+      int path = -1, s = 1;
+      double best = 0;
+      if (r == 1) {
+        int sel = 3;
+        for (int c = 0; c < 3; ++c)
+          if (ceil_div(N, bn_of_sel(c)) <= cus) { sel = c; break; }
+        path = sel;  // menu entries 0..3: the direct-activation tile of channel block sel
+      } else {
+        for (int i = 0; i < kW8A8PlanMenu; ++i) {
+          for (int s_req : {1, 2, 4}) {
+            int se = 1;
+            const int mt_i = kW8A8PlanMenuMt[v][i];
+            const double t = w8a8_model_time(r, N, K, wb, mt_i, kW8A8PlanMenuSel[v][i], s_req, cus, &se);
+            if (t < 0) continue;
+            const bool tie = path >= 0 && std::fabs(t - best) <= 1e-9 * best;
+            if (path < 0 || (t < best && !tie) || (tie && mt_i < kW8A8PlanMenuMt[v][path])) {
+              best = t; path = i; s = se;
+            }
+          }
+        }
+      }
+      SPECQ_REQUIRE(path >= 0, SPECQ_ENOTSUP, "w8a8 plan: no tiling for M=%d N=%d K=%d", 16 * r, N, K);
+      pick[v][e] = path;
+      split_of[v][e] = s;
+      if (e < R) total[v] += best;
+    }
+  }
+  const int v = total[1] < total[0] ? 1 : 0;
+  cfg->fn = cfg->layout == 0 ? w8a8_plan_fn_l0(v) : (cfg->layout == 1 ? w8a8_plan_fn_l1(v) : w8a8_plan_fn_l2(v));
   size_t ws = 0;
   int grid = 0, n_ctr = 0;
   size_t lds = 0;
   for (int e = 0; e < kW8A8PlanRows; ++e) {
     const int r = e == kW8A8PlanRows - 1 ? R : std::min(e + 1, R);
-    int path = -1, s = 1;
-    if (r == 1) {
-      int sel = 3;
-      for (int c = 0; c < 3; ++c)
-        if (ceil_div(N, bn_of_sel(c)) <= device_cus()) { sel = c; break; }
-      path = sel;  // menu entries 0..3: the direct-activation tile of channel block sel
-    } else {
-      double best = 0;
-      for (int i = 0; i < kW8A8PlanMenu; ++i) {
-        for (int s_req : {1, 2, 4}) {
-          int se = 1;
-          const double t = w8a8_model_time(r, N, K, wb, kW8A8PlanMenuMt[i], kW8A8PlanMenuSel[i], s_req, &se);
-          if (t < 0) continue;
-          const bool tie = path >= 0 && std::fabs(t - best) <= 1e-9 * best;
-          if (path < 0 || (t < best && !tie) || (tie && kW8A8PlanMenuMt[i] < kW8A8PlanMenuMt[path])) {
-            best = t; path = i; s = se;
-          }
-        }
-      }
-    }
-    SPECQ_REQUIRE(path >= 0, SPECQ_ENOTSUP, "w8a8 plan: no tiling for M=%d N=%d K=%d", 16 * r, N, K);
-    const int mt = kW8A8PlanMenuMt[path], bn = bn_of_sel(kW8A8PlanMenuSel[path]);
+    const int path = pick[v][e];
+    int s = split_of[v][e];
+    const int mt = kW8A8PlanMenuMt[v][path], bn = bn_of_sel(kW8A8PlanMenuSel[v][path]);
     W8A8PlanTile& t = cfg->plan_t[e];
     t.path = path;
     t.m_chunks = ceil_div(r, mt);
@@ -495,11 +531,11 @@ int w8a8_plan_table(int m_grid, const W8A8Group& grp, int K, W8A8Cfg* cfg) {
       n_ctr = std::max(n_ctr, t.m_chunks * tiles);
     }
     grid = std::max(grid, chunked_grid(tiles * t.splits, t.m_chunks));
-    if (mt == 1) lds = std::max(lds, (size_t)(kw_of_sel(kW8A8PlanMenuSel[path]) - 1) * 16 * bn * 4);
+    if (mt == 1) lds = std::max(lds, (size_t)(kw_of_sel(kW8A8PlanMenuSel[v][path]) - 1) * 16 * bn * 4);
   }
   const W8A8PlanTile& top = cfg->plan_t[std::min(R, kW8A8PlanRows) - 1];
-  cfg->mt = kW8A8PlanMenuMt[top.path];
-  cfg->bnsel = kW8A8PlanMenuSel[top.path];
+  cfg->mt = kW8A8PlanMenuMt[v][top.path];
+  cfg->bnsel = kW8A8PlanMenuSel[v][top.path];
   cfg->bn = bn_of_sel(cfg->bnsel);
   cfg->n_tiles = top.n_tiles; cfg->m_chunks = top.m_chunks; cfg->splits = top.splits; cfg->k_range = top.k_range;
   cfg->ws_partials = ws;
@@ -507,6 +543,8 @@ int w8a8_plan_table(int m_grid, const W8A8Group& grp, int K, W8A8Cfg* cfg) {
   cfg->n_counters = n_ctr;
   cfg->plan_grid = grid;
   cfg->lds = lds;
+  std::lock_guard<std::mutex> lock(mu);
+  cache[key] = *cfg;
   return SPECQ_OK;
 }
 
@@ -669,7 +707,8 @@ int w8a8_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, i
   const int kw = cfg.bn == 16 ? 4 : (cfg.bn == 32 ? 2 : 1), rw = cfg.bn == 128 ? 2 : 1, s = 4 / kw;
   // A plan-mode launch with automatic tiles reports its tiling for M = m_grid.
   if (cfg.family == kPlan) {
-    snprintf(out->name, sizeof(out->name), "specq::w8a8_plan_kernel<%d>", cfg.layout);
+    snprintf(out->name, sizeof(out->name), "specq::w8a8_plan_kernel<%d, %d>", cfg.layout,
+             cfg.fn == (cfg.layout == 0 ? w8a8_plan_fn_l0(1) : (cfg.layout == 1 ? w8a8_plan_fn_l1(1) : w8a8_plan_fn_l2(1))));
   } else if (cfg.family == kRk) {
     snprintf(out->name, sizeof(out->name), "specq::w8a8_rk_kernel<1, %d, %d, 4, %d>", rw, kw, cfg.layout);
   } else if (cfg.family == kWs) {

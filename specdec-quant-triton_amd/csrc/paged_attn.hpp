@@ -178,8 +178,20 @@ __device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-template <int D, int RB, typename ST>
-__global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) {
+// LDS bytes of one ring slot: K, V, then ks / vs (one dword per lane).
+template <int D>
+struct AttnSlot { static constexpr int value = 2 * kAttnChunk * D + 256; };
+
+// The kernel body for RB 16-row query blocks, on LDS arrays sized for RBL >= RB blocks (the
+// plan-mode launch below runs the body of the active rows' RB on arrays sized for the largest).
+template <int D, int RB, typename ST, int RBL>
+__device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&ring0)[kAttnWaves][AttnSlot<D>::value],
+                                                uint8_t (&ring1)[kAttnWaves][AttnSlot<D>::value],
+                                                uint8_t (&ring2)[kAttnWaves][AttnSlot<D>::value],
+                                                uint8_t (&ring3)[kAttnWaves][AttnSlot<D>::value],
+                                                float (&ml_lds)[kAttnWaves][2][RBL * 16],
+                                                v8h (&q_lds)[RBL][D / 32][64], int& s_last) {
+  static_assert(RB <= RBL, "LDS arrays hold the row blocks");
   constexpr int NU = D / 32;              // MFMA K-steps over the head dimension
   constexpr int ND = D / 16;              // 16-row d blocks of O^T = V bytes per lane per token
   constexpr int GR = D / 16;              // 16-byte granules per K/V row
@@ -190,22 +202,14 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
   constexpr int NT = kAttnThreads;
   constexpr int KB = kAttnChunk * D;      // K (or V) bytes per chunk
   constexpr int SC = 2 * KB;              // offset of the chunk's scale dwords in a slot
-  constexpr int SLOT = 2 * KB + 256;      // K, V, then ks / vs (one dword per lane)
+  constexpr int SLOT = AttnSlot<D>::value;
+  static_assert(SLOT == 2 * KB + 256, "slot layout");
   constexpr int NDMA = KB / 1024;         // 1 KB DMA instructions for K, and again for V
   constexpr int NVM = 2 * NDMA + 1;       // DMA instructions per chunk (K, V, scales)
   constexpr int HALF = 8 * D * 4;         // bytes of 8 fp32 O rows: one half of a merge block
   static_assert(D == 64 || D == 128, "head dim");
   static_assert(RB >= 1 && RB <= NS && HALF <= SLOT, "merge block halves fit a ring slot");
   static_assert((NS - 1) * NVM <= 63, "vmcnt range");
-  // The ring slots are separate LDS variables (see the schedule notes).
-  __shared__ __attribute__((aligned(16))) uint8_t ring0[kAttnWaves][SLOT];
-  __shared__ __attribute__((aligned(16))) uint8_t ring1[kAttnWaves][SLOT];
-  __shared__ __attribute__((aligned(16))) uint8_t ring2[kAttnWaves][SLOT];
-  __shared__ __attribute__((aligned(16))) uint8_t ring3[kAttnWaves][SLOT];
-  __shared__ float ml_lds[kAttnWaves][2][ROWS];
-  // Q fragments in MFMA B-operand order: [rb][u][lane] of 16 bytes (zero for padding rows).
-  __shared__ __attribute__((aligned(16))) v8h q_lds[RB][NU][64];
-  __shared__ int s_last;
   static_assert(NS == 4, "four ring variables");
 
   int n_seqs = p.n_seqs, q_len = p.q_len;
@@ -794,5 +798,42 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) 
   for (int it = 0; it < ITEMS; ++it)
     if (ivalid[it]) store_row4(threadIdx.x + NT * it, o[it]);
 }
+
+// The ring slots are separate LDS variables (see the schedule notes); Q fragments are staged
+// in MFMA B-operand order [rb][u][lane] of 16 bytes (zero for padding rows).
+#define SPECQ_ATTN_LDS(RBL)                                                          \
+  __shared__ __attribute__((aligned(16))) uint8_t ring0[kAttnWaves][AttnSlot<D>::value]; \
+  __shared__ __attribute__((aligned(16))) uint8_t ring1[kAttnWaves][AttnSlot<D>::value]; \
+  __shared__ __attribute__((aligned(16))) uint8_t ring2[kAttnWaves][AttnSlot<D>::value]; \
+  __shared__ __attribute__((aligned(16))) uint8_t ring3[kAttnWaves][AttnSlot<D>::value]; \
+  __shared__ float ml_lds[kAttnWaves][2][(RBL) * 16];                                 \
+  __shared__ __attribute__((aligned(16))) v8h q_lds[RBL][D / 32][64];                 \
+  __shared__ int s_last
+
+template <int D, int RB, typename ST>
+__global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) {
+  SPECQ_ATTN_LDS(RB);
+  paged_attn_body<D, RB, ST, RB>(p, ring0, ring1, ring2, ring3, ml_lds, q_lds, s_last);
+}
+
+// Plan-mode launch captured for programs of up to RBMAX row blocks: the active q_len (plan[1])
+// fixes how many rows a program holds, and the body of that many row blocks runs (a row's
+// result does not depend on the rows packed with it, so every choice is bit-identical).
+template <int D, int RBMAX, typename ST>
+__global__ __launch_bounds__(kAttnThreads) void paged_attn_plan_kernel(AttnParams p) {
+  SPECQ_ATTN_LDS(RBMAX);
+  const int q_len = min(max(p.plan[1], 0), p.ql_grid);
+  const int rb = uniform(min(max((min(q_len, p.QPP) * p.G + 15) / 16, 1), RBMAX));
+  if (rb == 1) {
+    paged_attn_body<D, 1, ST, RBMAX>(p, ring0, ring1, ring2, ring3, ml_lds, q_lds, s_last);
+  } else if (rb == 2) {
+    if constexpr (RBMAX >= 2) paged_attn_body<D, 2, ST, RBMAX>(p, ring0, ring1, ring2, ring3, ml_lds, q_lds, s_last);
+  } else if (rb == 3) {
+    if constexpr (RBMAX >= 3) paged_attn_body<D, 3, ST, RBMAX>(p, ring0, ring1, ring2, ring3, ml_lds, q_lds, s_last);
+  } else {
+    if constexpr (RBMAX >= 4) paged_attn_body<D, 4, ST, RBMAX>(p, ring0, ring1, ring2, ring3, ml_lds, q_lds, s_last);
+  }
+}
+#undef SPECQ_ATTN_LDS
 
 }  // namespace specq

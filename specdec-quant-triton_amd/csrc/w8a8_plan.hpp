@@ -10,14 +10,20 @@
 // split count (workgroups past the tiling's own grid exit at once).  INT32 sums are exact, so
 // every entry gives the bit-identical result of an eager call.
 //
-// The menu (index: token-tile depth x channel block):
-//   0..3   direct-activation 16-row tile, 16 / 32 / 64 / 128 channels
-//   4..6   32-row  streaming tile, 16 / 32 / 64 channels
-//   7..9   48-row  streaming tile, 32 / 64 / 128 channels
-//   10..12 80-row  streaming tile, 32 / 64 / 128 channels
-//   13..14 144-row streaming tile, 64 / 128 channels
-// The streaming tilings share four LDS slots sized for the largest of them (two of 144 rows x
-// 256 bytes, two of 80 x 256 for the 4-slot rings of the K-splitting tiles): 112 KB.
+// Two menus (index: token-tile depth x channel block), one launch variant each:
+//   variant 0                                   variant 1 (deep tiles, 2-slot rings only)
+//   0..3   16-row direct tile, 16/32/64/128     0..3   16-row direct tile, 16/32/64/128
+//   4..6   32-row, 16/32/64                     4      32-row, 64
+//   7..9   48-row, 32/64/128                    5..6   48-row, 64/128
+//   10..12 80-row, 32/64/128                    7..8   80-row, 64/128
+//   13..14 144-row, 64/128                      9..10  144-row, 64/128
+//                                               11..12 192-row, 64/128
+//                                               13..14 288-row, 64/128
+// The streaming tilings of a variant share four LDS slots sized for its largest tiling:
+// variant 0 two of 144 rows x 256 bytes and two of 80 x 256 (the 4-slot rings of the
+// K-splitting tiles), 112 KB; variant 1 two of 288 x 256, 144 KB.  The host takes the variant
+// whose table the cost model prices lower over the steps of M (the deep one for wide GEMMs
+// such as gate|up, whose large-M steps want one chunk of all rows).
 #pragma once
 #include "w8a8_tiles.hpp"
 
@@ -26,8 +32,12 @@ namespace specq {
 constexpr int kW8A8PlanRows = 19;   // entries: M in (16 e, 16 (e + 1)]; the last also beyond
 constexpr int kW8A8PlanMenu = 15;
 // (token tiles of 16 rows, channel-width selector) of each menu entry; depth 1 = direct-activation.
-constexpr int kW8A8PlanMenuMt[kW8A8PlanMenu] = {1, 1, 1, 1, 2, 2, 2, 3, 3, 3, 5, 5, 5, 9, 9};
-constexpr int kW8A8PlanMenuSel[kW8A8PlanMenu] = {0, 1, 2, 3, 0, 1, 2, 1, 2, 3, 1, 2, 3, 2, 3};
+constexpr int kW8A8PlanMenuMt[2][kW8A8PlanMenu] = {{1, 1, 1, 1, 2, 2, 2, 3, 3, 3, 5, 5, 5, 9, 9},
+                                                   {1, 1, 1, 1, 2, 3, 3, 5, 5, 9, 9, 12, 12, 18, 18}};
+constexpr int kW8A8PlanMenuSel[2][kW8A8PlanMenu] = {{0, 1, 2, 3, 0, 1, 2, 1, 2, 3, 1, 2, 3, 2, 3},
+                                                    {0, 1, 2, 3, 2, 2, 3, 2, 3, 2, 3, 2, 3, 2, 3}};
+constexpr int kW8A8PlanSlotA[2] = {9 * 16 * 256, 18 * 16 * 256};  // slots 0, 1
+constexpr int kW8A8PlanSlotB[2] = {5 * 16 * 256, 16};             // slots 2, 3
 
 struct W8A8PlanTile {
   int path;                           // menu index
@@ -39,24 +49,24 @@ struct W8A8PlanParams {
   W8A8PlanTile t[kW8A8PlanRows];
 };
 
-template <int I, int WL, class SlotPtr>
+template <int I, int WL, int V, class SlotPtr>
 __device__ __forceinline__ void w8a8_plan_path(const W8A8Params& p, SlotPtr slots) {
-  constexpr int MT = kW8A8PlanMenuMt[I], SEL = kW8A8PlanMenuSel[I];
+  constexpr int MT = kW8A8PlanMenuMt[V][I], SEL = kW8A8PlanMenuSel[V][I];
   using B = W8A8BnSel<SEL>;
   if constexpr (MT == 1) {
     w8a8_rk_body<1, B::RW, B::KW, 4, WL>(p);
   } else {
     using P = W8A8WsPick<MT, SEL>;
-    static_assert(P::Cfg::SLOT <= 9 * 16 * 256 && (P::NSLOT <= 2 || P::Cfg::SLOT <= 5 * 16 * 256),
+    static_assert(P::Cfg::SLOT <= kW8A8PlanSlotA[V] && (P::NSLOT <= 2 || P::Cfg::SLOT <= kW8A8PlanSlotB[V]),
                   "menu tiling fits the shared slots");
     w8a8_ws_body<MT, B::RW, B::KW, B::S, P::NSLOT, 4, WL>(p, slots);
   }
 }
 
-template <int WL>
+template <int WL, int V>
 __global__ __launch_bounds__(256) void w8a8_plan_kernel(W8A8PlanParams pp) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds_s0[9 * 16 * 256], lds_s1[9 * 16 * 256];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_s2[5 * 16 * 256], lds_s3[5 * 16 * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s0[kW8A8PlanSlotA[V]], lds_s1[kW8A8PlanSlotA[V]];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s2[kW8A8PlanSlotB[V]], lds_s3[kW8A8PlanSlotB[V]];
   auto slots = [&](auto ic) -> uint8_t* {
     constexpr int i = decltype(ic)::value;
     static_assert(i < 4, "menu tilings use at most four slots");
@@ -73,25 +83,23 @@ __global__ __launch_bounds__(256) void w8a8_plan_kernel(W8A8PlanParams pp) {
   p.n_tiles = t.n_tiles; p.m_chunks = t.m_chunks; p.splits = t.splits; p.k_range = t.k_range;
   p.grp_tile_end[0] = t.grp_tile_end[0]; p.grp_tile_end[1] = t.grp_tile_end[1]; p.grp_tile_end[2] = t.grp_tile_end[2];
   switch (uniform(t.path)) {
-    case 0: w8a8_plan_path<0, WL>(p, slots); break;
-    case 1: w8a8_plan_path<1, WL>(p, slots); break;
-    case 2: w8a8_plan_path<2, WL>(p, slots); break;
-    case 3: w8a8_plan_path<3, WL>(p, slots); break;
-    case 4: w8a8_plan_path<4, WL>(p, slots); break;
-    case 5: w8a8_plan_path<5, WL>(p, slots); break;
-    case 6: w8a8_plan_path<6, WL>(p, slots); break;
-    case 7: w8a8_plan_path<7, WL>(p, slots); break;
-    case 8: w8a8_plan_path<8, WL>(p, slots); break;
-    case 9: w8a8_plan_path<9, WL>(p, slots); break;
-    case 10: w8a8_plan_path<10, WL>(p, slots); break;
-    case 11: w8a8_plan_path<11, WL>(p, slots); break;
-    case 12: w8a8_plan_path<12, WL>(p, slots); break;
-    case 13: w8a8_plan_path<13, WL>(p, slots); break;
-    case 14: w8a8_plan_path<14, WL>(p, slots); break;
+    case 0: w8a8_plan_path<0, WL, V>(p, slots); break;
+    case 1: w8a8_plan_path<1, WL, V>(p, slots); break;
+    case 2: w8a8_plan_path<2, WL, V>(p, slots); break;
+    case 3: w8a8_plan_path<3, WL, V>(p, slots); break;
+    case 4: w8a8_plan_path<4, WL, V>(p, slots); break;
+    case 5: w8a8_plan_path<5, WL, V>(p, slots); break;
+    case 6: w8a8_plan_path<6, WL, V>(p, slots); break;
+    case 7: w8a8_plan_path<7, WL, V>(p, slots); break;
+    case 8: w8a8_plan_path<8, WL, V>(p, slots); break;
+    case 9: w8a8_plan_path<9, WL, V>(p, slots); break;
+    case 10: w8a8_plan_path<10, WL, V>(p, slots); break;
+    case 11: w8a8_plan_path<11, WL, V>(p, slots); break;
+    case 12: w8a8_plan_path<12, WL, V>(p, slots); break;
+    case 13: w8a8_plan_path<13, WL, V>(p, slots); break;
+    case 14: w8a8_plan_path<14, WL, V>(p, slots); break;
     default: break;
   }
 }
-
-const void* w8a8_plan_fn(int layout);  // instantiation units
 
 }  // namespace specq

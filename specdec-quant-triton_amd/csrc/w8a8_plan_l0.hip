@@ -3,6 +3,9 @@
 
 namespace specq {
 
-const void* w8a8_plan_fn_l0() { return reinterpret_cast<const void*>(&w8a8_plan_kernel<0>); }
+const void* w8a8_plan_fn_l0(int variant) {
+  return variant ? reinterpret_cast<const void*>(&w8a8_plan_kernel<0, 1>)
+                 : reinterpret_cast<const void*>(&w8a8_plan_kernel<0, 0>);
+}
 
 }  // namespace specq

@@ -3,6 +3,9 @@
 
 namespace specq {
 
-const void* w8a8_plan_fn_l1() { return reinterpret_cast<const void*>(&w8a8_plan_kernel<1>); }
+const void* w8a8_plan_fn_l1(int variant) {
+  return variant ? reinterpret_cast<const void*>(&w8a8_plan_kernel<1, 1>)
+                 : reinterpret_cast<const void*>(&w8a8_plan_kernel<1, 0>);
+}
 
 }  // namespace specq

@@ -3,6 +3,9 @@
 
 namespace specq {
 
-const void* w8a8_plan_fn_l2() { return reinterpret_cast<const void*>(&w8a8_plan_kernel<2>); }
+const void* w8a8_plan_fn_l2(int variant) {
+  return variant ? reinterpret_cast<const void*>(&w8a8_plan_kernel<2, 1>)
+                 : reinterpret_cast<const void*>(&w8a8_plan_kernel<2, 0>);
+}
 
 }  // namespace specq

@@ -21,20 +21,21 @@ class Plan:
         self.tiles = None
         self.dev = torch.zeros(8, dtype=torch.int32, device=device)
         self._host = [torch.zeros(8, dtype=torch.int32).pin_memory() for _ in range(self.SLOTS)]
-        self._done = [None] * self.SLOTS
+        self._host_np = [h.numpy() for h in self._host]  # views of the pinned slots (cheap writes)
+        self._done = [torch.cuda.Event() for _ in range(self.SLOTS)]
+        self._used = [False] * self.SLOTS
         self._i = 0
 
     def set(self, B: int, q_len: int) -> None:
         i = self._i
         self._i = (i + 1) % self.SLOTS
-        if self._done[i] is not None:
+        if self._used[i]:
             self._done[i].synchronize()  # the copy that last read this slot has completed
-        h = self._host[i]
+        h = self._host_np[i]
         h[0], h[1], h[2] = B * q_len, B, q_len
-        self.dev.copy_(h, non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record()
-        self._done[i] = ev
+        self.dev.copy_(self._host[i], non_blocking=True)
+        self._done[i].record()
+        self._used[i] = True
 
     @property
     def gemm(self) -> torch.Tensor:

@@ -3,7 +3,7 @@ active M on the device (w8a8_plan.hpp).
 
 A graph captured at M_MAX = 288 must give, for every active M, the bit-identical rows of an
 eager call and leave rows >= M untouched (bench_graphs.py:144-159, correctness.py:50-65).  The
-tiling changes with M (direct-activation tiles at M <= 16, 32- to 144-row streaming tiles above,
+tiling changes with M (direct-activation tiles at M <= 16, 32- to 288-row streaming tiles above,
 split-K where the cost model picks it), so every M = 0..288 is checked on the config-1 shapes,
 on packed INT8, row-major and packed INT4 (W4A8) weights, single and grouped, in eager calls
 and in one captured graph replayed over changing plans.
@@ -45,7 +45,7 @@ def test_plan_table_reports_a_tiling_per_step():
         rows = []
         for r in range(1, M_MAX // 16 + 1):
             cf = K.KernelInfo(0, 1 | 16, 16 * r, N, Kd, 0, 0, 4, 0).config
-            assert cf["block_m"] in (16, 32, 48, 80, 144) and cf["block_n"] in (16, 32, 64, 128)
+            assert cf["block_m"] in (16, 32, 48, 80, 144, 192, 288) and cf["block_n"] in (16, 32, 64, 128)
             rows.append((cf["block_m"], cf["block_n"], cf["split_k"]))
         note(f"plan tiles {name}: " + " ".join(f"{16 * (i + 1)}:{t}" for i, t in enumerate(rows)))
         assert rows[0][0] == 16, f"{name}: M <= 16 runs the direct-activation tile"
