@@ -476,6 +476,7 @@ int w8a8_plan_table(int m_grid, const W8A8Group& grp, int K, W8A8Cfg* cfg) {
       const int r = e == kW8A8PlanRows - 1 ? R : std::min(e + 1, R);
       int path = -1, s = 1;
       double best = 0;
+      int64_t best_wgs = 0;
       if (r == 1) {
         int sel = 3;
         for (int c = 0; c < 3; ++c)
@@ -488,9 +489,13 @@ int w8a8_plan_table(int m_grid, const W8A8Group& grp, int K, W8A8Cfg* cfg) {
             const int mt_i = kW8A8PlanMenuMt[v][i];
             const double t = w8a8_model_time(r, N, K, wb, mt_i, kW8A8PlanMenuSel[v][i], s_req, cus, &se);
             if (t < 0) continue;
+            // Equal prices go to fewer workgroups (a plan-mode launch holds one workgroup per CU,
+            // so every round counts), then to the shallower token tile.
+            const int64_t wgs = (int64_t)ceil_div(N, bn_of_sel(kW8A8PlanMenuSel[v][i])) * se * ceil_div(r, mt_i);
             const bool tie = path >= 0 && std::fabs(t - best) <= 1e-9 * best;
-            if (path < 0 || (t < best && !tie) || (tie && mt_i < kW8A8PlanMenuMt[v][path])) {
-              best = t; path = i; s = se;
+            if (path < 0 || (t < best && !tie) ||
+                (tie && (wgs < best_wgs || (wgs == best_wgs && mt_i < kW8A8PlanMenuMt[v][path])))) {
+              best = t; path = i; s = se; best_wgs = wgs;
             }
           }
         }

@@ -13,12 +13,16 @@
 // Two menus (index: token-tile depth x channel block), one launch variant each:
 //   variant 0                                   variant 1 (deep tiles, 2-slot rings only)
 //   0..3   16-row direct tile, 16/32/64/128     0..3   16-row direct tile, 16/32/64/128
-//   4..6   32-row, 16/32/64                     4      32-row, 64
-//   7..9   48-row, 32/64/128                    5..6   48-row, 64/128
-//   10..12 80-row, 32/64/128                    7..8   80-row, 64/128
-//   13..14 144-row, 64/128                      9..10  144-row, 64/128
-//                                               11..12 192-row, 64/128
-//                                               13..14 288-row, 64/128
+//   4..7   32-row, 16/32/64/128                 4..5   32-row, 64/128
+//   8..10  48-row, 32/64/128                    6..7   48-row, 64/128
+//   11..12 64-row, 64/128                       8..9   64-row, 64/128
+//   13..15 80-row, 32/64/128                    10..11 80-row, 64/128
+//   16..17 144-row, 64/128                      12..13 144-row, 64/128
+//                                               14     160-row, 128
+//                                               15..16 192-row, 64/128
+//                                               17     224-row, 128
+//                                               18     256-row, 128
+//                                               19..20 288-row, 64/128
 // The streaming tilings of a variant share four LDS slots sized for its largest tiling:
 // variant 0 two of 144 rows x 256 bytes and two of 80 x 256 (the 4-slot rings of the
 // K-splitting tiles), 112 KB; variant 1 two of 288 x 256, 144 KB.  The host takes the variant
@@ -30,12 +34,14 @@
 namespace specq {
 
 constexpr int kW8A8PlanRows = 19;   // entries: M in (16 e, 16 (e + 1)]; the last also beyond
-constexpr int kW8A8PlanMenu = 15;
+constexpr int kW8A8PlanMenu = 21;  // entries of the longer menu; variant 0 repeats its last
 // (token tiles of 16 rows, channel-width selector) of each menu entry; depth 1 = direct-activation.
-constexpr int kW8A8PlanMenuMt[2][kW8A8PlanMenu] = {{1, 1, 1, 1, 2, 2, 2, 3, 3, 3, 5, 5, 5, 9, 9},
-                                                   {1, 1, 1, 1, 2, 3, 3, 5, 5, 9, 9, 12, 12, 18, 18}};
-constexpr int kW8A8PlanMenuSel[2][kW8A8PlanMenu] = {{0, 1, 2, 3, 0, 1, 2, 1, 2, 3, 1, 2, 3, 2, 3},
-                                                    {0, 1, 2, 3, 2, 2, 3, 2, 3, 2, 3, 2, 3, 2, 3}};
+constexpr int kW8A8PlanMenuMt[2][kW8A8PlanMenu] = {
+    {1, 1, 1, 1, 2, 2, 2, 2, 3, 3, 3, 4, 4, 5, 5, 5, 9, 9, 9, 9, 9},
+    {1, 1, 1, 1, 2, 2, 3, 3, 4, 4, 5, 5, 9, 9, 10, 12, 12, 14, 16, 18, 18}};
+constexpr int kW8A8PlanMenuSel[2][kW8A8PlanMenu] = {
+    {0, 1, 2, 3, 0, 1, 2, 3, 1, 2, 3, 2, 3, 1, 2, 3, 2, 3, 3, 3, 3},
+    {0, 1, 2, 3, 2, 3, 2, 3, 2, 3, 2, 3, 2, 3, 3, 2, 3, 3, 3, 2, 3}};
 constexpr int kW8A8PlanSlotA[2] = {9 * 16 * 256, 18 * 16 * 256};  // slots 0, 1
 constexpr int kW8A8PlanSlotB[2] = {5 * 16 * 256, 16};             // slots 2, 3
 
@@ -98,6 +104,12 @@ __global__ __launch_bounds__(256) void w8a8_plan_kernel(W8A8PlanParams pp) {
     case 12: w8a8_plan_path<12, WL, V>(p, slots); break;
     case 13: w8a8_plan_path<13, WL, V>(p, slots); break;
     case 14: w8a8_plan_path<14, WL, V>(p, slots); break;
+    case 15: w8a8_plan_path<15, WL, V>(p, slots); break;
+    case 16: w8a8_plan_path<16, WL, V>(p, slots); break;
+    case 17: w8a8_plan_path<17, WL, V>(p, slots); break;
+    case 18: w8a8_plan_path<18, WL, V>(p, slots); break;
+    case 19: w8a8_plan_path<19, WL, V>(p, slots); break;
+    case 20: w8a8_plan_path<20, WL, V>(p, slots); break;
     default: break;
   }
 }

@@ -45,7 +45,8 @@ def test_plan_table_reports_a_tiling_per_step():
         rows = []
         for r in range(1, M_MAX // 16 + 1):
             cf = K.KernelInfo(0, 1 | 16, 16 * r, N, Kd, 0, 0, 4, 0).config
-            assert cf["block_m"] in (16, 32, 48, 80, 144, 192, 288) and cf["block_n"] in (16, 32, 64, 128)
+            assert cf["block_m"] in (16, 32, 48, 64, 80, 144, 160, 192, 224, 256, 288)
+            assert cf["block_n"] in (16, 32, 64, 128)
             rows.append((cf["block_m"], cf["block_n"], cf["split_k"]))
         note(f"plan tiles {name}: " + " ".join(f"{16 * (i + 1)}:{t}" for i, t in enumerate(rows)))
         assert rows[0][0] == 16, f"{name}: M <= 16 runs the direct-activation tile"
