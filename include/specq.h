@@ -61,7 +61,11 @@ const char* specq_last_error(void);
  *   grid_m_max  rows the grid is sized for (>= M); 0 means M.  The reference's grid_m_max.
  *   plan     NULL, or device int32*: plan[0] = active M (kernels.py:35-38)
  *   block_m  token rows per workgroup: a multiple of 16, at most 304 (the reference's
- *            BLOCK_M; 16/32/64/128 are its values); 0 = one chunk covering M.
+ *            BLOCK_M; 16/32/64/128 are its values); 0 = automatic.  Eager calls then take
+ *            the token-tile depth, channel block and split count from a cost model fitted to
+ *            measured latencies; calls with a plan and block_n = split_k = 0 launch a kernel
+ *            that holds a menu of tilings and runs, on the device, the one the model chose
+ *            for each 16 rows of the active M (plan[0]).  Every tiling gives the same result.
  *   block_n  output channels per workgroup: 16, 32, 64 or 128; 0 = auto (chosen with split_k
  *            from M, N and K by a cost model fitted to measured latencies).  (BLOCK_N)
  *   num_warps  waves per workgroup of the byte-granular fallback kernel (unaligned operands):
@@ -231,7 +235,9 @@ int specq_w4a16_pack_weight(const void* wq, int64_t ldq, int wq_layout, int N, i
  *   A sequence's KV range is cut into splits of whole 128-token units, their length chosen
  *   from the block table's capacity and the number of active (sequence, KV head) pairs, so a
  *   QPP=1 and a fused call, and an eager and a plan-mode call, cut a sequence at the same
- *   tokens and give bit-identical results.
+ *   tokens and give bit-identical results.  In plan mode the workgroups are sized on the
+ *   device to the active counts: the split count of the active sequences, and programs of
+ *   only as many 16-row blocks as the active q_len fills.
  * ------------------------------------------------------------------------------------- */
 size_t specq_paged_attn_workspace_size(int B_grid, int H, int H_KV, int ql_grid, int QPP,
                                        int max_pages, int PAGE);
@@ -294,7 +300,8 @@ int specq_silu_mul_quant_int8(const void* gate, int64_t ld_gate, const void* up,
  * kind: 0 = W8A8 (weight layout in `variant`: 0 row-major, 1 packed, 2 the packed INT4 weight
  * of W4A8), 1 = W4A16 (layout in
  * `variant`), 2 = paged attention (D in `variant`, | 1 << 16 for fp32 K/V scales).  For the GEMMs, `variant` | 16 describes a
- * call made with a plan (m_grid is then grid_m_max).
+ * call made with a plan (m_grid is then grid_m_max); a W8A8 plan-mode call with automatic
+ * tiles reports the tiling it runs when the active M is m_grid.
  * ------------------------------------------------------------------------------------- */
 typedef struct specq_kernel_attrs {
   char name[160];          /* kernel symbol */
