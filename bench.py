@@ -451,7 +451,11 @@ def bench_plan_graph(args, K, torch):
 
     def rows_computed(Mg, M, plan_mode, grid_tiles=False):
         """Token rows the qkv GEMM computes for active M on a grid of Mg rows (the tile the
-        library resolves for that call; plan-mode chunks past M exit without computing)."""
+        library resolves for that call; plan-mode chunks past M exit without computing).  A
+        plan-mode call with automatic tiles runs the tiling of M's 16-row step, which is the
+        one reported for a grid of that step's rows."""
+        if plan_mode and not grid_tiles:
+            Mg = min(Mg, 16 * -(-max(M, 1) // 16))
         bm = K.KernelInfo(0, 1 | (16 if plan_mode and not grid_tiles else 0), Mg, QKV, HID, 0, 0, 4, 0).config["block_m"]
         return bm * -(-M // bm) if plan_mode else bm * -(-Mg // bm)
 
