@@ -95,3 +95,25 @@ def test_noalloc_refuses_calls_beyond_the_scratch():
     torch.cuda.synchronize()
     assert rc == -28 and "static scratch" in _lib.lib().specq_last_error().decode()
     assert bool((out == 7.0).all())
+
+
+def test_noalloc_plan_mode_automatic_tiles():
+    # A plan-mode call with automatic tiles (the launch that runs, per 16 rows of the active M,
+    # its own tiling): the static scratch serves every step's split-K tiling, rows >= M untouched.
+    N, Kd, M_MAX = 4096, 14336, 288
+    a, w, sa, sw = (t.to(DEV) for t in gen.w8a8_inputs(M_MAX, N, Kd, seed=6))
+    wp = K.pack_weight_int8(w)
+    ref, _ = K.w8a8_matmul(a, sa, wp, sw, BLOCK_M=None)
+    plan = torch.zeros(8, dtype=torch.int32, device=DEV)
+    L = _lib.lib()
+    for M in (72, 8, 288, 144, 1, 200):
+        note(f"noalloc plan M={M}")
+        plan[0] = M
+        o = torch.full((M_MAX, N), 7.0, dtype=torch.float16, device=DEV)
+        rc = L.specq_w8a8_packed_noalloc(a.data_ptr(), a.stride(0), wp.data.data_ptr(), sa.data_ptr(), sw.data_ptr(),
+                                         o.data_ptr(), o.stride(0), M_MAX, N, Kd, M_MAX, plan.data_ptr(), 0, 0, 4, 0,
+                                         _stream())
+        assert rc == 0, L.specq_last_error().decode()
+        torch.cuda.synchronize()
+        assert torch.equal(o[:M], ref[:M]), f"noalloc plan mode differs from eager at M={M}"
+        assert bool((o[M:] == 7.0).all()), f"noalloc plan mode wrote rows >= M at M={M}"
