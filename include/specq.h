@@ -186,7 +186,9 @@ int specq_set_option(const char* name, int value);
  *   sc       fp16 [N, K/group] group scales, row stride ld_sc
  *   group    K group size: a power of two, a multiple of 32 (layouts 1, 2) or 16 (layout 0),
  *            dividing K.  K must be a multiple of 128.
- *   block_m  token rows per tile, a multiple of 16 up to 256 (0 = automatic);
+ *   block_m  token rows per tile, a multiple of 16 up to 256 (0 = automatic; with a plan
+ *            and block_n = 0 the launch holds a menu of tilings and runs, for each 16 rows
+ *            of the active M, the one the eager cost model picks there);
  *   block_n  64 or 128 channels per workgroup (0 = automatic); num_warps is ignored (4).
  *   Other arguments as specq_w8a8.  The fp32 accumulation order depends only on (N, K),
  *   split_k (0 = automatic, chosen from N and K) and whether the layout is the reference one:
@@ -300,7 +302,7 @@ int specq_silu_mul_quant_int8(const void* gate, int64_t ld_gate, const void* up,
  * kind: 0 = W8A8 (weight layout in `variant`: 0 row-major, 1 packed, 2 the packed INT4 weight
  * of W4A8), 1 = W4A16 (layout in
  * `variant`), 2 = paged attention (D in `variant`, | 1 << 16 for fp32 K/V scales).  For the GEMMs, `variant` | 16 describes a
- * call made with a plan (m_grid is then grid_m_max); a W8A8 plan-mode call with automatic
+ * call made with a plan (m_grid is then grid_m_max); a plan-mode GEMM call with automatic
  * tiles reports the tiling it runs when the active M is m_grid.
  * ------------------------------------------------------------------------------------- */
 typedef struct specq_kernel_attrs {

@@ -6,11 +6,19 @@
 //   RK  register-stream kernel (w4a16_rk.hpp) for 16- and 32-row token tiles (w4a16_path 1).
 #include <algorithm>
 #include <atomic>
+#include <cmath>
+#include <map>
+#include <mutex>
 
 #include "api_common.hpp"
+#include "w4a16_plan.hpp"
 #include "w4a16_tiles.hpp"
 
 namespace specq {
+
+const void* w4a16_plan_fn_l0();  // w4a16_plan_l*.hip
+const void* w4a16_plan_fn_l1();
+const void* w4a16_plan_fn_l2();
 
 // Packs a W4A16 weight (layout 0 or 1, row stride ldq bytes) into 1 KB MFMA fragments:
 // fragment (b, t) of K block b and 16-row tile t at (b * ntiles + t) KB; lane l's 16 bytes hold
@@ -51,12 +59,15 @@ std::atomic<int> g_w4a16_path{0};
 
 namespace {
 
-enum W4Family { kW4Rk = 1, kW4Ws = 2 };
+// kW4Plan: plan-mode launch holding the menu of LDS-staged tilings (w4a16_plan.hpp), one per
+// 16 rows of the active M.
+enum W4Family { kW4Rk = 1, kW4Ws = 2, kW4Plan = 3 };
 
 struct W4Cfg {
   int family, layout, mt, rw, splits, bps, n_tiles, m_chunks, units, grid, nblocks;
   size_t ws_partials, ws_counters;
   const void* fn;
+  W4PlanTile plan_t[kW4PlanRows];  // kW4Plan: the tiling of each 16-row step of M
 };
 
 // Split count: a function of (N, K) only (or the caller's split_k), so the fp32 summation
@@ -84,6 +95,18 @@ int w4_auto_splits(int N, int nblocks) {
 //   weights at 7 TB/s, plus 2 us.
 // The split count is the caller's or w4_auto_splits(N, K), so the summation order, and with it
 // every result, is the same for every tile.
+// Modelled time of one tiling (token-tile depth mt, rw 64-channel fragments) of `rows16` token
+// tiles with `splits` K splits on `cus` CUs, from the model above.
+double w4_model_time(int rows16, int N, int K, int splits, int mt, int rw, int cus) {
+  const int chunks = ceil_div(rows16, mt), rows = mt * 16;
+  const int bn = 64 * rw;
+  const double rounds = (double)ceil_div(ceil_div(N, bn) * splits * chunks, cus);
+  const double kk = (double)K / splits;
+  const double t_in = rounds * (bn * 0.5 + rows * 2.0) * kk / 60e3;
+  const double t_work = rounds * (bn * kk * 8e-6 + (double)rows * bn * kk * 4e-7);
+  return std::max(std::max(t_in, t_work), (double)N * K * 0.5 / 7e6) + 2.0;
+}
+
 void w4_auto_tiles(int M, int N, int K, int splits, int rw_fixed, int* mt_out, int* rw_out) {
   const int cus = device_cus();
   const int rows16 = ceil_div(std::max(M, 1), 16);
@@ -96,20 +119,89 @@ void w4_auto_tiles(int M, int N, int K, int splits, int rw_fixed, int* mt_out, i
     const int mt = ceil_div(rows16, c);
     if (mt == last_mt || mt > kMaxAutoMt) continue;
     last_mt = mt;
-    const int chunks = ceil_div(rows16, mt), rows = mt * 16;
     for (int rw = 1; rw <= 2; ++rw) {
       if (rw_fixed > 0 && rw != rw_fixed) continue;
-      const int bn = 64 * rw;
-      const double rounds = (double)ceil_div(ceil_div(N, bn) * splits * chunks, cus);
-      const double kk = (double)K / splits;
-      const double t_in = rounds * (bn * 0.5 + rows * 2.0) * kk / 60e3;
-      const double t_work = rounds * (bn * kk * 8e-6 + (double)rows * bn * kk * 4e-7);
-      const double t = std::max(std::max(t_in, t_work), (double)N * K * 0.5 / 7e6) + 2.0;
+      const double t = w4_model_time(rows16, N, K, splits, mt, rw, cus);
       if (best_mt < 0 || t < best_t) { best_t = t; best_mt = mt; best_rw = rw; }
     }
   }
   *mt_out = best_mt;
   *rw_out = best_rw;
+}
+
+// Plan-mode calls with automatic tiles: the per-16-row table of w4a16_plan_kernel, each step's
+// menu tiling priced lowest by the eager model at the step's largest M (the decode rule at
+// M <= 16), every entry with the split count of (N, K).  Equal prices go to fewer workgroups,
+// then to the shallower tile.  Tables are cached per shape.
+int w4_plan_config(int layout, int m_grid, int N, int K, int split_k, W4Cfg* cfg) {
+  const int cus = device_cus();
+  struct Key {
+    int v[6];
+    bool operator<(const Key& o) const { return std::lexicographical_compare(v, v + 6, o.v, o.v + 6); }
+  };
+  const Key key{{cus, layout, m_grid, N, K, split_k}};
+  static std::mutex mu;
+  static std::map<Key, W4Cfg> cache;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) {
+      *cfg = it->second;
+      return SPECQ_OK;
+    }
+  }
+  const int R = ceil_div(std::max(m_grid, 1), 16);
+  cfg->family = kW4Plan; cfg->layout = layout;
+  cfg->nblocks = K / 128;
+  int splits = split_k > 0 ? split_k : w4_auto_splits(N, cfg->nblocks);
+  if (splits > cfg->nblocks) splits = cfg->nblocks;
+  cfg->bps = ceil_div(cfg->nblocks, splits);
+  cfg->splits = ceil_div(cfg->nblocks, cfg->bps);
+  size_t ws = 0;
+  int grid = 0;
+  for (int e = 0; e < kW4PlanRows; ++e) {
+    const int r = e == kW4PlanRows - 1 ? R : std::min(e + 1, R);
+    int path = -1;
+    if (r == 1) {
+      path = ceil_div(N, 64) > cus ? 1 : 0;  // 16-row tile; 128 channels keep wide N to one round
+    } else {
+      double best = 0;
+      int64_t best_wgs = 0;
+      for (int i = 0; i < kW4PlanMenu; ++i) {
+        const int mt = kW4PlanMenuMt[i], rw = kW4PlanMenuRw[i];
+        const double t = w4_model_time(r, N, K, cfg->splits, mt, rw, cus);
+        const int64_t wgs = (int64_t)ceil_div(N, 64 * rw) * cfg->splits * ceil_div(r, mt);
+        const bool tie = path >= 0 && std::fabs(t - best) <= 1e-9 * best;
+        if (path < 0 || (t < best && !tie) ||
+            (tie && (wgs < best_wgs || (wgs == best_wgs && mt < kW4PlanMenuMt[path])))) {
+          best = t; path = i; best_wgs = wgs;
+        }
+      }
+    }
+    const int mt = kW4PlanMenuMt[path], rw = kW4PlanMenuRw[path];
+    W4PlanTile& t = cfg->plan_t[e];
+    t.path = path;
+    t.n_tiles = ceil_div(N, 64 * rw);
+    t.m_chunks = ceil_div(r, mt);
+    SPECQ_REQUIRE((int64_t)t.m_chunks * t.n_tiles <= kMaxCounters, SPECQ_ENOTSUP,
+                  "w4a16 plan: %d x %d tiles exceed the counter region", t.m_chunks, t.n_tiles);
+    if (cfg->splits > 1)
+      ws = std::max(ws, align_up((size_t)t.m_chunks * t.n_tiles * cfg->splits * (mt * 16) * (64 * rw) * 4, 256));
+    grid = std::max(grid, chunked_grid(t.n_tiles * cfg->splits, t.m_chunks));
+  }
+  const W4PlanTile& top = cfg->plan_t[std::min(R, kW4PlanRows) - 1];
+  cfg->mt = kW4PlanMenuMt[top.path];
+  cfg->rw = kW4PlanMenuRw[top.path];
+  cfg->n_tiles = top.n_tiles;
+  cfg->m_chunks = top.m_chunks;
+  cfg->units = cfg->n_tiles * cfg->splits;
+  cfg->grid = grid;
+  cfg->ws_partials = ws;
+  cfg->ws_counters = cfg->splits > 1 ? kCounterBytes : 0;
+  cfg->fn = layout == 0 ? w4a16_plan_fn_l0() : (layout == 1 ? w4a16_plan_fn_l1() : w4a16_plan_fn_l2());
+  std::lock_guard<std::mutex> lock(mu);
+  cache[key] = *cfg;
+  return SPECQ_OK;
 }
 
 int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, int split_k, bool plan_mode,
@@ -118,6 +210,8 @@ int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, in
   SPECQ_REQUIRE(m_grid >= 0 && N > 0 && K > 0, SPECQ_EINVAL, "w4a16: bad sizes M=%d N=%d K=%d", m_grid, N, K);
   SPECQ_REQUIRE(K % 128 == 0, SPECQ_ENOTSUP, "w4a16: K=%d must be a multiple of 128", K);
   const int rows16 = ceil_div(m_grid > 0 ? m_grid : 1, 16);
+  if (plan_mode && block_m <= 0 && block_n <= 0 && g_w4a16_path.load() == 0)
+    return w4_plan_config(layout, m_grid, N, K, split_k, cfg);
   int mt;
   if (block_m > 0) {
     SPECQ_REQUIRE(block_m % 16 == 0 && block_m <= 16 * kW4MaxMt, SPECQ_ENOTSUP,
@@ -206,7 +300,9 @@ int w4a16_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   hipFuncAttributes fa;
   if (hipFuncGetAttributes(&fa, cfg.fn) != hipSuccess) return fail(SPECQ_EIO, "w4a16: hipFuncGetAttributes failed");
   // The name carries the template arguments exactly as profilers print the kernel symbol.
-  if (cfg.family == kW4Rk)
+  if (cfg.family == kW4Plan)
+    snprintf(out->name, sizeof(out->name), "specq::w4a16_plan_kernel<%d>", layout);
+  else if (cfg.family == kW4Rk)
     snprintf(out->name, sizeof(out->name), "specq::w4a16_rk_kernel<%d, %d, %d>", cfg.mt, cfg.rw, layout);
   else {
     int s = 0, nslot = 0, nsw = 0;
@@ -274,6 +370,12 @@ extern "C" int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t l
   p.counters = need ? (int32_t*)workspace : nullptr;
   p.partials = need ? (float*)((char*)workspace + kCounterBytes) : nullptr;
   p.vec_store = ((uintptr_t)c % 8 == 0) && (ldc % 4 == 0);
+  if (cfg.family == kW4Plan) {
+    W4PlanParams pp;
+    pp.p = p;
+    for (int e = 0; e < kW4PlanRows; ++e) pp.t[e] = cfg.plan_t[e];
+    return launch(cfg.fn, cfg.grid, 256, 0, (hipStream_t)stream, &pp);
+  }
   return launch(cfg.fn, cfg.grid, 256, 0, (hipStream_t)stream, &p);
 }
 

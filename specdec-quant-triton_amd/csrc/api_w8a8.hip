@@ -11,6 +11,7 @@
 // families with the same tiles.
 #include <algorithm>
 #include <atomic>
+#include <cmath>
 #include <map>
 #include <mutex>
 #include <vector>

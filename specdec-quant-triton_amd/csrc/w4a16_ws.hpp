@@ -40,26 +40,17 @@ struct W4WsCfg {
                              wait_w(0) <= 63 && P * S * WPER + P * A_L <= 63 && NSLOT * SLOT <= 160 * 1024;
 };
 
-template <int MT, int RW, int S, int NSLOT, int NSW, int LAYOUT>
-__global__ __launch_bounds__(256) void w4a16_ws_kernel(W4A16Params p) {
+// The kernel body.  `slot_ptr(std::integral_constant<int, i>)` returns activation slot i
+// (i < NSLOT, at least SLOT bytes each, 16-byte aligned).  Separate LDS variables per slot:
+// the compiler's wait-count pass can then tell that reads of one slot do not depend on the DMA
+// still filling another.  Also inlined into the plan-mode launch that holds several tilings
+// (w4a16_plan.hpp), which passes slots sized for its largest tiling.
+template <int MT, int RW, int S, int NSLOT, int NSW, int LAYOUT, class SlotPtr>
+__device__ __forceinline__ void w4a16_ws_body(W4A16Params p, SlotPtr slot_ptr) {
   using C = W4WsCfg<MT, RW, S, NSLOT, NSW, LAYOUT>;
   static_assert(C::OK, "unsupported W4A16 weight-stream tile");
   constexpr int BM = C::BM, BNW = C::BNW, BN = C::BN, A_L = C::A_L, NS = C::NS, D = C::D, P = C::P;
-  constexpr int SLOT = C::SLOT, WPER = C::WPER, NSC = C::NSC;
-  // Separate LDS variables per slot: the compiler's wait-count pass can then tell that reads
-  // of one slot do not depend on the DMA still filling another.
-  __shared__ __attribute__((aligned(16))) uint8_t lds_s0[SLOT], lds_s1[SLOT];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_s2[NSLOT > 2 ? SLOT : 16], lds_s3[NSLOT > 3 ? SLOT : 16];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_s4[NSLOT > 4 ? SLOT : 16], lds_s5[NSLOT > 5 ? SLOT : 16];
-  auto slot_ptr = [&](auto ic) -> uint8_t* {
-    constexpr int i = decltype(ic)::value;
-    if constexpr (i == 0) return lds_s0;
-    else if constexpr (i == 1) return lds_s1;
-    else if constexpr (i == 2) return lds_s2;
-    else if constexpr (i == 3) return lds_s3;
-    else if constexpr (i == 4) return lds_s4;
-    else return lds_s5;
-  };
+  constexpr int WPER = C::WPER, NSC = C::NSC;
 
   int mc, tile, split;
   if (!w4_decode_id(p, mc, tile, split)) return;
@@ -173,16 +164,21 @@ __global__ __launch_bounds__(256) void w4a16_ws_kernel(W4A16Params p) {
         const int b = blk0 + c * S + j;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
+          // The step's MT activation fragments are read first, so their LDS latency overlaps
+          // (with each other and with the dequantization of the weight fragments) instead of
+          // standing between every pair of MFMAs.
+          v8h af[MT];
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+            af[t] = *reinterpret_cast<const v8h*>(aslot + (j * BM + 16 * t + r) * 256 + 16 * (pc[u] ^ r));
+          __builtin_amdgcn_sched_barrier(0);
           v8h wf[RW];
 #pragma unroll
           for (int i = 0; i < RW; ++i) wf[i] = wt.frag(b, i, u, wring[ri], sring[ri]);
 #pragma unroll
-          for (int t = 0; t < MT; ++t) {
-            const int row = 16 * t + r;
-            const v8h af = *reinterpret_cast<const v8h*>(aslot + (j * BM + row) * 256 + 16 * (pc[u] ^ r));
+          for (int t = 0; t < MT; ++t)
 #pragma unroll
-            for (int i = 0; i < RW; ++i) acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[i], af, acc[i][t], 0, 0, 0);
-          }
+            for (int i = 0; i < RW; ++i) acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[i], af[t], acc[i][t], 0, 0, 0);
         }
       });
     });
@@ -191,6 +187,23 @@ __global__ __launch_bounds__(256) void w4a16_ws_kernel(W4A16Params p) {
 
   __shared__ int s_last_ws4;
   w4_epilogue<MT, RW, BM, BN>(p, acc, mc, tile, split, m0, n0, w * BNW, M, &s_last_ws4);
+}
+
+template <int MT, int RW, int S, int NSLOT, int NSW, int LAYOUT>
+__global__ __launch_bounds__(256) void w4a16_ws_kernel(W4A16Params p) {
+  constexpr int SLOT = W4WsCfg<MT, RW, S, NSLOT, NSW, LAYOUT>::SLOT;
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s0[SLOT], lds_s1[SLOT];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s2[NSLOT > 2 ? SLOT : 16], lds_s3[NSLOT > 3 ? SLOT : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s4[NSLOT > 4 ? SLOT : 16], lds_s5[NSLOT > 5 ? SLOT : 16];
+  w4a16_ws_body<MT, RW, S, NSLOT, NSW, LAYOUT>(p, [&](auto ic) -> uint8_t* {
+    constexpr int i = decltype(ic)::value;
+    if constexpr (i == 0) return lds_s0;
+    else if constexpr (i == 1) return lds_s1;
+    else if constexpr (i == 2) return lds_s2;
+    else if constexpr (i == 3) return lds_s3;
+    else if constexpr (i == 4) return lds_s4;
+    else return lds_s5;
+  });
 }
 
 }  // namespace specq
