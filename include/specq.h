@@ -186,16 +186,20 @@ int specq_set_option(const char* name, int value);
  *   sc       fp16 [N, K/group] group scales, row stride ld_sc
  *   group    K group size: a power of two, a multiple of 32 (layouts 1, 2) or 16 (layout 0),
  *            dividing K.  K must be a multiple of 128.
- *   block_m  token rows per tile, a multiple of 16 up to 256 (0 = automatic; with a plan
+ *   block_m  token rows per tile, a multiple of 16 up to 256 (tiles deeper than 144 rows
+ *            run as equal chunks of at most 144 rows; 0 = automatic; with a plan
  *            and block_n = 0 the launch holds a menu of tilings and runs, for each 16 rows
  *            of the active M, the one the eager cost model picks there);
- *   block_n  64 or 128 channels per workgroup (0 = automatic); num_warps is ignored (4).
+ *   block_n  64 or 128 channels per workgroup (0 = automatic); num_warps is ignored (the
+ *            LDS-staged kernels run 8 waves, the register-stream family 4).
  *   Other arguments as specq_w8a8.  The fp32 accumulation order depends only on (N, K),
  *   split_k (0 = automatic, chosen from N and K) and whether the layout is the reference one:
- *   split s sums its contiguous range of 128-wide K blocks in order and the splits are added
- *   in split order; a block is k in [128b, 128b + 128) for layouts 1 and 2 and the two runs
- *   [64b, 64b + 64) and K/2 + [64b, 64b + 64) for layout 0.  It never depends on M, block_m,
- *   block_n or the plan, so those give bit-identical results, and so do layouts 1 and 2.
+ *   split s takes a contiguous range of 128-wide K blocks and sums the blocks at even and at
+ *   odd local index as two streams, each from zero in block order, then adds them (even +
+ *   odd); the splits are added in split order.  A block is k in [128b, 128b + 128) for
+ *   layouts 1 and 2 and the two runs [64b, 64b + 64) and K/2 + [64b, 64b + 64) for layout 0.
+ *   It never depends on M, block_m, block_n or the plan, so those give bit-identical results,
+ *   and so do layouts 1 and 2.
  * ------------------------------------------------------------------------------------- */
 size_t specq_w4a16_workspace_size(int m_grid, int N, int K, int block_m, int block_n,
                                   int num_warps, int split_k);

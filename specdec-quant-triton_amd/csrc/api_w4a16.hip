@@ -2,7 +2,8 @@
 // launch, and the load-time weight packing.
 //
 // Kernel families (identical fp32 summation order, so every choice is bit-identical):
-//   WS  LDS-staged activations (w4a16_ws.hpp) for any token tile up to 256 rows (default).
+//   WS  LDS-staged activations (w4a16_ws.hpp) for token tiles up to 144 rows (default; a
+//       deeper BLOCK_M runs as equal chunks of at most 144 rows).
 //   RK  register-stream kernel (w4a16_rk.hpp) for 16- and 32-row token tiles (w4a16_path 1).
 #include <algorithm>
 #include <atomic>
@@ -214,9 +215,12 @@ int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, in
     return w4_plan_config(layout, m_grid, N, K, split_k, cfg);
   int mt;
   if (block_m > 0) {
-    SPECQ_REQUIRE(block_m % 16 == 0 && block_m <= 16 * kW4MaxMt, SPECQ_ENOTSUP,
-                  "w4a16: BLOCK_M=%d must be a multiple of 16 and at most %d", block_m, 16 * kW4MaxMt);
-    mt = block_m / 16;
+    SPECQ_REQUIRE(block_m % 16 == 0 && block_m <= 256, SPECQ_ENOTSUP,
+                  "w4a16: BLOCK_M=%d must be a multiple of 16 and at most 256", block_m);
+    // Tiles deeper than the deepest compiled one run as equal chunks of at most that depth
+    // (the result does not depend on the tiling).
+    const int req = block_m / 16;
+    mt = ceil_div(req, ceil_div(req, kW4MaxMt));
   } else {
     // One chunk of token rows covering M (the weight is read once), split evenly past the
     // deepest tile.  With a plan the active M is usually far below the grid's: chunks of at
@@ -313,9 +317,9 @@ int w4a16_attrs(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   out->num_regs = fa.numRegs;
   out->lds_bytes = (int)fa.sharedSizeBytes;
   out->scratch_bytes = (int)fa.localSizeBytes;
-  out->threads = 256;
+  out->threads = cfg.family == kW4Rk ? 256 : kW4WsThreads;
   out->grid = cfg.grid;
-  out->block_m = cfg.mt * 16; out->block_n = 64 * cfg.rw; out->num_warps = 4;
+  out->block_m = cfg.mt * 16; out->block_n = 64 * cfg.rw; out->num_warps = out->threads / 64;
   out->split_k = cfg.splits;
   return SPECQ_OK;
 }
@@ -374,9 +378,9 @@ extern "C" int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t l
     W4PlanParams pp;
     pp.p = p;
     for (int e = 0; e < kW4PlanRows; ++e) pp.t[e] = cfg.plan_t[e];
-    return launch(cfg.fn, cfg.grid, 256, 0, (hipStream_t)stream, &pp);
+    return launch(cfg.fn, cfg.grid, kW4WsThreads, 0, (hipStream_t)stream, &pp);
   }
-  return launch(cfg.fn, cfg.grid, 256, 0, (hipStream_t)stream, &p);
+  return launch(cfg.fn, cfg.grid, cfg.family == kW4Rk ? 256 : kW4WsThreads, 0, (hipStream_t)stream, &p);
 }
 
 extern "C" size_t specq_w4a16_packed_bytes(int N, int K) {

@@ -19,11 +19,13 @@
 //         K block b and 16-row tile t at (b * ntiles + t) KB, so a wave's block is one
 //         contiguous 1 KB load and the workgroups running together sweep one window.
 //  * The fp32 summation order is fixed by (N, K), the split count and the K order of the
-//    layout (layouts 1 and 2 share one; layout 0's blocks pair k with k + K/2): split s sums
-//    the blocks of its contiguous range in increasing order (4 MFMA K steps per block, in
-//    order), starting from zero, and the splits are added in split order by the last
-//    workgroup to arrive.  Token tiling, channel tiling, kernel family and plan mode never
-//    change it, so every tile choice and plan-mode replay produces bit-identical results.
+//    layout (layouts 1 and 2 share one; layout 0's blocks pair k with k + K/2): split s takes
+//    a contiguous range of blocks and sums it as two streams, the blocks at even and at odd
+//    local index, each starting from zero in increasing block order (4 MFMA K steps per
+//    block, in order); the split's result is even + odd, and the splits are added in split
+//    order by the last workgroup to arrive.  Token tiling, channel tiling, kernel family and
+//    plan mode never change it, so every tile choice and plan-mode replay produces
+//    bit-identical results.
 #pragma once
 #include "common.hpp"
 

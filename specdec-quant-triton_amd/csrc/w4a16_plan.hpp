@@ -9,9 +9,9 @@
 // an eager call.
 //
 // Menu (index: token rows x channels): 0..1 16 x 64/128, 2..3 32, 4..5 48, 6..7 64, 8..9 80,
-// 10 96 x 128, 11 112 x 128, 12..13 144.  The tilings share four LDS slots sized for the
-// largest of them: two of 144 rows x 256 bytes, two of 96 x 256 (the 4-slot rings of tiles up
-// to 96 rows), 120 KB.
+// 10 96 x 128, 11 112 x 128, 12..13 144.  Every tiling runs 8 waves in two streams, each with a
+// 2-slot ring; the tilings share two slot variables of two stream halves each, sized for the
+// largest tiling (4 x 144 rows x 256 bytes, 144 KB).
 #pragma once
 #include "w4a16_tiles.hpp"
 
@@ -22,7 +22,7 @@ constexpr int kW4PlanMenu = 14;
 constexpr int kW4PlanMenuMt[kW4PlanMenu] = {1, 1, 2, 2, 3, 3, 4, 4, 5, 5, 6, 7, 9, 9};
 constexpr int kW4PlanMenuRw[kW4PlanMenu] = {1, 2, 1, 2, 1, 2, 1, 2, 1, 2, 2, 2, 1, 2};
 constexpr int kW4PlanSlotA = 9 * 16 * 256;  // slots 0, 1
-constexpr int kW4PlanSlotB = 6 * 16 * 256;  // slots 2, 3
+constexpr int kW4PlanSlotB = 16;            // slots 2, 3 (unused by 2-slot rings)
 
 struct W4PlanTile {
   int path;  // menu index
@@ -37,22 +37,23 @@ template <int I, int LAYOUT, class SlotPtr>
 __device__ __forceinline__ void w4a16_plan_path(const W4A16Params& p, SlotPtr slots) {
   constexpr int MT = kW4PlanMenuMt[I], RW = kW4PlanMenuRw[I];
   using P = W4WsPick<MT, RW, LAYOUT>;
-  static_assert(P::Cfg::SLOT <= kW4PlanSlotA && (P::NSLOT <= 2 || P::Cfg::SLOT <= kW4PlanSlotB) && P::NSLOT <= 4,
+  static_assert(P::Cfg::SLOT <= kW4PlanSlotA && (P::NSLOT <= 2 || P::Cfg::SLOT <= kW4PlanSlotB) && P::NSLOT <= 4 &&
+                    4 * RW * MT * 1024 <= 2 * kW4PlanSlotA,
                 "menu tiling fits the shared slots");
   w4a16_ws_body<MT, RW, P::S, P::NSLOT, P::NSW, LAYOUT>(p, slots);
 }
 
 template <int LAYOUT>
-__global__ __launch_bounds__(256) void w4a16_plan_kernel(W4PlanParams pp) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds_s0[kW4PlanSlotA], lds_s1[kW4PlanSlotA];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_s2[kW4PlanSlotB], lds_s3[kW4PlanSlotB];
-  auto slots = [&](auto ic) -> uint8_t* {
+__global__ __launch_bounds__(kW4WsThreads) void w4a16_plan_kernel(W4PlanParams pp) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s0[2][kW4PlanSlotA], lds_s1[2][kW4PlanSlotA];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_s2[2][kW4PlanSlotB], lds_s3[2][kW4PlanSlotB];
+  auto slots = [&](auto ic, int h) -> uint8_t* {
     constexpr int i = decltype(ic)::value;
     static_assert(i < 4, "menu tilings use at most four slots");
-    if constexpr (i == 0) return lds_s0;
-    else if constexpr (i == 1) return lds_s1;
-    else if constexpr (i == 2) return lds_s2;
-    else return lds_s3;
+    if constexpr (i == 0) return lds_s0[h];
+    else if constexpr (i == 1) return lds_s1[h];
+    else if constexpr (i == 2) return lds_s2[h];
+    else return lds_s3[h];
   };
   int M = min(max(pp.p.plan[0], 0), pp.p.m_grid);
   M = uniform(M);

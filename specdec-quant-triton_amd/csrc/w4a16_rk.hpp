@@ -12,8 +12,10 @@
 //    loads (blocks past the split's range are out-of-range buffer reads that return zero and
 //    add nothing), so a compile-time s_waitcnt vmcnt separates the block being multiplied
 //    from the blocks in flight.
-//  * The workgroup's K range is its split (contiguous blocks); splits are summed in order by
-//    the last workgroup to arrive (w4_splitk_finish).
+//  * The workgroup's K range is its split (contiguous blocks).  The blocks at even and odd
+//    local index are summed into two accumulator sets (the two streams of the summation order,
+//    w4a16.hpp), added as even + odd at the end; splits are summed in order by the last
+//    workgroup to arrive (w4_splitk_finish).
 #pragma once
 #include "w4a16.hpp"
 
@@ -27,7 +29,8 @@ struct W4RkCfg {
   static constexpr int VG = RW * (4 + NSC) + 16 * MT;   // VGPRs per ring slot
   static constexpr int NS_REG = 168 / VG, NS_CNT = 63 / PER;
   static constexpr int NS0 = NS_REG < NS_CNT ? NS_REG : NS_CNT;
-  static constexpr int NS = NS0 > 8 ? 8 : (NS0 < 2 ? 2 : NS0);
+  // Even, so a block's parity within the split is its ring slot's (see the accumulators).
+  static constexpr int NS = NS0 > 8 ? 8 : (NS0 < 2 ? 2 : (NS0 & ~1));
   static constexpr int D = NS - 1;
   static constexpr bool OK = D * PER <= 63;
 };
@@ -77,11 +80,13 @@ __global__ __launch_bounds__(256) void w4a16_rk_kernel(W4A16Params p) {
             asrc, oob_unless(live & (arow[j] != kOOB), arow[j] + (uint32_t)(2 * w4_k<LAYOUT>(b, u, g, halfK))), 0, 0);
   };
 
-  v4f acc[RW][MT];
+  v4f acc[2][RW][MT];  // [stream: local block parity]
 #pragma unroll
-  for (int i = 0; i < RW; ++i)
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int j = 0; j < MT; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < RW; ++i)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) acc[h][i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
   v4i wring[NS][RW];
   uint32_t sring[NS][RW][NSC];
@@ -111,15 +116,20 @@ __global__ __launch_bounds__(256) void w4a16_rk_kernel(W4A16Params p) {
         for (int j = 0; j < MT; ++j) {
           const v8h af = __builtin_bit_cast(v8h, aring[t][j][u]);
 #pragma unroll
-          for (int i = 0; i < RW; ++i) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[i], af, acc[i][j], 0, 0, 0);
+          for (int i = 0; i < RW; ++i) acc[t & 1][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wf[i], af, acc[t & 1][i][j], 0, 0, 0);
         }
       }
     });
   }
   wait_vmcnt<0>();
+  v4f sum[RW][MT];
+#pragma unroll
+  for (int i = 0; i < RW; ++i)
+#pragma unroll
+    for (int j = 0; j < MT; ++j) sum[i][j] = acc[0][i][j] + acc[1][i][j];
 
   __shared__ int s_last_rk4;
-  w4_epilogue<MT, RW, BM, BN>(p, acc, mc, tile, split, m0, n0, w * BNW, M, &s_last_rk4);
+  w4_epilogue<MT, RW, BM, BN>(p, sum, mc, tile, split, m0, n0, w * BNW, M, &s_last_rk4);
 }
 
 }  // namespace specq

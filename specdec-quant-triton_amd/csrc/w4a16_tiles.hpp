@@ -10,31 +10,18 @@
 
 namespace specq {
 
-constexpr int kW4MaxMt = 16;    // deepest token tile (256 rows)
+constexpr int kW4MaxMt = 9;     // deepest token tile (144 rows: two streams x two LDS slots)
 constexpr int kW4RkMaxMt = 2;
 
-// LDS ring and weight-ring depth per tile (measured on the Llama-3-8B linears): chunks of 2
-// blocks for 16-row tiles (1 beyond), 4 LDS slots up to 96 rows (2 beyond), and a weight ring
-// as deep as the LDS ring but at least 4 blocks, as far as the wait counts fit the 6-bit load
-// counter.  Deeper weight rings measured slower.
+// LDS ring and weight-ring depth per tile (measured on the Llama-3-8B linears, 8-wave
+// kernel): chunks of 2 blocks for 16-row tiles (1 beyond), 2 LDS slots per stream (one chunk
+// in flight ahead of the one being multiplied), and a weight ring as deep as the LDS ring (2
+// blocks per stream, 4 for 16-row tiles); deeper rings of either kind measured slower.
 template <int MT, int RW, int LAYOUT>
 struct W4WsPick {
   static constexpr int S = MT == 1 ? 2 : 1;
-  static constexpr int WPER = RW * (1 + W4Nsc<LAYOUT>::value);
-  static constexpr bool fits(int nslot, int nsw) {
-    return (nsw - 1) * WPER + ((nsw - 1 + S - 1) / S) * MT * S <= 63 && (nslot - 1) * S * (WPER + MT) <= 63 &&
-           nslot * MT * 16 * 256 * S <= 160 * 1024;
-  }
-  static constexpr int choose() {  // nslot * 100 + nsw
-    for (int nslot = MT <= 6 ? 4 : 2; nslot >= 2; --nslot) {
-      const int body = S * nslot;
-      for (int nsw = ((4 + body - 1) / body) * body; nsw >= body; nsw -= body)
-        if (fits(nslot, nsw)) return nslot * 100 + nsw;
-    }
-    return 0;
-  }
-  static constexpr int NSLOT = choose() / 100;
-  static constexpr int NSW = choose() % 100;
+  static constexpr int NSLOT = 2;
+  static constexpr int NSW = S * NSLOT;
   using Cfg = W4WsCfg<MT, RW, S, NSLOT, NSW, LAYOUT>;
 };
 // The same choice at run time (kernel names in resource queries).

@@ -1,5 +1,5 @@
 // Instantiations of the LDS-staged-activation W4A16 kernel for the packed fragment layout:
-// token tiles of 1 .. 16 x 16 rows, BLOCK_N = 64 (RW 1) and 128 (RW 2).
+// token tiles of 1 .. 9 x 16 rows, BLOCK_N = 64 (RW 1) and 128 (RW 2).
 #include "w4a16_tiles.hpp"
 
 namespace specq {
@@ -24,20 +24,6 @@ const void* w4a16_ws_fn_l2(int mt, int rw) {
     case 34: return w4a16_ws_pick<8, 2, 2>();
     case 37: return w4a16_ws_pick<9, 1, 2>();
     case 38: return w4a16_ws_pick<9, 2, 2>();
-    case 41: return w4a16_ws_pick<10, 1, 2>();
-    case 42: return w4a16_ws_pick<10, 2, 2>();
-    case 45: return w4a16_ws_pick<11, 1, 2>();
-    case 46: return w4a16_ws_pick<11, 2, 2>();
-    case 49: return w4a16_ws_pick<12, 1, 2>();
-    case 50: return w4a16_ws_pick<12, 2, 2>();
-    case 53: return w4a16_ws_pick<13, 1, 2>();
-    case 54: return w4a16_ws_pick<13, 2, 2>();
-    case 57: return w4a16_ws_pick<14, 1, 2>();
-    case 58: return w4a16_ws_pick<14, 2, 2>();
-    case 61: return w4a16_ws_pick<15, 1, 2>();
-    case 62: return w4a16_ws_pick<15, 2, 2>();
-    case 65: return w4a16_ws_pick<16, 1, 2>();
-    case 66: return w4a16_ws_pick<16, 2, 2>();
     default: return nullptr;
   }
 }
