@@ -129,7 +129,8 @@ def _pack(wp):
     return out
 
 
-@pytest.mark.parametrize("shape", [(1000, 1024), (4096, 4096), (1024, 4096), (4096, 14336), (17, 256), (1, 128)])
+@pytest.mark.parametrize("shape", [(1000, 1024), (4096, 4096), (1024, 4096), (4096, 14336), (17, 256), (1, 128),
+                                   (33, 384), (70, 640)])
 def test_w4a16_layouts_families_tiles_bit_identical(shape):
     """Every kernel family (w4a16_path 1: register stream, 2: LDS-staged), BLOCK_M and
     BLOCK_N gives the same bits, and so do the layouts that walk K in the same order (int32
@@ -161,6 +162,36 @@ def test_w4a16_layouts_families_tiles_bit_identical(shape):
                                 check_tol(out, ref[:M], what)
                             else:
                                 assert torch.equal(out, base[order]), what
+    finally:
+        _lib.set_option("w4a16_path", 0)
+
+
+@pytest.mark.parametrize("split_k", [1, 2, 3])
+def test_w4a16_odd_block_counts_per_split(split_k):
+    """K = 640 is 5 blocks: splits of 5, 3 + 2 and 2 + 2 + 1 blocks, so the odd-index stream of
+    a split is one block short or empty.  Both kernel families, every BLOCK_M, the same bits;
+    within tolerance of the oracle."""
+    from specq import _lib
+    N, Kd = 200, 640
+    note(f"w4a16 odd blocks split_k={split_k}")
+    qu, sc = gen.int4_weights(N, Kd, 128, seed=57)
+    a = gen.fp16_acts(100, Kd, seed=58)
+    ref = O.w4a16(a.numpy(), qu.numpy(), sc.numpy(), 128)
+    wi, a, sc = gen.pack_i32(qu).to(DEV), a.to(DEV), sc.to(DEV)
+    try:
+        for M in (1, 16, 17, 100):
+            base = None
+            for path in (1, 2):
+                _lib.set_option("w4a16_path", path)
+                for bm in (16, 32, 48, 144):
+                    out, ck = K.w4a16_matmul(a[:M], wi, sc, BLOCK_M=bm, split_k=split_k)
+                    torch.cuda.synchronize()
+                    what = f"M={M} path={path} BLOCK_M={bm} split_k={split_k} ({ck.name})"
+                    if base is None:
+                        base = out
+                        check_tol(out, ref[:M], what)
+                    else:
+                        assert torch.equal(out, base), what
     finally:
         _lib.set_option("w4a16_path", 0)
 
