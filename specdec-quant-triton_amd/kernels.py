@@ -44,7 +44,8 @@ Differences a caller may notice:
     summation order depends only on (N, K), split_k and whether the weight is the reference
     uint8 packing (whose bytes pair k with k + K/2), so every W4A16 tile choice is
     bit-identical too.
-    W4A16 BLOCK_M is at most 256.
+    W4A16 BLOCK_M is at most 256 (tiles deeper than 144 rows run as equal chunks of at most
+    144 rows); its LDS-staged kernels run 8 waves whatever num_warps says.
 """
 from __future__ import annotations
 
