@@ -1,8 +1,8 @@
 // Tile table of the W4A16 kernels, shared by the instantiation units and the C-ABI dispatcher.
 //   rk (w4a16_rk.hpp): token tiles of 1-2 x 16 rows, activations loaded into registers.
-//   ws (w4a16_ws.hpp): token tiles of 1-16 x 16 rows, activations staged in an LDS ring of
-//      NSLOT chunks of S 128-wide K blocks (4 KB per block per 16 token rows), weights in a
-//      register ring NSW blocks deep (W4WsPick).
+//   ws (w4a16_ws.hpp): token tiles of 1-9 x 16 rows, 8 waves in two K streams, each stream's
+//      activations staged in an LDS ring of NSLOT chunks of S 128-wide K blocks (4 KB per
+//      block per 16 token rows), weights in a register ring NSW blocks deep (W4WsPick).
 // RW = 1 or 2 16-channel fragments per wave, i.e. BLOCK_N = 64 or 128 per workgroup.
 #pragma once
 #include "w4a16_rk.hpp"
