@@ -45,6 +45,7 @@ for _p in (ROOT, PKG):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # dense
 # The seven linears of a Llama-3-8B layer, and how a layer launches them:
 # GEMMs that share an activation run as one grouped launch.
 CONFIG1 = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
@@ -298,7 +299,9 @@ def bench_w4a16(args, K, torch):
         ms = time_replays(graph, args.steps, args.warmup)
         b = args.layers * sum(w4a16_bytes(M, N, Kd) for _, N, Kd in CONFIG1)
         flops = args.layers * sum(2 * M * N * Kd for _, N, Kd in CONFIG1)
-        res[label] = dict(M=M, ms=ms, GBps=b / (ms * 1e-3) / 1e9, TFLOPs=flops / (ms * 1e-3) / 1e12)
+        gbps, tflops = b / (ms * 1e-3) / 1e9, flops / (ms * 1e-3) / 1e12
+        res[label] = dict(M=M, ms=ms, GBps=gbps, TFLOPs=tflops, hbm_frac=gbps / HBM_PEAK_GBS,
+                          mfma_frac=tflops / FP16_MFMA_PEAK_TFLOPS)
         del graph
     del layers, raw
     torch.cuda.empty_cache()
@@ -367,7 +370,8 @@ def bench_attention(args, K, torch):
         for name, qpp in (("fused", ql), ("qpp1", 1)):
             fn = lambda: K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=qpp, out=out)  # noqa: E731
             ms = do_bench(fn, warmup=5, rep=20)
-            res[f"ctx{ctx}_{name}"] = dict(us=ms * 1e3, GBps=b / (ms * 1e-3) / 1e9)
+            gbps = b / (ms * 1e-3) / 1e9
+            res[f"ctx{ctx}_{name}"] = dict(us=ms * 1e3, GBps=gbps, hbm_frac=gbps / HBM_PEAK_GBS)
         log(f"attention ctx={ctx}: fused {res[f'ctx{ctx}_fused']['us']:.1f} us")
     # The step before attention: the k+1 new tokens' K/V quantised into the cache pages.
     for B in (args.B, 32):
@@ -708,7 +712,7 @@ def main() -> int:
         detail["w4a8_decode"] = {k: round(x, 4) for k, x in w48["decode"].items()}
         detail["w4a8_verify_over_decode"] = round(w48["verify"]["ms"] / w48["decode"]["ms"], 4)
         attn = bench_attention(args, K, torch)
-        detail["attention_B8_k8"] = {k: {kk: round(x, 2) for kk, x in r.items()}
+        detail["attention_B8_k8"] = {k: {kk: round(x, 4 if kk.endswith("frac") else 2) for kk, x in r.items()}
                                      for k, r in attn.items() if not k.startswith("kv_append")}
         detail["kv_append_k8"] = {k: {kk: round(x, 2) for kk, x in r.items()}
                                   for k, r in attn.items() if k.startswith("kv_append")}
