@@ -166,6 +166,52 @@ def test_w4a16_layouts_families_tiles_bit_identical(shape):
         _lib.set_option("w4a16_path", 0)
 
 
+@pytest.mark.parametrize("group", [16, 32, 64, 256])
+def test_w4a16_group_sizes(group):
+    """Group sizes other than 128 (scales change within a 128-wide K block for groups below 128,
+    and every two blocks for 256): every layout that supports the group (16 only with the
+    reference uint8 layout), both kernel families and a plan-mode call, against the oracle;
+    the layouts that walk K in the same order give the same bits."""
+    from specq import _lib
+    N, Kd = 200, 1024
+    note(f"w4a16 group={group}")
+    qu, sc = gen.int4_weights(N, Kd, group, seed=60 + group)
+    a = gen.fp16_acts(100, Kd, seed=61)
+    ref = O.w4a16(a.numpy(), qu.numpy(), sc.numpy(), group)
+    a, sc = a.to(DEV), sc.to(DEV)
+    weights = {"u8": ("u8", gen.pack_u8_reference(qu).to(DEV))}
+    if group >= 32:
+        wi = gen.pack_i32(qu).to(DEV)
+        weights.update({"i32": ("k", wi), "packed": ("k", _pack(wi))})
+    plan = torch.zeros(8, dtype=torch.int32, device=DEV)
+    try:
+        for M in (1, 17, 72, 100):
+            base = {}
+            for path in (1, 2):
+                _lib.set_option("w4a16_path", path)
+                for wname, (order, wp) in weights.items():
+                    for bm in (None, 16, 32, 80):
+                        out, ck = K.w4a16_matmul(a[:M], wp, sc, group=group, BLOCK_M=bm, BLOCK_K=min(64, group))
+                        torch.cuda.synchronize()
+                        what = f"group={group} M={M} path={path} {wname} BLOCK_M={bm} ({ck.name})"
+                        if order not in base:
+                            base[order] = out
+                            check_tol(out, ref[:M], what)
+                        else:
+                            assert torch.equal(out, base[order]), what
+            _lib.set_option("w4a16_path", 0)
+            for wname, (order, wp) in weights.items():
+                plan[0] = M
+                outp = torch.full((100, N), 7.0, dtype=torch.float16, device=DEV)
+                K.w4a16_matmul(a, wp, sc, group=group, out=outp, plan=plan, grid_m_max=100, BLOCK_M=None,
+                               BLOCK_K=min(64, group))
+                torch.cuda.synchronize()
+                assert torch.equal(outp[:M], base[order]), f"group={group} {wname}: plan mode differs at M={M}"
+                assert bool((outp[M:] == 7.0).all()), f"group={group} {wname}: plan mode wrote rows >= M"
+    finally:
+        _lib.set_option("w4a16_path", 0)
+
+
 @pytest.mark.parametrize("split_k", [1, 2, 3])
 def test_w4a16_odd_block_counts_per_split(split_k):
     """K = 640 is 5 blocks: splits of 5, 3 + 2 and 2 + 2 + 1 blocks, so the odd-index stream of
