@@ -75,9 +75,10 @@ __global__ __launch_bounds__(256) void elt_kernel(EltParams p) {
   }
 }
 
-// Register-resident row: thread t holds the 8-element vectors t, t + 256, ... (VPT of them).
-template <int MODE, int VPT>
-__global__ __launch_bounds__(256) void elt_vec_kernel(EltParams p) {
+// Register-resident row: thread t holds the 8-element vectors t, t + NT, ... (VPT of them).
+// Wide rows run NT = 1024 threads (four waves per SIMD hide the exp / reciprocal chains).
+template <int MODE, int VPT, int NT>
+__global__ __launch_bounds__(NT) void elt_vec_kernel(EltParams p) {
   int M = p.M;
   if (p.plan != nullptr) M = min(max(p.plan[0], 0), p.m_grid);
   const int m = blockIdx.x;
@@ -88,7 +89,7 @@ __global__ __launch_bounds__(256) void elt_vec_kernel(EltParams p) {
   v8h xv[VPT], uv[VPT];
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    const int v = t + 256 * i;
+    const int v = t + NT * i;
     if (v < nv) {
       xv[i] = xr[v];
       if constexpr (MODE != 1) uv[i] = ur[v];
@@ -106,14 +107,14 @@ __global__ __launch_bounds__(256) void elt_vec_kernel(EltParams p) {
     v8h* hr = reinterpret_cast<v8h*>(p.h + (int64_t)m * p.ldh);
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
-      if (t + 256 * i < nv) hr[t + 256 * i] = val[i];
+      if (t + NT * i < nv) hr[t + NT * i] = val[i];
     return;
   } else {
-    __shared__ float red[256 / kWave];
+    __shared__ float red[NT / kWave];
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
-      if (t + 256 * i < nv)
+      if (t + NT * i < nv)
 #pragma unroll
         for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf((float)val[i][j]));
 #pragma unroll
@@ -122,12 +123,12 @@ __global__ __launch_bounds__(256) void elt_vec_kernel(EltParams p) {
     __syncthreads();
     amax = red[0];
 #pragma unroll
-    for (int i = 1; i < 256 / kWave; ++i) amax = fmaxf(amax, red[i]);
+    for (int i = 1; i < NT / kWave; ++i) amax = fmaxf(amax, red[i]);
     const float s = fmaxf(amax, 1e-8f) / 127.0f;
     v2i* qr = reinterpret_cast<v2i*>(p.q + (int64_t)m * p.ldq);
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      if (t + 256 * i >= nv) continue;
+      if (t + NT * i >= nv) continue;
       int w[2] = {0, 0};
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -135,20 +136,28 @@ __global__ __launch_bounds__(256) void elt_vec_kernel(EltParams p) {
         v = fminf(fmaxf(v, -127.f), 127.f);
         w[j >> 2] |= ((int)v & 0xff) << (8 * (j & 3));
       }
-      qr[t + 256 * i] = v2i{w[0], w[1]};
+      qr[t + NT * i] = v2i{w[0], w[1]};
     }
     if (t == 0) p.s[m] = s;
   }
 }
 
 template <int MODE>
-static const void* elt_vec_fn(int vpt) {
+static const void* elt_vec_fn(int vpt, int nt) {
+  if (nt == 1024) {
+    switch (vpt) {
+      case 1: return reinterpret_cast<const void*>(&elt_vec_kernel<MODE, 1, 1024>);
+      case 2: return reinterpret_cast<const void*>(&elt_vec_kernel<MODE, 2, 1024>);
+      case 4: return reinterpret_cast<const void*>(&elt_vec_kernel<MODE, 4, 1024>);
+    }
+    return nullptr;
+  }
   switch (vpt) {
-    case 1: return reinterpret_cast<const void*>(&elt_vec_kernel<MODE, 1>);
-    case 2: return reinterpret_cast<const void*>(&elt_vec_kernel<MODE, 2>);
-    case 4: return reinterpret_cast<const void*>(&elt_vec_kernel<MODE, 4>);
-    case 8: return reinterpret_cast<const void*>(&elt_vec_kernel<MODE, 8>);
-    case 16: return reinterpret_cast<const void*>(&elt_vec_kernel<MODE, 16>);
+    case 1: return reinterpret_cast<const void*>(&elt_vec_kernel<MODE, 1, 256>);
+    case 2: return reinterpret_cast<const void*>(&elt_vec_kernel<MODE, 2, 256>);
+    case 4: return reinterpret_cast<const void*>(&elt_vec_kernel<MODE, 4, 256>);
+    case 8: return reinterpret_cast<const void*>(&elt_vec_kernel<MODE, 8, 256>);
+    case 16: return reinterpret_cast<const void*>(&elt_vec_kernel<MODE, 16, 256>);
   }
   return nullptr;
 }
@@ -162,17 +171,21 @@ static int launch_elt(int mode, EltParams& p, hipStream_t stream) {
   if (mode == 0) vec = vec && (uintptr_t)p.h % 16 == 0 && p.ldh % 8 == 0;
   else vec = vec && (uintptr_t)p.q % 8 == 0 && p.ldq % 8 == 0;
   const void* fn = nullptr;
+  int nt = 256;
   if (vec) {
-    const int per_thread = (p.N / 8 + 255) / 256;
+    nt = p.N / 8 >= 1024 ? 1024 : 256;
+    const int per_thread = (p.N / 8 + nt - 1) / nt;
     int vpt = 1;
     while (vpt < per_thread) vpt <<= 1;
-    fn = mode == 0 ? elt_vec_fn<0>(vpt) : (mode == 1 ? elt_vec_fn<1>(vpt) : elt_vec_fn<2>(vpt));
+    fn = mode == 0 ? elt_vec_fn<0>(vpt, nt) : (mode == 1 ? elt_vec_fn<1>(vpt, nt) : elt_vec_fn<2>(vpt, nt));
   }
-  if (fn == nullptr)
+  if (fn == nullptr) {
+    nt = 256;
     fn = mode == 0 ? reinterpret_cast<const void*>(&elt_kernel<0>)
        : mode == 1 ? reinterpret_cast<const void*>(&elt_kernel<1>)
                    : reinterpret_cast<const void*>(&elt_kernel<2>);
-  return launch(fn, m_grid, 256, 0, stream, &p);
+  }
+  return launch(fn, m_grid, nt, 0, stream, &p);
 }
 
 }  // namespace specq
