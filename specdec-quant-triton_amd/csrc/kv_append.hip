@@ -35,6 +35,19 @@ struct KvAppendParams {
 template <int LPR, bool SF32>
 __global__ __launch_bounds__(256) void kv_append_kernel(KvAppendParams p) {
   constexpr int RPP = 256 / LPR;  // rows per pass
+  const int b = blockIdx.x / p.ql_grid, i = blockIdx.x % p.ql_grid;
+  const int t = threadIdx.x, grp = t / LPR, l = t % LPR;
+  auto row_src = [&](int row) {
+    const bool is_v = row >= p.H_KV;
+    const int h = is_v ? row - p.H_KV : row;
+    return (is_v ? p.v : p.k) + (int64_t)b * p.s_nb + (int64_t)i * p.s_nt + (int64_t)h * p.s_nh + 8 * l;
+  };
+  // The first pass's new K/V values and the context length depend on neither the plan nor
+  // the block table (every (b, i) of the grid lies inside the new K/V tensor and ctx_len), so
+  // their loads go out together with the plan's instead of after it.
+  v8h x_first = {};
+  if (grp < 2 * p.H_KV) x_first = *reinterpret_cast<const v8h*>(row_src(grp));
+  const int L = p.ctx_len[b];
   int nb = p.n_seqs, ql = p.q_len;
   if (p.plan != nullptr) {
     nb = min(max(p.plan[0], 0), p.B_grid);
@@ -42,20 +55,17 @@ __global__ __launch_bounds__(256) void kv_append_kernel(KvAppendParams p) {
   }
   nb = uniform(nb);
   ql = uniform(ql);
-  const int b = blockIdx.x / p.ql_grid, i = blockIdx.x % p.ql_grid;
   if (b >= nb || i >= ql) return;
-  const int pos = uniform(p.ctx_len[b] - ql + i);
+  const int pos = uniform(L - ql + i);
   if (pos < 0 || pos / p.PAGE >= p.max_pages) return;
   const int page = uniform(p.bt[(int64_t)b * p.s_bt + pos / p.PAGE]);
   if (page < 0 || page >= p.n_pages) return;
   const int slot = pos % p.PAGE;
 
-  const int t = threadIdx.x, grp = t / LPR, l = t % LPR;
   for (int row = grp; row < 2 * p.H_KV; row += RPP) {
     const bool is_v = row >= p.H_KV;
     const int h = is_v ? row - p.H_KV : row;
-    const _Float16* src = (is_v ? p.v : p.k) + (int64_t)b * p.s_nb + (int64_t)i * p.s_nt + (int64_t)h * p.s_nh;
-    const v8h x = *reinterpret_cast<const v8h*>(src + 8 * l);
+    const v8h x = row == grp ? x_first : *reinterpret_cast<const v8h*>(row_src(row));
     float amax = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf((float)x[j]));
