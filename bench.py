@@ -17,8 +17,8 @@ timed region starts.
   roofline     the dominant kernel (the grouped gate|up launch, 54% of the bytes): algorithmic
                bytes per launch / its mean launch duration, measured with HIP events around a
                graph of back-to-back launches on the stream the kernels run on, against 8 TB/s
-  cpu_baseline the reference's PyTorch formulas on the host cores (oracle/cpu_baseline.py,
-               BASELINE.md section 3): torch._int_mm with the fp32 epilogue on one layer's seven
+  cpu_baseline the reference's PyTorch formulas on the host cores (oracle/cpu_baseline.py):
+               torch._int_mm with the fp32 epilogue on one layer's seven
                linears at M = 72 (the value), plus the fp32 formula, W4A16 and attention timings
   detail       the k=0 decode step (M = 8) and the verify/decode ratio (target <= 1.1); the same
                step as 7 separate launches per layer, on row-major weights, and on the fused
@@ -372,7 +372,16 @@ def bench_attention(args, K, torch):
             ms = do_bench(fn, warmup=5, rep=20)
             gbps = b / (ms * 1e-3) / 1e9
             res[f"ctx{ctx}_{name}"] = dict(us=ms * 1e3, GBps=gbps, hbm_frac=gbps / HBM_PEAK_GBS)
-        log(f"attention ctx={ctx}: fused {res[f'ctx{ctx}_fused']['us']:.1f} us")
+        # The same call after a zeroing-only flush (triton.testing.do_bench's): the dirty lines it
+        # leaves are written back while the kernel reads, so this figure carries that traffic.
+        fn = lambda: K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=ql, out=out)  # noqa: E731
+        ms = do_bench(fn, warmup=5, rep=20, flush="dirty")
+        res[f"ctx{ctx}_fused_dirty_flush"] = dict(us=ms * 1e3, GBps=b / (ms * 1e-3) / 1e9)
+        log(f"attention ctx={ctx}: fused {res[f'ctx{ctx}_fused']['us']:.1f} us "
+            f"({res[f'ctx{ctx}_fused_dirty_flush']['us']:.1f} us after a zeroing-only flush)")
+    # Floor of this timing method: an empty-bodied one-element launch between the same events.
+    tiny = torch.zeros(1, device="cuda")
+    res["event_floor_us"] = do_bench(lambda: tiny.add_(1), warmup=5, rep=20) * 1e3
     # The step before attention: the k+1 new tokens' K/V quantised into the cache pages.
     for B in (args.B, 32):
         L = 4096 + ql
@@ -565,8 +574,8 @@ def bench_plan_graph(args, K, torch):
 
 
 def cpu_baseline(args, M: int, seconds: float):
-    """The reference's PyTorch formulas on the host cores (oracle/cpu_baseline.py, the plan of
-    BASELINE.md section 3), each on a bounded sample of the same workload:
+    """The reference's PyTorch formulas on the host cores (oracle/cpu_baseline.py), each on a
+    bounded sample of the same workload:
       value   torch._int_mm + the fp32 epilogue over one layer's seven config-1 linears at M
       also    the reference test's fp32 formula on the same layer (correctness.py:37), W4A16
               x.float() @ deq.float().T on the same shapes (correctness.py:76), and dense fp32
@@ -713,7 +722,8 @@ def main() -> int:
         detail["w4a8_verify_over_decode"] = round(w48["verify"]["ms"] / w48["decode"]["ms"], 4)
         attn = bench_attention(args, K, torch)
         detail["attention_B8_k8"] = {k: {kk: round(x, 4 if kk.endswith("frac") else 2) for kk, x in r.items()}
-                                     for k, r in attn.items() if not k.startswith("kv_append")}
+                                     for k, r in attn.items() if isinstance(r, dict) and not k.startswith("kv_append")}
+        detail["event_timing_floor_us"] = round(attn["event_floor_us"], 2)
         detail["kv_append_k8"] = {k: {kk: round(x, 2) for kk, x in r.items()}
                                   for k, r in attn.items() if k.startswith("kv_append")}
         detail["plan_graph_4layer"] = {k: round(x, 4) for k, x in bench_plan_graph(args, K, torch).items()}
