@@ -211,8 +211,8 @@ int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t ldq, int wq_
 
 /* W4A16 weight packed once at load time into 1 KB MFMA fragments (wq_layout 2 above): fragment
  * (b, t) of 128-wide K block b and 16-row tile t at (b * ceil(N/16) + t) KB; lane l's 16 bytes
- * hold row 16t + l%16 at k = 128b + 32*(l/16) + 8u + j as word u, byte i = nibble(j = i) |
- * nibble(j = i + 4) << 4 (rows past N hold nibble 8).  The source is layout 0 or 1 (row stride
+ * hold row 16t + l%16 at k = 128b + 32*(l/16) + 8u + j as word u, nibble j at bits 4p..4p+3
+ * with p = j/2 for even j and 4 + j/2 for odd j (rows past N hold nibble 8).  The source is layout 0 or 1 (row stride
  * ldq in elements of its storage type); `packed` holds specq_w4a16_packed_bytes() bytes, and
  * the scales stay as they are.  Results are bit-identical to layout 1 of the same weight.  No
  * reference counterpart: the reference reads the row-major packing on every call. */

@@ -23,8 +23,8 @@ const void* w4a16_plan_fn_l2();
 
 // Packs a W4A16 weight (layout 0 or 1, row stride ldq bytes) into 1 KB MFMA fragments:
 // fragment (b, t) of K block b and 16-row tile t at (b * ntiles + t) KB; lane l's 16 bytes hold
-// the nibbles of row 16t + l%16 for k = 128b + 32*(l/16) + 8u + j as word u, byte i =
-// nibble(j = i) | nibble(j = i + 4) << 4.  Rows past N hold nibble 8 (weight 0).
+// the nibbles of row 16t + l%16 for k = 128b + 32*(l/16) + 8u + j as word u, nibble j at bits
+// 4p..4p+3 with p = j/2 for even j and 4 + j/2 for odd j.  Rows past N hold nibble 8 (weight 0).
 __global__ __launch_bounds__(256) void w4a16_pack_kernel(const uint8_t* __restrict__ wq, int64_t ldq, int layout,
                                                          int N, int K, uint8_t* __restrict__ out) {
   const int ntiles = (N + 15) / 16;
@@ -43,13 +43,14 @@ __global__ __launch_bounds__(256) void w4a16_pack_kernel(const uint8_t* __restri
     }
     return (src[k >> 1] >> (4 * (k & 1))) & 15u;  // int32 words in k order = bytes in k order
   };
+  // Weight j of a word at nibble position (j odd ? 4 : 0) + j / 2 (w4_dequant_packed).
   int words[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int k0 = 128 * b + 32 * g + 8 * u;
     uint32_t x = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x |= (nib(k0 + i) | (nib(k0 + i + 4) << 4)) << (8 * i);
+    for (int j = 0; j < 8; ++j) x |= nib(k0 + j) << (4 * ((j & 1) * 4 + (j >> 1)));
     words[u] = (int)x;
   }
   *reinterpret_cast<v4i*>(out + frag * 1024 + l * 16) = v4i{words[0], words[1], words[2], words[3]};

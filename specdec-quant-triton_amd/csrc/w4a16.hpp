@@ -17,7 +17,9 @@
 //      1  int32 [N, K/8], 8 nibbles per word in k order;
 //      2  packed at load time (w4a16_pack_kernel): 1 KB MFMA fragments, fragment (b, t) of
 //         K block b and 16-row tile t at (b * ntiles + t) KB, so a wave's block is one
-//         contiguous 1 KB load and the workgroups running together sweep one window.
+//         contiguous 1 KB load and the workgroups running together sweep one window.  Within
+//         a word the 8 nibbles sit where fp16 magic constants extract them without byte
+//         shuffles (w4_dequant).
 //  * The fp32 summation order is fixed by (N, K), the split count and the K order of the
 //    layout (layouts 1 and 2 share one; layout 0's blocks pair k with k + K/2): split s takes
 //    a contiguous range of blocks and sums it as two streams, the blocks at even and at odd
@@ -57,33 +59,65 @@ __device__ __forceinline__ v2h nib_pair(uint32_t y, uint32_t sel) {
 
 // The 8 dequantized weights of MFMA K step u from a lane's 16 packed bytes.  s2 holds the
 // scale twice.  (1024 + n) - 1032 = n - 8 exactly; the product is the one rounding.
-template <int LAYOUT>
-__device__ __forceinline__ v8h w4_dequant(const v4i& wq, int u, v2h s2) {
-  uint32_t y0, y1;  // nibbles of weights 0..3 and 4..7, one per byte
-  if constexpr (LAYOUT == 1) {
-    const uint32_t x = (uint32_t)wq[u];
-    const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
-    y0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
-    y1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
-  } else if constexpr (LAYOUT == 0) {
-    const uint32_t x0 = (uint32_t)wq[(u & 1) * 2], x1 = (uint32_t)wq[(u & 1) * 2 + 1];
-    const int sh = (u >> 1) * 4;
-    y0 = (x0 >> sh) & 0x0F0F0F0Fu;
-    y1 = (x1 >> sh) & 0x0F0F0F0Fu;
-  } else {
-    const uint32_t x = (uint32_t)wq[u];
-    y0 = x & 0x0F0F0F0Fu;
-    y1 = (x >> 4) & 0x0F0F0F0Fu;
-  }
-  const v2h bias = {(_Float16)1032.0f, (_Float16)1032.0f};
-  const v2h h0 = (nib_pair(y0, 0x04010400u) - bias) * s2;
-  const v2h h1 = (nib_pair(y0, 0x04030402u) - bias) * s2;
-  const v2h h2 = (nib_pair(y1, 0x04010400u) - bias) * s2;
-  const v2h h3 = (nib_pair(y1, 0x04030402u) - bias) * s2;
+//
+// Layout 2 word (w4a16_pack_kernel): weights j = 0..7 of the step at nibble positions
+// 0, 4, 1, 5, 2, 6, 3, 7 (bits 4p..4p+3), i.e. the pairs (0,1), (2,3), (4,5), (6,7) at bits
+// {0-3, 16-19}, {4-7, 20-23}, {8-11, 24-27}, {12-15, 28-31}.  One AND-OR per pair turns a
+// pair into two fp16: a nibble in bits 0-3 of a half under exponent 0x64 is 1024 + n (ulp 1),
+// a nibble in bits 4-7 under exponent 0x54 is 64 + n (ulp 1/16); the upper two pairs take one
+// shift first.  Subtracting 1032 or 72 gives n - 8 exactly, so every layout dequantizes to the
+// same fp16 values.
+//
+// v_and_or_b32 is a VOP3 instruction, which takes no literal on this architecture, so the
+// compiler would split (x & m) | c into two VOP2 instructions with literals; the masks go in
+// scalar registers and the exponent patterns in (loop-invariant) vector registers instead.
+__device__ __forceinline__ uint32_t and_or_b32(uint32_t x, uint32_t mask, uint32_t bits) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(bits));
+  return r;
+}
+
+__device__ __forceinline__ v8h w4_dequant_packed(uint32_t x, v2h s2) {
+  const uint32_t y = x >> 8;
+  const v2h b1024 = {(_Float16)1032.0f, (_Float16)1032.0f};
+  const v2h b64 = {(_Float16)72.0f, (_Float16)72.0f};
+  const v2h h0 = (__builtin_bit_cast(v2h, and_or_b32(x, 0x000F000Fu, 0x64006400u)) - b1024) * s2;
+  const v2h h1 = (__builtin_bit_cast(v2h, and_or_b32(x, 0x00F000F0u, 0x54005400u)) - b64) * s2;
+  const v2h h2 = (__builtin_bit_cast(v2h, and_or_b32(y, 0x000F000Fu, 0x64006400u)) - b1024) * s2;
+  const v2h h3 = (__builtin_bit_cast(v2h, and_or_b32(y, 0x00F000F0u, 0x54005400u)) - b64) * s2;
   v8h r;
   r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
   r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
   return r;
+}
+
+template <int LAYOUT>
+__device__ __forceinline__ v8h w4_dequant(const v4i& wq, int u, v2h s2) {
+  if constexpr (LAYOUT == 2) {
+    return w4_dequant_packed((uint32_t)wq[u], s2);
+  } else {
+    uint32_t y0, y1;  // nibbles of weights 0..3 and 4..7, one per byte
+    if constexpr (LAYOUT == 1) {
+      const uint32_t x = (uint32_t)wq[u];
+      const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
+      y0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+      y1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+    } else {
+      const uint32_t x0 = (uint32_t)wq[(u & 1) * 2], x1 = (uint32_t)wq[(u & 1) * 2 + 1];
+      const int sh = (u >> 1) * 4;
+      y0 = (x0 >> sh) & 0x0F0F0F0Fu;
+      y1 = (x1 >> sh) & 0x0F0F0F0Fu;
+    }
+    const v2h bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const v2h h0 = (nib_pair(y0, 0x04010400u) - bias) * s2;
+    const v2h h1 = (nib_pair(y0, 0x04030402u) - bias) * s2;
+    const v2h h2 = (nib_pair(y1, 0x04010400u) - bias) * s2;
+    const v2h h3 = (nib_pair(y1, 0x04030402u) - bias) * s2;
+    v8h r;
+    r[0] = h0[0]; r[1] = h0[1]; r[2] = h1[0]; r[3] = h1[1];
+    r[4] = h2[0]; r[5] = h2[1]; r[6] = h3[0]; r[7] = h3[1];
+    return r;
+  }
 }
 
 // First of the 8 K indices of MFMA step u for lane group g in block b.

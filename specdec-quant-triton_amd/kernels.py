@@ -414,8 +414,9 @@ class PackedWeightInt4:
     MFMA fragments for w4a16_matmul.
 
     Fragment (128-wide K block b, 16-row tile t) is the 1 KB at (b * ceil(N/16) + t) KB; lane
-    l's 16 bytes hold row 16t + l%16 at k = 128b + 32*(l/16) + 8u + j as word u, byte
-    i = nibble(j = i) | nibble(j = i + 4) << 4.  Every weight load is then 1 KB contiguous.  The
+    l's 16 bytes hold row 16t + l%16 at k = 128b + 32*(l/16) + 8u + j as word u, nibble j at
+    bits 4p..4p+3 with p = j/2 for even j and 4 + j/2 for odd j (each pair of weights then
+    becomes two fp16 with one AND-OR).  Every weight load is 1 KB contiguous.  The
     group scales are not repacked.  Results are bit-identical to passing the int32 packing of
     the same weight (the reference uint8 packing sums K in another order, so it agrees to
     fp32 rounding).
