@@ -269,8 +269,10 @@ def bench_w8a8(args, K, torch):
 
 def bench_w4a16(args, K, torch):
     """W4A16 (config 2) over the seven config-1 linears, M = 72 and 8: INT4 weights (int32, 8
-    nibbles per word) packed once at load into MFMA fragments (pack_weight_int4), and the int32
-    weights as given for the verification step; one launch per linear."""
+    nibbles per word) packed once at load into MFMA fragments (pack_weight_int4).  The step runs
+    q|k|v and gate|up as grouped launches over their separate weights (w4a16_matmul_grouped,
+    bit-identical to one call per linear), 4 launches per layer like the W8A8 step; the same step
+    as 7 launches per layer, and the grouped step on the int32 weights as given, go beside it."""
     g = torch.Generator(device="cuda").manual_seed(3)
     layers, raw = [], []
     for _ in range(args.layers):
@@ -285,19 +287,33 @@ def bench_w4a16(args, K, torch):
     x = torch.randn((300, 4096), device="cuda", generator=g).half()
     x_ff = torch.randn((300, 14336), device="cuda", generator=g).half()
     outs = {name: torch.empty((300, N), dtype=torch.float16, device="cuda") for name, N, _ in CONFIG1}
+    shape = {n: (N, Kd) for n, N, Kd in CONFIG1}
     res = {}
-    for label, M, ls in (("verify", args.B * (args.k + 1), layers), ("decode", args.B, layers),
-                         ("verify_int32", args.B * (args.k + 1), raw)):
+    vM, dM = args.B * (args.k + 1), args.B
+    for label, M, ls, grouped in (("verify", vM, layers, True), ("decode", dM, layers, True),
+                                  ("verify_7_launches", vM, layers, False), ("decode_7_launches", dM, layers, False),
+                                  ("verify_int32", vM, raw, True)):
         def step():
             for lw in ls:
-                for name, N, Kd in CONFIG1:
-                    K.w4a16_matmul(x[:M] if Kd == 4096 else x_ff[:M], *lw[name], out=outs[name][:M], BLOCK_M=None)
+                if grouped:
+                    for _, mem in LAUNCHES:
+                        xa = x[:M] if shape[mem[0]][1] == 4096 else x_ff[:M]
+                        K.w4a16_matmul_grouped(xa, [lw[m] for m in mem], outs=[outs[m][:M] for m in mem])
+                else:
+                    for name, N, Kd in CONFIG1:
+                        K.w4a16_matmul(x[:M] if Kd == 4096 else x_ff[:M], *lw[name], out=outs[name][:M],
+                                       BLOCK_M=None)
         step()
         torch.cuda.synchronize()
         graph = capture(step)
         log(f"w4a16 {label} M={M}")
         ms = time_replays(graph, args.steps, args.warmup)
-        b = args.layers * sum(w4a16_bytes(M, N, Kd) for _, N, Kd in CONFIG1)
+        # Algorithmic bytes: every weight, scale and output once, each launch's activations once.
+        if grouped:
+            b = args.layers * sum(sum(w4a16_bytes(M, shape[m][0], shape[m][1]) for m in mem)
+                                  - (len(mem) - 1) * 2 * M * shape[mem[0]][1] for _, mem in LAUNCHES)
+        else:
+            b = args.layers * sum(w4a16_bytes(M, N, Kd) for _, N, Kd in CONFIG1)
         flops = args.layers * sum(2 * M * N * Kd for _, N, Kd in CONFIG1)
         gbps, tflops = b / (ms * 1e-3) / 1e9, flops / (ms * 1e-3) / 1e12
         res[label] = dict(M=M, ms=ms, GBps=gbps, TFLOPs=tflops, hbm_frac=gbps / HBM_PEAK_GBS,
@@ -714,6 +730,8 @@ def main() -> int:
         detail["w4a16_verify"] = {k: round(x, 4) for k, x in w4["verify"].items()}
         detail["w4a16_decode"] = {k: round(x, 4) for k, x in w4["decode"].items()}
         detail["w4a16_verify_int32_weights"] = {k: round(x, 4) for k, x in w4["verify_int32"].items()}
+        detail["w4a16_verify_7_launches"] = {k: round(x, 4) for k, x in w4["verify_7_launches"].items()}
+        detail["w4a16_decode_7_launches"] = {k: round(x, 4) for k, x in w4["decode_7_launches"].items()}
         detail["w4a16_verify_over_decode"] = round(w4["verify"]["ms"] / w4["decode"]["ms"], 4)
         detail["w4a16_verify_over_w8a8_decode"] = round(w4["verify"]["ms"] / d["ms"], 4)
         w48 = bench_w4a8(args, K, torch)

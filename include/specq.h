@@ -209,6 +209,28 @@ int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t ldq, int wq_
                 int block_m, int block_n, int num_warps, int split_k,
                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* Grouped W4A16: up to 4 GEMMs that share one fp16 activation (a, M, K, group) -- q, k and v,
+ * or gate and up -- in one launch, each with its own packed weight, group scales, output and N:
+ *   C_g[m, n] = fp16( sum_k a[m,k] * fp16(fp16(q_g[n,k]) * sc_g[n, k/group]) ),  n < N[g]
+ * Results are bit-identical to one specq_w4a16 call per member with the same split_k: every
+ * member keeps the split count its own call would use (split_k, or the automatic count of its
+ * N and K), and W4A16 results do not depend on the tiles.  When the members' automatic counts
+ * differ the members run as one launch each, in order on `stream`.  Otherwise the tiles are
+ * those of one GEMM of width sum(N) (the fused weight of bench_matmul.py:16 without fusing the
+ * tensors), each member's channel tiles starting a new tile.  A plan-mode grouped call runs the
+ * streaming kernel at the tiles of grid_m_max (no on-device menu).  No reference counterpart
+ * (the reference fuses the weights instead).
+ *   wq, ldq, sc, ld_sc, c, ldc, N  arrays of n_members entries (host memory); ldq may be NULL
+ *            for wq_layout 2
+ *   Other arguments as specq_w4a16, all members with the same wq_layout. */
+size_t specq_w4a16_grouped_workspace_size(int m_grid, int n_members, const int* N, int K, int block_m,
+                                          int block_n, int num_warps, int split_k);
+int specq_w4a16_grouped(const void* a, int64_t lda, int n_members, const void* const* wq, const int64_t* ldq,
+                        int wq_layout, const void* const* sc, const int64_t* ld_sc, void* const* c,
+                        const int64_t* ldc, const int* N, int M, int K, int group, int grid_m_max,
+                        const int32_t* plan, int block_m, int block_n, int num_warps, int split_k,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* W4A16 weight packed once at load time into 1 KB MFMA fragments (wq_layout 2 above): fragment
  * (b, t) of 128-wide K block b and 16-row tile t at (b * ceil(N/16) + t) KB; lane l's 16 bytes
  * hold row 16t + l%16 at k = 128b + 32*(l/16) + 8u + j as word u, nibble j at bits 4p..4p+3

@@ -207,12 +207,12 @@ int w4_plan_config(int layout, int m_grid, int N, int K, int split_k, W4Cfg* cfg
 }
 
 int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, int split_k, bool plan_mode,
-              W4Cfg* cfg) {
+              W4Cfg* cfg, bool allow_menu = true) {
   SPECQ_REQUIRE(layout >= 0 && layout <= 2, SPECQ_EINVAL, "w4a16: unknown weight layout %d", layout);
   SPECQ_REQUIRE(m_grid >= 0 && N > 0 && K > 0, SPECQ_EINVAL, "w4a16: bad sizes M=%d N=%d K=%d", m_grid, N, K);
   SPECQ_REQUIRE(K % 128 == 0, SPECQ_ENOTSUP, "w4a16: K=%d must be a multiple of 128", K);
   const int rows16 = ceil_div(m_grid > 0 ? m_grid : 1, 16);
-  if (plan_mode && block_m <= 0 && block_n <= 0 && g_w4a16_path.load() == 0)
+  if (allow_menu && plan_mode && block_m <= 0 && block_n <= 0 && g_w4a16_path.load() == 0)
     return w4_plan_config(layout, m_grid, N, K, split_k, cfg);
   int mt;
   if (block_m > 0) {
@@ -290,6 +290,49 @@ size_t w4_workspace(int m_grid, int N, int K, int block_m, int block_n, int spli
   }
   clear_error();
   return need;
+}
+
+// Split count of every member of a grouped launch (the caller's, or each member's own
+// w4_auto_splits, which must then agree), so each member sums K exactly as its own call would.
+// 0 when the members' automatic counts differ.
+int w4_group_splits(int n_members, const int* N, int K, int split_k) {
+  const int nb = K / 128;
+  int common = -1;
+  for (int g = 0; g < n_members; ++g) {
+    int s = split_k > 0 ? split_k : w4_auto_splits(N[g], nb);
+    if (s > nb) s = nb;
+    s = ceil_div(nb, ceil_div(nb, s));  // the count a call with this request runs
+    if (common >= 0 && s != common) return 0;
+    common = s;
+  }
+  return common;
+}
+
+// Tiles of a grouped launch: chosen as for one GEMM of the members' total width (never the
+// plan-mode menu: a plan-mode grouped call runs the streaming kernel at the tiles of its grid's
+// M, reading the active M on the device), every member with the common split count; each
+// member's channel tiles start a new tile, so the launch-wide tile count is the members' sum.
+int w4_group_config(int layout, int m_grid, int n_members, const int* N, int K, int block_m, int block_n,
+                    int splits, bool plan_mode, W4Cfg* cfg, int* tile_end) {
+  int64_t n_total = 0;
+  for (int g = 0; g < n_members; ++g) n_total += N[g];
+  SPECQ_REQUIRE(n_total <= INT32_MAX, SPECQ_EINVAL, "w4a16_grouped: total N too large");
+  int rc = w4_config(layout, m_grid, (int)n_total, K, block_m, block_n, splits, plan_mode, cfg, false);
+  if (rc) return rc;
+  const int BN = 64 * cfg->rw, BM = cfg->mt * 16;
+  int tiles = 0;
+  for (int g = 0; g < n_members; ++g) {
+    tiles += ceil_div(N[g], BN);
+    tile_end[g] = tiles;
+  }
+  cfg->n_tiles = tiles;
+  cfg->units = tiles * cfg->splits;
+  cfg->grid = chunked_grid(cfg->units, cfg->m_chunks);
+  cfg->ws_partials = cfg->splits > 1 ? align_up((size_t)cfg->m_chunks * tiles * cfg->splits * BM * BN * 4, 256) : 0;
+  cfg->ws_counters = cfg->splits > 1 ? kCounterBytes : 0;
+  SPECQ_REQUIRE((int64_t)cfg->m_chunks * tiles <= kMaxCounters, SPECQ_ENOTSUP,
+                "w4a16_grouped: %d x %d tiles exceed the counter region", cfg->m_chunks, tiles);
+  return SPECQ_OK;
 }
 
 }  // namespace
@@ -375,11 +418,106 @@ extern "C" int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t l
   p.counters = need ? (int32_t*)workspace : nullptr;
   p.partials = need ? (float*)((char*)workspace + kCounterBytes) : nullptr;
   p.vec_store = ((uintptr_t)c % 8 == 0) && (ldc % 4 == 0);
+  p.n_grp = 1;
   if (cfg.family == kW4Plan) {
     W4PlanParams pp;
     pp.p = p;
     for (int e = 0; e < kW4PlanRows; ++e) pp.t[e] = cfg.plan_t[e];
     return launch(cfg.fn, cfg.grid, kW4WsThreads, 0, (hipStream_t)stream, &pp);
+  }
+  return launch(cfg.fn, cfg.grid, cfg.family == kW4Rk ? 256 : kW4WsThreads, 0, (hipStream_t)stream, &p);
+}
+
+extern "C" size_t specq_w4a16_grouped_workspace_size(int m_grid, int n_members, const int* N, int K, int block_m,
+                                                     int block_n, int num_warps, int split_k) {
+  (void)num_warps;
+  if (n_members < 1 || n_members > kW4MaxGroup || N == nullptr || K <= 0 || K % 128 != 0) return 0;
+  for (int g = 0; g < n_members; ++g)
+    if (N[g] <= 0) return 0;
+  size_t need = 0;
+  const int splits = w4_group_splits(n_members, N, K, split_k);
+  if (n_members == 1 || splits == 0) {
+    for (int g = 0; g < n_members; ++g) need = std::max(need, w4_workspace(m_grid, N[g], K, block_m, block_n, split_k));
+    return need;
+  }
+  for (int plan_mode = 0; plan_mode < 2; ++plan_mode) {
+    W4Cfg cfg;
+    int tile_end[kW4MaxGroup];
+    if (w4_group_config(1, m_grid, n_members, N, K, block_m, block_n, splits, plan_mode != 0, &cfg, tile_end) ==
+        SPECQ_OK)
+      need = std::max(need, cfg.ws_partials + cfg.ws_counters);
+  }
+  clear_error();
+  return need;
+}
+
+extern "C" int specq_w4a16_grouped(const void* a, int64_t lda, int n_members, const void* const* wq,
+                                   const int64_t* ldq, int wq_layout, const void* const* sc, const int64_t* ld_sc,
+                                   void* const* c, const int64_t* ldc, const int* N, int M, int K, int group,
+                                   int grid_m_max, const int32_t* plan, int block_m, int block_n, int num_warps,
+                                   int split_k, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  SPECQ_REQUIRE(n_members >= 1 && n_members <= kW4MaxGroup, SPECQ_EINVAL,
+                "w4a16_grouped: %d GEMMs (1..%d supported)", n_members, kW4MaxGroup);
+  SPECQ_REQUIRE(wq && sc && c && ldc && N && ld_sc && (wq_layout == 2 || ldq), SPECQ_EINVAL,
+                "w4a16_grouped: null member array");
+  // Every member is checked as its own call would check it (the same entry point with M = 0
+  // launches nothing and returns after the checks).
+  for (int g = 0; g < n_members; ++g) {
+    const int rc = specq_w4a16(a, lda, wq[g], wq_layout == 2 ? 0 : ldq[g], wq_layout, sc[g], ld_sc[g], c[g], ldc[g],
+                               0, N[g], K, group, 0, nullptr, block_m, block_n, num_warps, split_k, nullptr, 0,
+                               stream);
+    if (rc) return rc;
+  }
+  SPECQ_REQUIRE(M >= 0, SPECQ_EINVAL, "w4a16_grouped: bad M=%d", M);
+  SPECQ_REQUIRE(grid_m_max == 0 || grid_m_max >= M, SPECQ_EINVAL, "w4a16_grouped: grid_m_max=%d < M=%d", grid_m_max, M);
+  const int m_grid = grid_m_max > 0 ? grid_m_max : M;
+  if (m_grid == 0) return SPECQ_OK;
+  const int splits = w4_group_splits(n_members, N, K, split_k);
+  if (n_members == 1 || splits == 0) {
+    // Members whose automatic split counts differ run as one launch each, in order on the
+    // stream (the workspace is reused: the last workgroup of a tile resets its counter).
+    for (int g = 0; g < n_members; ++g) {
+      const int rc = specq_w4a16(a, lda, wq[g], wq_layout == 2 ? 0 : ldq[g], wq_layout, sc[g], ld_sc[g], c[g],
+                                 ldc[g], M, N[g], K, group, grid_m_max, plan, block_m, block_n, num_warps, split_k,
+                                 workspace, workspace_bytes, stream);
+      if (rc) return rc;
+    }
+    return SPECQ_OK;
+  }
+  W4Cfg cfg;
+  int tile_end[kW4MaxGroup];
+  int rc = w4_group_config(wq_layout, m_grid, n_members, N, K, block_m, block_n, splits, plan != nullptr, &cfg,
+                           tile_end);
+  if (rc) return rc;
+  const size_t need = cfg.ws_partials + cfg.ws_counters;
+  SPECQ_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), SPECQ_ENOSPC,
+                "w4a16_grouped: workspace of %zu bytes required, %zu given", need, workspace ? workspace_bytes : 0);
+  auto row_bytes = [&](int g) -> int64_t { return wq_layout == 1 ? ldq[g] * 4 : (wq_layout == 0 ? ldq[g] : 0); };
+  auto vec_ok = [&](int g) { return ((uintptr_t)c[g] % 8 == 0) && (ldc[g] % 4 == 0) ? 1 : 0; };
+  W4A16Params p;
+  p.A = (const _Float16*)a; p.lda = lda; p.Wq = (const uint8_t*)wq[0]; p.ldq = row_bytes(0);
+  p.sc = (const _Float16*)sc[0]; p.ld_sc = ld_sc[0]; p.C = (_Float16*)c[0]; p.ldc = ldc[0]; p.plan = plan;
+  p.M = M; p.N = N[0]; p.K = K; p.m_grid = m_grid;
+  p.group_shift = __builtin_ctz((unsigned)group);
+  p.n_tiles = cfg.n_tiles; p.m_chunks = cfg.m_chunks; p.splits = cfg.splits; p.units = cfg.units;
+  p.nblocks = cfg.nblocks; p.bps = cfg.bps; p.ntiles16 = ceil_div(N[0], 16);
+  p.counters = need ? (int32_t*)workspace : nullptr;
+  p.partials = need ? (float*)((char*)workspace + kCounterBytes) : nullptr;
+  p.vec_store = vec_ok(0);
+  p.n_grp = n_members;
+  for (int g = 1; g < kW4MaxGroup; ++g) {
+    const bool on = g < n_members;
+    p.grp_tile_end[g - 1] = on ? tile_end[g - 1] : 0;
+    p.grp_Wq[g - 1] = on ? (const uint8_t*)wq[g] : nullptr;
+    p.grp_ldq[g - 1] = on ? row_bytes(g) : 0;
+    p.grp_sc[g - 1] = on ? (const _Float16*)sc[g] : nullptr;
+    p.grp_ld_sc[g - 1] = on ? ld_sc[g] : 0;
+    p.grp_C[g - 1] = on ? (_Float16*)c[g] : nullptr;
+    p.grp_ldc[g - 1] = on ? ldc[g] : 0;
+    p.grp_N[g - 1] = on ? N[g] : 0;
+    p.grp_ntiles16[g - 1] = on ? ceil_div(N[g], 16) : 0;
+    p.grp_vec_store[g - 1] = on ? vec_ok(g) : 0;
   }
   return launch(cfg.fn, cfg.grid, cfg.family == kW4Rk ? 256 : kW4WsThreads, 0, (hipStream_t)stream, &p);
 }

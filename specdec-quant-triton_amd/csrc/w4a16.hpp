@@ -33,6 +33,8 @@
 
 namespace specq {
 
+constexpr int kW4MaxGroup = 4;  // GEMMs of one grouped launch
+
 struct W4A16Params {
   const _Float16* A; int64_t lda;
   const uint8_t* Wq; int64_t ldq;  // row stride in bytes (layouts 0, 1)
@@ -49,7 +51,39 @@ struct W4A16Params {
   float* partials;       // [m_chunks][n_tiles][splits][BM][BN] when splits > 1
   int32_t* counters;     // [m_chunks][n_tiles]
   int vec_store;
+  // Grouped launch: n_grp GEMMs sharing A (and K, group, splits), member 0 in the fields
+  // above and member g >= 1 in grp_*[g - 1]; member g owns launch-wide channel tiles
+  // [grp_tile_end[g - 2] (0 for g = 0), grp_tile_end[g - 1]).
+  int n_grp;
+  int grp_tile_end[kW4MaxGroup - 1];
+  const uint8_t* grp_Wq[kW4MaxGroup - 1];
+  int64_t grp_ldq[kW4MaxGroup - 1];
+  const _Float16* grp_sc[kW4MaxGroup - 1];
+  int64_t grp_ld_sc[kW4MaxGroup - 1];
+  _Float16* grp_C[kW4MaxGroup - 1];
+  int64_t grp_ldc[kW4MaxGroup - 1];
+  int grp_N[kW4MaxGroup - 1], grp_ntiles16[kW4MaxGroup - 1], grp_vec_store[kW4MaxGroup - 1];
 };
+
+// Points the weight, scale and output fields of p at the GEMM of a grouped launch that owns
+// launch-wide channel tile `tile`, and returns the tile's index within that GEMM.  The member
+// is picked with scalar selects (the parameter block is never indexed dynamically).  Split-K
+// counters and partial tiles stay indexed by the launch-wide tile.
+__device__ __forceinline__ int w4_select_member(W4A16Params& p, int tile) {
+  if (p.n_grp <= 1) return tile;
+  int first = 0;
+#pragma unroll
+  for (int g = 1; g < kW4MaxGroup; ++g) {
+    if (g < p.n_grp && tile >= p.grp_tile_end[g - 1]) {  // g is a constant once unrolled
+      first = p.grp_tile_end[g - 1];
+      p.Wq = p.grp_Wq[g - 1]; p.ldq = p.grp_ldq[g - 1];
+      p.sc = p.grp_sc[g - 1]; p.ld_sc = p.grp_ld_sc[g - 1];
+      p.C = p.grp_C[g - 1]; p.ldc = p.grp_ldc[g - 1];
+      p.N = p.grp_N[g - 1]; p.ntiles16 = p.grp_ntiles16[g - 1]; p.vec_store = p.grp_vec_store[g - 1];
+    }
+  }
+  return tile - first;
+}
 
 
 // Two unsigned nibbles (bytes of y selected by sel) -> half2 of (nibble + 1024).
@@ -247,6 +281,8 @@ __device__ __forceinline__ void w4_splitk_finish(const W4A16Params& p, rsrc_t pr
 }
 
 // Epilogue shared by the families: store the wave's fp32 tiles, or hand them to split-K.
+// `tile` is the launch-wide channel tile (counters, partials); n0_wave - nl_wave is the first
+// channel of the tile within its GEMM.
 template <int MT, int RW, int BM, int BN>
 __device__ __forceinline__ void w4_epilogue(const W4A16Params& p, const v4f (&acc)[RW][MT], int mc, int tile, int split,
                                             int m0, int n0_wave, int nl_wave, int M, int* s_last) {
@@ -267,7 +303,7 @@ __device__ __forceinline__ void w4_epilogue(const W4A16Params& p, const v4f (&ac
   for (int i = 0; i < RW; ++i)
 #pragma unroll
     for (int j = 0; j < MT; ++j) w4_publish_quad<BM, BN>(prs, split, 16 * j + r, nl_wave + 16 * i + 4 * g, acc[i][j]);
-  w4_splitk_finish<BM, BN>(p, prs, cidx, m0, tile * BN, M, s_last);
+  w4_splitk_finish<BM, BN>(p, prs, cidx, m0, n0_wave - nl_wave, M, s_last);
 }
 
 }  // namespace specq

@@ -50,7 +50,8 @@ __global__ __launch_bounds__(256) void w4a16_rk_kernel(W4A16Params p) {
   if (m0 >= M) return;
 
   const int lane = lane_id(), w = uniform(wave_id()), g = lane >> 4, r = lane & 15;
-  const int n0 = tile * BN + w * BNW;  // first channel of this wave
+  const int ltile = w4_select_member(p, tile);  // tile within its GEMM (weights, outputs)
+  const int n0 = ltile * BN + w * BNW;  // first channel of this wave
   const int blk0 = split * p.bps;
   const int cnt = max(0, min(p.nblocks, blk0 + p.bps) - blk0);
   const int halfK = p.K / 2;

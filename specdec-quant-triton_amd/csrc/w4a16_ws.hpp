@@ -74,7 +74,8 @@ __device__ __forceinline__ void w4a16_ws_body(W4A16Params p, SlotPtr slot_ptr) {
 
   const int lane = lane_id(), wv = uniform(wave_id()), g = lane >> 4, r = lane & 15;
   const int h = wv >> 2, w = wv & 3;  // stream, channel group
-  const int n0 = tile * BN + w * BNW;
+  const int ltile = w4_select_member(p, tile);  // tile within its GEMM (weights, outputs)
+  const int n0 = ltile * BN + w * BNW;
   const int blk0 = split * p.bps;
   const int nblk = max(0, min(p.nblocks, blk0 + p.bps) - blk0);
   // Stream h holds the split's local blocks 2q + h, q = 0 .. nq_h - 1; both streams run
@@ -242,7 +243,7 @@ __device__ __forceinline__ void w4a16_ws_body(W4A16Params p, SlotPtr slot_ptr) {
       for (int j = 0; j < MT; ++j) w4_publish_quad<BM, BN>(prs, split, 16 * j + r, w * BNW + 16 * i + 4 * g, acc[i][j]);
   }
   // Every thread of the workgroup takes part in the arrival and the last one's finish.
-  w4_splitk_finish<BM, BN>(p, prs, cidx, m0, tile * BN, M, &s_last_ws4);
+  w4_splitk_finish<BM, BN>(p, prs, cidx, m0, ltile * BN, M, &s_last_ws4);
 }
 
 constexpr int kW4WsThreads = 512;

@@ -70,7 +70,7 @@ __all__ = [
     "silu_mul", "quantize_act_int8_gpu", "silu_mul_quant_int8", "paged_kv_append",
     "pack_int4_i32", "KernelInfo", "PackedWeightInt8", "pack_weight_int8", "PackedWeightInt4", "pack_weight_int4",
     "w4a8_matmul", "quantize_weight_int4_channel", "PackedWeightW4A8", "pack_weight_w4a8",
-    "w8a8_matmul_grouped",
+    "w8a8_matmul_grouped", "w4a16_matmul_grouped",
 ]
 
 
@@ -497,6 +497,78 @@ def w4a16_matmul(a, wp, sc, group=128, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK
               wptr, wbytes, _stream_ptr(a))
     _w4a16_kernel._note(a.device.index or 0, (bm, bn, layout))
     return out, KernelInfo(1, layout | (16 if plan is not None else 0), m_grid, N, K, bm, bn, 4, split_k)
+
+
+def w4a16_matmul_grouped(a, weights, group=128, outs=None, BLOCK_M=None, BLOCK_N=None, num_warps=4, plan=None,
+                         grid_m_max=None, split_k=0, workspace=None):
+    """Up to four W4A16 GEMMs that share one fp16 activation (q, k and v; gate and up) in one launch.
+
+    outs[g] = fp16(a @ dequant(wp_g, sc_g).T) for weights[g] = (wp_g, sc_g), bit-identical to one
+    w4a16_matmul call per GEMM with the same split_k.  The wp_g are all PackedWeightInt4, all int32
+    [N_g, K/8] or all uint8 [N_g, K/2].  The launch uses the tiles of one GEMM of width sum(N_g), as
+    the reference's fused qkv / gate_up weights do (bench_matmul.py:16), while the weights and
+    outputs stay separate; members whose automatic split counts differ run as one launch each.
+    Other arguments as w4a16_matmul.  Returns (outs, ck).
+    """
+    n = len(weights)
+    if not 1 <= n <= 4:
+        raise RuntimeError(f"w4a16_matmul_grouped: {n} GEMMs (1..4 supported)")
+    wps = [w for w, _ in weights]
+    if all(isinstance(w, PackedWeightInt4) for w in wps):
+        layout = 2
+    elif all(isinstance(w, torch.Tensor) and w.dtype == torch.int32 for w in wps):
+        layout = 1
+    elif all(isinstance(w, torch.Tensor) and w.dtype == torch.uint8 for w in wps):
+        layout = 0
+    else:
+        raise RuntimeError("w4a16_matmul_grouped: weights must all be PackedWeightInt4, all int32 [N, K/8] "
+                           "or all uint8 [N, K/2]")
+    scs = [sc for _, sc in weights]
+    _require_gpu(a, *scs)
+    if a.dtype != torch.float16 or any(sc.dtype != torch.float16 for sc in scs):
+        raise RuntimeError("w4a16_matmul_grouped expects fp16 activations and fp16 scales")
+    assert BLOCK_N is None or BLOCK_N in (64, 128)
+    M, K = a.shape
+    if layout == 2:
+        Ns = [w.N for w in wps]
+        if any(w.K != K for w in wps):
+            raise RuntimeError(f"w4a16_matmul_grouped: packed weight K does not match K={K}")
+        w_ptrs, w_lds = [w.data.data_ptr() for w in wps], [0] * n
+    else:
+        _require_gpu(*wps)
+        wps = [_rowmajor(w) for w in wps]
+        per = 2 if layout == 0 else 8
+        Ns = [int(w.shape[0]) for w in wps]
+        if any(w.shape[1] * per != K for w in wps):
+            raise RuntimeError(f"w4a16_matmul_grouped: packed weights do not match K={K}")
+        w_ptrs, w_lds = [w.data_ptr() for w in wps], [w.stride(0) for w in wps]
+    a = _rowmajor(a)
+    scs = [_rowmajor(sc) for sc in scs]
+    if a.data_ptr() % 16 or a.stride(0) % 8:
+        a = a.contiguous() if a.data_ptr() % 16 == 0 else a.clone()
+    if outs is None:
+        outs = [torch.empty((M, N), device=a.device, dtype=torch.float16) for N in Ns]
+    if len(outs) != n:
+        raise RuntimeError("w4a16_matmul_grouped: one output per GEMM")
+    for o, N in zip(outs, Ns):
+        if o.dtype != torch.float16 or o.stride(-1) != 1 or tuple(o.shape) != (M, N):
+            raise RuntimeError(f"w4a16_matmul_grouped: outputs must be fp16 [M, N] with unit inner stride, got "
+                               f"{tuple(o.shape)} for N={N}")
+    m_grid = int(grid_m_max) if grid_m_max is not None else M
+    bm = int(BLOCK_M) if BLOCK_M else 0
+    bn = 0 if not BLOCK_N else int(BLOCK_N)
+    arr = lambda ct, vals: (ct * n)(*vals)  # noqa: E731
+    n_arr = arr(ctypes.c_int, Ns)
+    ws = workspace or _ws.shared(a.device)
+    need = _lib.lib().specq_w4a16_grouped_workspace_size(m_grid, n, n_arr, K, bm, bn, 4, split_k)
+    wptr, wbytes = ws.ensure(need)
+    _lib.call("specq_w4a16_grouped", a.data_ptr(), a.stride(0), n, arr(ctypes.c_void_p, w_ptrs),
+              arr(ctypes.c_int64, w_lds), layout, arr(ctypes.c_void_p, [sc.data_ptr() for sc in scs]),
+              arr(ctypes.c_int64, [sc.stride(0) for sc in scs]), arr(ctypes.c_void_p, [o.data_ptr() for o in outs]),
+              arr(ctypes.c_int64, [o.stride(0) for o in outs]), n_arr, M, K, int(group), int(grid_m_max or 0),
+              _plan_ptr(plan), bm, bn, 4, split_k, wptr, wbytes, _stream_ptr(a))
+    _w4a16_kernel._note(a.device.index or 0, (bm, bn, "grouped", layout))
+    return outs, KernelInfo(1, layout | (16 if plan is not None else 0), m_grid, sum(Ns), K, bm, bn, 4, split_k)
 
 
 # ----------------------------------------------------------------------------------------

@@ -65,6 +65,10 @@ SIGNATURES = {
     "specq_w4a16": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_vp, _c_i64, _c_vp, _c_i64,
                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp,
                              _c_int, _c_int, _c_int, _c_int, _c_vp, _c_size, _c_vp]),
+    "specq_w4a16_grouped_workspace_size": (_c_size, [_c_int, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "specq_w4a16_grouped": (_c_int, [_c_vp, _c_i64, _c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                     _c_int, _c_int, _c_int, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp,
+                                     _c_size, _c_vp]),
     "specq_paged_attn_workspace_size": (_c_size, [_c_int] * 7),
     "specq_paged_attn": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64,
                                   _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
