@@ -4,7 +4,7 @@ config 1  W8A8, every M = 1..300 x BLOCK_M in {16, 32, 64, 128} on the four Llam
           shapes (the sweep of correctness.py:33-40 at the config shapes), row-major weights;
           load-time packed weights at the automatic tile for every M.  Bit-exact, and rows
           >= M of the output are never written.
-config 2  W4A16 at correctness.py:74's M list x BLOCK_M in {16, 32, 64, 128} on the four
+config 2  W4A16 at every M = 1..300 (correctness.py:74's list is a subset) x BLOCK_M in {16, 32, 64, 128} on the four
           shapes, int32 packing: relative Frobenius error < 2e-3 (correctness.py:77-79) and
           the elementwise bound |out - ref| <= 2**-10 |ref| + 2e-3 rms(ref); every BLOCK_M and
           the load-time packed weight bit-identical to the automatic tile; the reference's
@@ -39,7 +39,6 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 SENT = 0x7C01            # an fp16 NaN bit pattern: no finite result has it
 M_ALL = list(range(1, 301))
-W4_MS = list(range(1, 65)) + [72, 99, 128, 129, 200, 288, 300]   # correctness.py:74
 
 
 # ---------------------------------------------------------------------------------- config 1
@@ -99,12 +98,13 @@ def test_config2_w4a16_m_sweep_every_block_m(shape):
     wu = gen.pack_u8_reference(qu).to(DEV)
     a, sc = a.to(DEV), sc.to(DEV)
     wpk = K.pack_weight_int4(wi)
-    note(f"config2 w4a16 N={N} K={Kd} {len(W4_MS)} M x BLOCK_M in (auto, 16, 32, 64, 128)")
+    # Every M = 1..300 (correctness.py:74's list is a subset), as the W8A8 sweep above.
+    note(f"config2 w4a16 N={N} K={Kd} {len(M_ALL)} M x BLOCK_M in (auto, 16, 32, 64, 128)")
     auto = torch.empty((300, N), dtype=torch.float16, device=DEV)
     out = torch.empty((300, N), dtype=torch.float16, device=DEV)
-    fro = torch.zeros(len(W4_MS), 2, dtype=torch.float64, device=DEV)      # int32, uint8 layouts
-    excess = torch.zeros(len(W4_MS), 2, dtype=torch.float64, device=DEV)
-    differ = torch.zeros(len(W4_MS), dtype=torch.int64, device=DEV)
+    fro = torch.zeros(len(M_ALL), 2, dtype=torch.float64, device=DEV)      # int32, uint8 layouts
+    excess = torch.zeros(len(M_ALL), 2, dtype=torch.float64, device=DEV)
+    differ = torch.zeros(len(M_ALL), dtype=torch.int64, device=DEV)
 
     def tol(i, j, o, r):
         e = o.double() - r
@@ -112,7 +112,7 @@ def test_config2_w4a16_m_sweep_every_block_m(shape):
         rms = r.square().mean().sqrt()
         excess[i, j] = (e.abs() - (2.0 ** -10 * r.abs() + 2e-3 * rms)).max()
 
-    for i, M in enumerate(W4_MS):
+    for i, M in enumerate(M_ALL):
         K.w4a16_matmul(a[:M], wi, sc, out=auto[:M], BLOCK_M=None)
         tol(i, 0, auto[:M], ref[:M])
         for bm in (16, 32, 64, 128):
@@ -124,9 +124,9 @@ def test_config2_w4a16_m_sweep_every_block_m(shape):
         tol(i, 1, out[:M], ref[:M])
     torch.cuda.synchronize()
     fro, excess, differ = fro.cpu().numpy(), excess.cpu().numpy(), differ.cpu().numpy()
-    assert (fro < 2e-3).all(), f"rel-Frobenius {fro.max():.3e} at M={W4_MS[int(fro.max(1).argmax())]}"
+    assert (fro < 2e-3).all(), f"rel-Frobenius {fro.max():.3e} at M={M_ALL[int(fro.max(1).argmax())]}"
     assert (excess <= 0).all(), f"elementwise bound exceeded by {excess.max():.3e}"
-    assert not differ.any(), f"tiles or layouts differ from the automatic tile at M={[M for M, d in zip(W4_MS, differ) if d][:10]}"
+    assert not differ.any(), f"tiles or layouts differ from the automatic tile at M={[M for M, d in zip(M_ALL, differ) if d][:10]}"
     print(f"config2 N={N} K={Kd}: max rel-Frobenius {fro.max():.2e}")
 
 
