@@ -79,6 +79,38 @@ def test_w4a16_validation_errors(built_lib):
     assert f(*bad_group) in (-22, -95)
 
 
+def test_w4a16_grouped_validation_errors(built_lib):
+    import ctypes
+    from specq import _lib
+    L = _lib.lib()
+    arr = lambda ct, vals: (ct * len(vals))(*vals)  # noqa: E731
+    # Pointers are fake but aligned: every call below must fail before any launch.
+    wq, ldq = arr(ctypes.c_void_p, [16 * 1024] * 3), arr(ctypes.c_int64, [512] * 3)   # int32 [N, K/8]
+    sc, ldsc = arr(ctypes.c_void_p, [4096] * 3), arr(ctypes.c_int64, [32] * 3)
+    c, ldc = arr(ctypes.c_void_p, [8192] * 3), arr(ctypes.c_int64, [4096, 1024, 1024])
+    N = arr(ctypes.c_int, [4096, 1024, 1024])
+
+    def call(nm=3, M=72, K=4096, group=128, layout=1):
+        return L.specq_w4a16_grouped(16, K, nm, wq, ldq, layout, sc, ldsc, c, ldc, N, M, K, group, 0, None,
+                                     0, 0, 4, 0, None, 0, None)
+    assert call(nm=0) == -22
+    assert call(nm=5) == -22
+    assert "1..4" in L.specq_last_error().decode()
+    assert call(layout=3) == -22               # checked per member, as the one-GEMM call does
+    assert call(K=200) in (-22, -95)
+    assert call(group=48) in (-22, -95)
+    # q|k|v split K four ways each: the launch needs a workspace and is refused without one
+    assert call() == -28
+    # Workspace sizes: the split members' tiles, none for unsplit gate|up, and members whose
+    # automatic split counts differ take the largest of their own calls.
+    f = L.specq_w4a16_grouped_workspace_size
+    assert f(72, 3, N, 4096, 0, 0, 4, 0) > 256 * 1024
+    assert f(72, 0, N, 4096, 0, 0, 4, 0) == 0
+    assert f(72, 2, arr(ctypes.c_int, [14336, 14336]), 4096, 0, 0, 4, 0) == 0
+    assert f(72, 2, arr(ctypes.c_int, [4096, 14336]), 4096, 0, 0, 4, 0) == \
+        L.specq_w4a16_workspace_size(72, 4096, 4096, 0, 0, 4, 0)
+
+
 def test_attn_validation_errors(built_lib):
     from specq import _lib
     f = _lib.lib().specq_paged_attn
