@@ -345,7 +345,8 @@ def staircase_md(args) -> int:
 
 
 def staircase(args) -> int:
-    """W8A8 latency over M on the config-1 shapes (library tile choice and fixed BLOCK_M)."""
+    """W8A8 (or, with --kind w4a16, W4A16) latency over M on the config-1 shapes: the library's
+    tile choice at every M = 1..300 and fixed BLOCK_M at the staircase's edges."""
     import torch
 
     if PKG not in sys.path:
@@ -357,12 +358,20 @@ def staircase(args) -> int:
     shapes = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]
     bounds = [1, 8, 16, 17, 24, 32, 33, 48, 64, 65, 72, 96, 128, 129, 144, 160, 192, 256, 288, 300]
     res = {}
+    w4 = getattr(args, "kind", "w8a8") == "w4a16"
     for N, Kd in shapes:
-        copies = max(4, -(-600 * (1 << 20) // (N * Kd)))  # > 2x the Infinity Cache per cycle
-        ws = [K.pack_weight_int8(torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=g))
-              for _ in range(copies)]
-        sw = torch.rand((N,), device="cuda", generator=g) * 0.009 + 0.001
-        a = torch.randint(-127, 128, (300, Kd), dtype=torch.int8, device="cuda", generator=g)
+        wbytes = N * Kd // 2 if w4 else N * Kd
+        copies = max(4, -(-600 * (1 << 20) // wbytes))  # > 2x the Infinity Cache per cycle
+        if w4:  # INT4 weights packed at load, fp16 group scales and activations (config 2)
+            ws = [K.pack_weight_int4(torch.randint(-2 ** 31, 2 ** 31 - 1, (N, Kd // 8), dtype=torch.int32,
+                                                   device="cuda", generator=g)) for _ in range(copies)]
+            sw = (torch.rand((N, Kd // 128), device="cuda", generator=g) * 0.018 + 0.002).half()
+            a = torch.randn((300, Kd), device="cuda", generator=g).half()
+        else:
+            ws = [K.pack_weight_int8(torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=g))
+                  for _ in range(copies)]
+            sw = torch.rand((N,), device="cuda", generator=g) * 0.009 + 0.001
+            a = torch.randint(-127, 128, (300, Kd), dtype=torch.int8, device="cuda", generator=g)
         sa = torch.rand((300,), device="cuda", generator=g) * 0.015 + 0.005
         out = torch.empty((300, N), dtype=torch.float16, device="cuda")
         row = {}
@@ -370,10 +379,13 @@ def staircase(args) -> int:
             for M in (range(1, 301) if bm is None else bounds):
                 def run(M=M, bm=bm):
                     for w in ws:
-                        K.w8a8_matmul(a[:M], sa[:M], w, sw, out=out[:M], BLOCK_M=bm)
+                        if w4:
+                            K.w4a16_matmul(a[:M], w, sw, out=out[:M], BLOCK_M=bm)
+                        else:
+                            K.w8a8_matmul(a[:M], sa[:M], w, sw, out=out[:M], BLOCK_M=bm)
                 row.setdefault(str(bm or "auto"), {})[M] = round(_graph_us(run, copies, reps=3), 2)
         res[f"{N}x{Kd}"] = row
-        print(f"[staircase] {N}x{Kd} done", flush=True)
+        print(f"[staircase] {'w4a16' if w4 else 'w8a8'} {N}x{Kd} done", flush=True)
         del ws
         torch.cuda.empty_cache()
     with open(args.out, "w") as fh:
@@ -412,6 +424,7 @@ def main() -> int:
     sm.add_argument("json")
     c = sub.add_parser("staircase")
     c.add_argument("--out", required=True)
+    c.add_argument("--kind", choices=("w8a8", "w4a16"), default="w8a8")
     args = ap.parse_args()
     return {"probe": probe, "stats": stats, "traffic": traffic, "mfma": mfma, "staircase": staircase,
             "staircase-md": staircase_md, "sq": sq}[args.cmd](args)
