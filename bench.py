@@ -385,7 +385,7 @@ def bench_attention(args, K, torch):
         b = attn_bytes(B, L, ql, H, H_KV, D, 4)
         for name, qpp in (("fused", ql), ("qpp1", 1)):
             fn = lambda: K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=qpp, out=out)  # noqa: E731
-            ms = do_bench(fn, warmup=5, rep=20)
+            ms = do_bench(fn, warmup=5, rep=20, flush="clean")
             gbps = b / (ms * 1e-3) / 1e9
             res[f"ctx{ctx}_{name}"] = dict(us=ms * 1e3, GBps=gbps, hbm_frac=gbps / HBM_PEAK_GBS)
         # The same call after a zeroing-only flush (triton.testing.do_bench's): the dirty lines it
@@ -397,7 +397,7 @@ def bench_attention(args, K, torch):
             f"({res[f'ctx{ctx}_fused_dirty_flush']['us']:.1f} us after a zeroing-only flush)")
     # Floor of this timing method: an empty-bodied one-element launch between the same events.
     tiny = torch.zeros(1, device="cuda")
-    res["event_floor_us"] = do_bench(lambda: tiny.add_(1), warmup=5, rep=20) * 1e3
+    res["event_floor_us"] = do_bench(lambda: tiny.add_(1), warmup=5, rep=20, flush="clean") * 1e3
     # The step before attention: the k+1 new tokens' K/V quantised into the cache pages.
     for B in (args.B, 32):
         L = 4096 + ql
@@ -406,7 +406,7 @@ def bench_attention(args, K, torch):
         kn = torch.randn((B, ql, H_KV, D), generator=g).half().cuda()
         vn = torch.randn((B, ql, H_KV, D), generator=g).half().cuda()
         fn = lambda: K.paged_kv_append(kn, vn, kc, vc, ks, vs, bt, cl, ql)  # noqa: E731
-        ms = do_bench(fn, warmup=5, rep=50)
+        ms = do_bench(fn, warmup=5, rep=50, flush="clean")
         b = kv_append_bytes(B, ql, H_KV, D, 4)
         res[f"kv_append_B{B}"] = dict(us=ms * 1e3, GBps=b / (ms * 1e-3) / 1e9)
     log(f"kv append B={args.B}: {res[f'kv_append_B{args.B}']['us']:.1f} us")
@@ -596,13 +596,20 @@ def cpu_baseline(args, M: int, seconds: float):
       also    the reference test's fp32 formula on the same layer (correctness.py:37), W4A16
               x.float() @ deq.float().T on the same shapes (correctness.py:76), and dense fp32
               attention at B=8, k=8, ctx 4096 (kernels.py:289-309)
-    Threads: torch's intra-op pool as configured for the process (OMP_NUM_THREADS)."""
+    Threads: every CPU the process may run on (os.sched_getaffinity), capped by OMP_NUM_THREADS
+    where that is set -- the GPU box gives one GPU's job a share of 16 of the host's CPUs.
+    Both the host's CPU count and the threads used are reported."""
     import statistics as st
 
     import torch
 
     from oracle import cpu_baseline as C
 
+    host_cpus = os.cpu_count() or 1
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else host_cpus
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    cores = min(usable, int(omp)) if omp.isdigit() and int(omp) > 0 else usable
+    torch.set_num_threads(cores)
     cores = torch.get_num_threads()
     model = "unknown CPU"
     try:
@@ -657,7 +664,7 @@ def cpu_baseline(args, M: int, seconds: float):
     b_att = attn_bytes(8, 4096 + 9, 9, 32, 8, 128, 4)
     return dict(
         value=round(b_layer / t_int / 1e9, 3), unit="GB/s", cores=int(cores), kind="port",
-        cpu=model,
+        cpu=model, host_cpus=int(host_cpus), affinity_cpus=int(usable), omp_num_threads=omp or None,
         sample=(f"torch._int_mm + fp32 epilogue (oracle/cpu_baseline.py) over one Llama-3-8B layer's seven "
                 f"linears at M={M}: median {t_int * 1e3:.1f} ms of {n_int} reps; bytes counted as for the GPU step"),
         fp32_formula_layer_ms=round(t_f32 * 1e3, 2), fp32_formula_reps=n_f32,

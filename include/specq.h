@@ -288,8 +288,11 @@ int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64_t s_qh,
  * (RNE) or fp32.  Replaces the host-side q8 of make_paged_kv (kernels.py:265-286) with the
  * on-device step that runs before attention in a serving loop.
  *   k_new, v_new  fp16 [B_grid, ql_grid, H_KV, D], shared strides s_nb, s_nt, s_nh
- *                 (rows 16-byte aligned)
- *   kc, vc, ks, vs, block_tbl, ctx_len  as specq_paged_attn (cache rows 8-byte aligned);
+ *                 (rows 16-byte aligned).  Every workgroup of the [B_grid, ql_grid] grid
+ *                 reads its new K/V row and ctx_len[b] before it checks whether b and i are
+ *                 active, so k_new, v_new and ctx_len must cover all B_grid sequences and
+ *                 ql_grid tokens, in eager calls (n_seqs < B_grid) as in plan mode
+ *   kc, vc, ks, vs, block_tbl  as specq_paged_attn (cache rows 8-byte aligned);
  *                 n_pages = pages in the pool (rows naming a page outside [0, n_pages), or a
  *                 position outside [0, max_pages * PAGE), are skipped)
  *   plan     NULL, or device int32*: plan[0] = n_seqs, plan[1] = q_len (as specq_paged_attn)

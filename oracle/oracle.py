@@ -143,15 +143,14 @@ def w4a16(a, qu, sc, group: int = 128) -> np.ndarray:
 # ------------------------------------------------------------------------------------------
 # Paged verification attention (kernels.py:178-236, 289-309)
 # ------------------------------------------------------------------------------------------
-def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len: int, round_p_fp16: bool = False,
-                    magnitude: bool = False):
+def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len: int, magnitude: bool = False):
     """float64 dense restatement of paged_attention_ref (kernels.py:289-309).
 
     out[b, i, h] = sum_t softmax_t(q . k_t * ks_t / sqrt(D), t <= L - q_len + i) * v_t * vs_t
     with K/V gathered through the block table (page = bt[b, t // PAGE], slot = t % PAGE) and
-    the GQA group of query head h reading KV head h // G.  With round_p_fp16 the normalised
-    softmax weight times vs_t is rounded to fp16 as the kernel does before the PV product
-    (kernels.py:232), which is a per-term relative perturbation of at most 2**-11.
+    the GQA group of query head h reading KV head h // G.  The kernel rounds each normalised
+    softmax weight times vs_t to fp16 before the PV product (kernels.py:232), a per-term
+    relative perturbation of at most 2**-11 that the tests bound against `mag` below.
     Rows i >= q_len are left at zero.  Returns float64 [B, QLMAX, H, D]; with magnitude=True
     also mag[b, i, h] = sum_t p_t * |v_t * vs_t| (same shape), the scale against which the
     rounding of each p_t * vs_t term is measured (it bounds |out| and equals it when every
@@ -189,8 +188,6 @@ def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len: int, round_p_f
             den = e.sum(axis=1, keepdims=True)
             p = np.where(den > 0, e / np.where(den > 0, den, 1.0), 0.0)
             pv = p * v_sc[None, :, kh]
-            if round_p_fp16:
-                pv = pv.astype(np.float16).astype(np.float64)
             out[b, :q_len, kh * G:(kh + 1) * G, :] = (pv @ v_int[:, kh, :]).reshape(q_len, G, D)
             if magnitude:
                 mag[b, :q_len, kh * G:(kh + 1) * G, :] = (np.abs(pv) @ np.abs(v_int[:, kh, :])).reshape(q_len, G, D)

@@ -13,9 +13,10 @@
 //    program reads each K/V byte once for all (k+1) * G rows.
 //  * Split length follows the work on the device: a split is a whole number of 128-token
 //    units, as many as make (active sequences) x (KV heads) x (splits) reach the CU count for
-//    a sequence filling the block table, between 256 and 4096 tokens and at most 64 splits,
-//    the units spread evenly over the splits (attn_split_units).  It depends only on the block table's capacity and the number of
-//    active sequences, so a QPP=1 and a fused program, and an eager and a plan-mode call, cut
+//    a sequence filling the block table, at most 4096 tokens and at most 64 splits, and at
+//    least 256 tokens (384 once the block table holds 4096 tokens or more), the units spread
+//    evenly over the splits (attn_split_units).  It depends only on the block table's
+//    capacity and the number of active sequences, so a QPP=1 and a fused program, and an eager and a plan-mode call, cut
 //    a sequence at the same tokens, and the page ids of a split can be fetched before the
 //    sequence's length is known.
 //  * Eight waves (two per SIMD, so one wave's MFMA and LDS latencies hide behind the other's

@@ -180,6 +180,20 @@ def _rowmajor(t: torch.Tensor) -> torch.Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
+def _check_out(out: torch.Tensor, M: int, N: int, who: str) -> None:
+    """The kernels write rows < M and columns < N of out: it must hold at least that."""
+    if out.dim() != 2 or out.shape[0] < M or out.shape[1] < N:
+        raise RuntimeError(f"{who}: out {tuple(out.shape)} is smaller than [M, N] = [{M}, {N}]")
+
+
+def _check_w4_scales(sc: torch.Tensor, N: int, K: int, group: int, who: str) -> None:
+    """W4A16 scales are fp16 [N, K/group]; a smaller tensor would be read past its end."""
+    if group <= 0 or K % group:
+        raise RuntimeError(f"{who}: K={K} is not a multiple of group={group}")
+    if sc.dim() != 2 or tuple(sc.shape) != (N, K // group):
+        raise RuntimeError(f"{who}: scales {tuple(sc.shape)} must be [N, K/group] = [{N}, {K // group}]")
+
+
 def _plan_ptr(plan) -> int:
     if plan is None:
         return 0
@@ -253,10 +267,13 @@ def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK_K=12
         w_q = _rowmajor(w_q)
     sa = sa.float().contiguous()
     sw = sw.float().contiguous()
+    if sa.numel() < M or sw.numel() != N:
+        raise RuntimeError(f"w8a8_matmul: scales sa {tuple(sa.shape)} / sw {tuple(sw.shape)} do not cover M={M} / N={N}")
     if out is None:
         out = torch.empty((M, N), device=a_q.device, dtype=torch.float16)
     if out.dtype != torch.float16 or out.stride(-1) != 1:
         raise RuntimeError("w8a8_matmul: out must be fp16 with unit inner stride")
+    _check_out(out, M, N, "w8a8_matmul")
     m_grid = int(grid_m_max) if grid_m_max is not None else M
     bm = int(BLOCK_M) if BLOCK_M else 0  # 0: the library picks the tile (cost model over M, N, K)
     bn = _w8a8_block_n(BLOCK_N)
@@ -472,6 +489,7 @@ def w4a16_matmul(a, wp, sc, group=128, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK
         raise RuntimeError("w4a16_matmul: wp must be uint8 [N, K/2], int32 [N, K/8] or a PackedWeightInt4")
     if a.dtype != torch.float16 or sc.dtype != torch.float16:
         raise RuntimeError("w4a16_matmul expects fp16 activations and fp16 scales")
+    _check_w4_scales(sc, N, K, int(group), "w4a16_matmul")
     a, sc = _rowmajor(a), _rowmajor(sc)
     if layout == 2:
         w_ptr, w_ld = wp.data.data_ptr(), 0
@@ -485,6 +503,7 @@ def w4a16_matmul(a, wp, sc, group=128, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK
         out = torch.empty((M, N), device=a.device, dtype=torch.float16)
     if out.dtype != torch.float16 or out.stride(-1) != 1:
         raise RuntimeError("w4a16_matmul: out must be fp16 with unit inner stride")
+    _check_out(out, M, N, "w4a16_matmul")
     m_grid = int(grid_m_max) if grid_m_max is not None else M
     bm = int(BLOCK_M) if BLOCK_M else 0
     bn = 0 if not BLOCK_N else (64 if BLOCK_N <= 64 else 128)
@@ -542,6 +561,8 @@ def w4a16_matmul_grouped(a, weights, group=128, outs=None, BLOCK_M=None, BLOCK_N
         if any(w.shape[1] * per != K for w in wps):
             raise RuntimeError(f"w4a16_matmul_grouped: packed weights do not match K={K}")
         w_ptrs, w_lds = [w.data_ptr() for w in wps], [w.stride(0) for w in wps]
+    for sc, N in zip(scs, Ns):
+        _check_w4_scales(sc, N, K, int(group), "w4a16_matmul_grouped")
     a = _rowmajor(a)
     scs = [_rowmajor(sc) for sc in scs]
     if a.data_ptr() % 16 or a.stride(0) % 8:

@@ -8,7 +8,9 @@ HBM while it reads its own data: at B=8, k=8, ctx 4096 the paged attention measu
 after a zeroing flush, against 35.5 us after a flush that reads last, and 33.2 us with no
 flush.  The default flush therefore zeroes the buffer and then reads it back (a sum into one
 scalar), so the timed kernel starts with cold, clean caches, the state the reference's flush
-produced on its 2 MiB L2.  `flush="dirty"` keeps the zeroing-only flush for comparison.
+produced on its 2 MiB L2.  `do_bench` keeps triton.testing.do_bench's zeroing-only flush as
+its default (`flush="dirty"`), so the reference's bench scripts run through this drop-in
+measure what they measured before; `flush="clean"` asks for the zero-then-read flush.
 Each rep is bracketed by events on the current stream; the median is returned in
 milliseconds.  An empty kernel timed this way takes about 6.4 us (the events' own launch
 latency), a floor every figure from here carries.
@@ -38,10 +40,11 @@ def flush_cache(device=None, nbytes: int = 512 << 20, mode: str = "clean") -> No
         torch.sum(buf, dim=0, dtype=torch.int64, out=sink)
 
 
-def do_bench(fn, warmup: int = 10, rep: int = 40, flush="clean", return_mode: str = "median"):
-    """Median (or min / mean / all) event time of fn in ms; flush: "clean", "dirty" or False."""
+def do_bench(fn, warmup: int = 10, rep: int = 40, flush="dirty", return_mode: str = "median"):
+    """Median (or min / mean / all) event time of fn in ms; flush: "dirty" (zeroing only, as
+    triton.testing.do_bench), "clean" (zero, then read back) or False."""
     if flush is True:
-        flush = "clean"
+        flush = "dirty"
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()

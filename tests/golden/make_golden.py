@@ -16,6 +16,8 @@ import importlib.util
 import os
 import sys
 
+sys.dont_write_bytecode = True  # importing the reference must leave no __pycache__ in its tree
+
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))

@@ -119,3 +119,32 @@ def test_w4a16_grouped_argument_checks():
         K.w4a16_matmul_grouped(a, [mem[0], (torch.zeros((1024, 512), dtype=torch.int32, device=DEV), mem[1][1])])
     with pytest.raises(RuntimeError, match="outputs"):
         K.w4a16_matmul_grouped(a, mem, outs=[torch.empty((8, 4096), dtype=torch.float16, device=DEV)] * 3)
+    with pytest.raises(RuntimeError, match=r"\[N, K/group\]"):
+        K.w4a16_matmul_grouped(a, [mem[0], (mem[1][0], mem[1][1][:512]), mem[2]])
+    with pytest.raises(RuntimeError, match=r"\[N, K/group\]"):
+        K.w4a16_matmul(a, mem[0][0], mem[0][1][:, :16])
+
+
+@pytest.mark.parametrize("name", ["qkv", "ragged"])
+def test_w4a16_grouped_register_stream_path(name):
+    """The register-stream family (w4a16_path 1, 16- and 32-row tiles) in grouped launches: its
+    per-member selection and split-K column base run only there.  Each member must equal its
+    single call on the same family, tile and split count."""
+    from specq import _lib
+
+    Kd = GROUPS[name][0][1]
+    mem = [(w, sc) for w, sc, _ in members(name, 2, seed=81)]
+    a = gen.fp16_acts(64, Kd, seed=82, device=DEV)
+    try:
+        _lib.set_option("w4a16_path", 1)
+        for M in (1, 8, 20, 32):
+            for bm in (16, 32):
+                for sk in (1, 2):
+                    note(f"w4a16 grouped rk {name} M={M} BLOCK_M={bm} split_k={sk}")
+                    outs, _ = K.w4a16_matmul_grouped(a[:M], mem, BLOCK_M=bm, split_k=sk)
+                    refs = [K.w4a16_matmul(a[:M], w, sc, BLOCK_M=bm, split_k=sk)[0] for w, sc in mem]
+                    torch.cuda.synchronize()
+                    for g, (o, r) in enumerate(zip(outs, refs)):
+                        assert torch.equal(o, r), f"rk member {g} differs ({name} M={M} bm={bm} sk={sk})"
+    finally:
+        _lib.set_option("w4a16_path", 0)
