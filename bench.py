@@ -22,11 +22,15 @@ timed region starts.
                linears at M = 72 (the value), plus the fp32 formula, W4A16 and attention timings
   detail       the k=0 decode step (M = 8) and the verify/decode ratio (target <= 1.1); the same
                step as 7 separate launches per layer, on row-major weights, and on the fused
-               weights the reference benchmarks (bench_matmul.py:16); per-launch times; W4A16
-               and W4A8 steps; INT8 paged verification attention at B=8, k=8; the paged
-               KV-cache append; and the plan-buffer graph replay of the config-4 stack
+               weights the reference benchmarks (bench_matmul.py:16); per-launch times; the
+               per-layer t(B, k) / t(B, 0) grid of W8A8 and W4A16 (REPORT.md:71-78); W4A16 and
+               W4A8 steps; INT8 paged verification attention over the reference's B x k x QPP
+               grid at ctx 1024 and 4096 (bench_attention.py:16-39); the paged KV-cache append;
+               and the plan-buffer graph replay of the config-4 stack.  W8A8 launches, attention
+               and the KV append are all timed the same way: graphs of back-to-back launches
+               over distinct weights or caches, events on the stream the kernels run on
 
-Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-detail]
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-detail] [--write-grids DIR]
 """
 from __future__ import annotations
 
@@ -206,6 +210,7 @@ def per_launch_us(K, torch, layers, acts, M, outs, args):
 # Parts of the run
 # ------------------------------------------------------------------------------------------
 def bench_w8a8(args, K, torch):
+    from specq import grids
     g = torch.Generator(device="cuda").manual_seed(2)
     M_max = 300
     a = torch.randint(-127, 128, (M_max, 4096), dtype=torch.int8, device="cuda", generator=g)
@@ -239,6 +244,11 @@ def bench_w8a8(args, K, torch):
     M = res["verify"]["M"]
     res["launches"] = per_launch_us(K, torch, layers, acts, M, outs, args)
     res["launches_decode"] = per_launch_us(K, torch, layers, acts, args.B, outs, args)
+    if not args.no_detail:
+        # The reference's verification-cost table (REPORT.md:71-78): t(B, k) / t(B, 0) per layer.
+        flat = [[lw[m] for _, mem in LAUNCHES for m in mem] for lw in layers]
+        log("w8a8 layer grid B x k")
+        res["grid_us"], res["grid_ratio"] = grids.layer_ratio_grid(K, flat, "w8a8")
     del layers
     torch.cuda.empty_cache()
     # The same verification step on row-major weights (the reference's w_q layout).
@@ -267,12 +277,27 @@ def bench_w8a8(args, K, torch):
     return res
 
 
+def i32_to_u8_reference(wp):
+    """The same INT4 weight in the reference's uint8 layout (kernels.py:143-145): byte j of a
+    row holds k = j in its low nibble and k = j + K/2 in its high nibble; wp is int32 [N, K/8]
+    with nibble i of word j holding k = 8j + i."""
+    import torch
+
+    N = wp.shape[0]
+    q = torch.stack([(wp >> (4 * i)) & 0xF for i in range(8)], dim=-1).reshape(N, -1).to(torch.uint8)
+    half = q.shape[1] // 2
+    return (q[:, :half] | (q[:, half:] << 4)).contiguous()
+
+
 def bench_w4a16(args, K, torch):
     """W4A16 (config 2) over the seven config-1 linears, M = 72 and 8: INT4 weights (int32, 8
     nibbles per word) packed once at load into MFMA fragments (pack_weight_int4).  The step runs
     q|k|v and gate|up as grouped launches over their separate weights (w4a16_matmul_grouped,
     bit-identical to one call per linear), 4 launches per layer like the W8A8 step; the same step
-    as 7 launches per layer, and the grouped step on the int32 weights as given, go beside it."""
+    as 7 launches per layer, and the grouped step on the int32 and the reference's uint8 weights
+    as given, go beside it, with the per-layer t(B, k) / t(B, 0) grid."""
+    from specq import grids
+
     g = torch.Generator(device="cuda").manual_seed(3)
     layers, raw = [], []
     for _ in range(args.layers):
@@ -290,9 +315,11 @@ def bench_w4a16(args, K, torch):
     shape = {n: (N, Kd) for n, N, Kd in CONFIG1}
     res = {}
     vM, dM = args.B * (args.k + 1), args.B
+    raw_u8 = [{name: (i32_to_u8_reference(wp), sc) for name, (wp, sc) in lr.items()} for lr in raw]
     for label, M, ls, grouped in (("verify", vM, layers, True), ("decode", dM, layers, True),
                                   ("verify_7_launches", vM, layers, False), ("decode_7_launches", dM, layers, False),
-                                  ("verify_int32", vM, raw, True)):
+                                  ("verify_int32", vM, raw, True), ("verify_uint8", vM, raw_u8, True),
+                                  ("decode_uint8", dM, raw_u8, True)):
         def step():
             for lw in ls:
                 if grouped:
@@ -319,7 +346,10 @@ def bench_w4a16(args, K, torch):
         res[label] = dict(M=M, ms=ms, GBps=gbps, TFLOPs=tflops, hbm_frac=gbps / HBM_PEAK_GBS,
                           mfma_frac=tflops / FP16_MFMA_PEAK_TFLOPS)
         del graph
-    del layers, raw
+    log("w4a16 layer grid B x k")
+    flat = [[lw[m] for _, mem in LAUNCHES for m in mem] for lw in layers]
+    res["grid_us"], res["grid_ratio"] = grids.layer_ratio_grid(K, flat, "w4a16")
+    del layers, raw, raw_u8
     torch.cuda.empty_cache()
     return res
 
@@ -370,46 +400,59 @@ def bench_w4a8(args, K, torch):
 
 
 def bench_attention(args, K, torch):
-    """INT8 paged verification attention (config 3): B=8, k=8, context 4096, fused vs QPP=1."""
-    from specq import gen
+    """INT8 paged verification attention (config 3) and the paged KV-cache append.
+
+    The grid of the reference's attention benchmark (bench_attention.py:16-39): B in
+    {1, 2, 4, 8, 16, 32} x k = 0..8 x QPP in {1, k + 1} at context 1024 and 4096, each point the
+    mean launch of a graph of back-to-back launches over distinct caches (specq/grids.py), so
+    every launch reads HBM and no per-call event overhead is counted; fractions are algorithmic
+    bytes / time against 8 TB/s.  The B = 8, k = 8 point is also timed the reference's way
+    (events around each call after triton.testing.do_bench's zeroing flush), for comparison
+    with its published figures only."""
+    from specq import gen, grids
     from specq.timing import do_bench
 
     H, H_KV, D = 32, 8, 128
-    res = {}
+    res = {"grid": {}}
+    B, ql = args.B, args.k + 1
     for ctx in (1024, 4096):
-        B, ql = args.B, args.k + 1
+        log(f"attention grid ctx={ctx}")
+        g = grids.attention_grid(K, ctx, H=H, H_KV=H_KV, D=D)
+        res["grid"][ctx] = g
+        for name, qpp in (("fused", ql), ("qpp1", 1)):
+            r = g[(B, args.k, qpp)]
+            res[f"ctx{ctx}_{name}"] = dict(us=r["us"], GBps=r["GBps"], hbm_frac=r["frac"], kv_GBps=r["kv_GBps"])
+        log(f"attention B={B} k={args.k} ctx={ctx}: fused {res[f'ctx{ctx}_fused']['us']:.1f} us in a graph, "
+            f"QPP=1 {res[f'ctx{ctx}_qpp1']['us']:.1f} us")
+        # The reference's own method on the same call: events around each call, zeroing flush.
         L = ctx + ql
-        kc, vc, ks, vs, bt, cl = (t.cuda() for t in gen.paged_kv(B, [L] * B, H_KV, D, seed=5))
+        kc, vc, ks, vs, bt, cl = grids.make_caches(B, L, H_KV, D, 1, seed=5)[0]
         q = gen.queries(B, ql, H, D, seed=6).cuda()
         out = torch.zeros_like(q)
-        b = attn_bytes(B, L, ql, H, H_KV, D, 4)
-        for name, qpp in (("fused", ql), ("qpp1", 1)):
-            fn = lambda: K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=qpp, out=out)  # noqa: E731
-            ms = do_bench(fn, warmup=5, rep=20, flush="clean")
-            gbps = b / (ms * 1e-3) / 1e9
-            res[f"ctx{ctx}_{name}"] = dict(us=ms * 1e3, GBps=gbps, hbm_frac=gbps / HBM_PEAK_GBS)
-        # The same call after a zeroing-only flush (triton.testing.do_bench's): the dirty lines it
-        # leaves are written back while the kernel reads, so this figure carries that traffic.
         fn = lambda: K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=ql, out=out)  # noqa: E731
         ms = do_bench(fn, warmup=5, rep=20, flush="dirty")
-        res[f"ctx{ctx}_fused_dirty_flush"] = dict(us=ms * 1e3, GBps=b / (ms * 1e-3) / 1e9)
-        log(f"attention ctx={ctx}: fused {res[f'ctx{ctx}_fused']['us']:.1f} us "
-            f"({res[f'ctx{ctx}_fused_dirty_flush']['us']:.1f} us after a zeroing-only flush)")
-    # Floor of this timing method: an empty-bodied one-element launch between the same events.
-    tiny = torch.zeros(1, device="cuda")
-    res["event_floor_us"] = do_bench(lambda: tiny.add_(1), warmup=5, rep=20, flush="clean") * 1e3
-    # The step before attention: the k+1 new tokens' K/V quantised into the cache pages.
-    for B in (args.B, 32):
+        res[f"ctx{ctx}_fused_reference_method"] = dict(us=ms * 1e3)
+        del kc, vc, ks, vs, bt, cl
+        torch.cuda.empty_cache()
+    # The step before attention: the k+1 new tokens' K/V quantised into the cache pages, a graph
+    # over distinct caches (each append touches one page per sequence and head).
+    for Bx in (B, 32):
         L = 4096 + ql
-        kc, vc, ks, vs, bt, cl = (t.cuda() for t in gen.paged_kv(B, [L] * B, H_KV, D, seed=7))
-        g = torch.Generator().manual_seed(8)
-        kn = torch.randn((B, ql, H_KV, D), generator=g).half().cuda()
-        vn = torch.randn((B, ql, H_KV, D), generator=g).half().cuda()
-        fn = lambda: K.paged_kv_append(kn, vn, kc, vc, ks, vs, bt, cl, ql)  # noqa: E731
-        ms = do_bench(fn, warmup=5, rep=50, flush="clean")
-        b = kv_append_bytes(B, ql, H_KV, D, 4)
-        res[f"kv_append_B{B}"] = dict(us=ms * 1e3, GBps=b / (ms * 1e-3) / 1e9)
-    log(f"kv append B={args.B}: {res[f'kv_append_B{args.B}']['us']:.1f} us")
+        copies = 64
+        caches = grids.make_caches(Bx, L, H_KV, D, copies, seed=7)
+        gq = torch.Generator(device="cuda").manual_seed(8)
+        kn = torch.randn((Bx, ql, H_KV, D), device="cuda", generator=gq).half()
+        vn = torch.randn((Bx, ql, H_KV, D), device="cuda", generator=gq).half()
+
+        def run(caches=caches, kn=kn, vn=vn):
+            for kc, vc, ks, vs, bt, cl in caches:
+                K.paged_kv_append(kn, vn, kc, vc, ks, vs, bt, cl, ql)
+        us = grids.graph_us(run, copies)
+        b = kv_append_bytes(Bx, ql, H_KV, D, 4)
+        res[f"kv_append_B{Bx}"] = dict(us=us, GBps=b / (us * 1e-6) / 1e9)
+        del caches
+        torch.cuda.empty_cache()
+    log(f"kv append B={B}: {res[f'kv_append_B{B}']['us']:.2f} us in a graph")
     return res
 
 
@@ -697,6 +740,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-detail", action="store_true")
+    ap.add_argument("--write-grids", metavar="DIR", help="also write the B x k grids as markdown tables into DIR")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -732,11 +776,20 @@ def main() -> int:
               "w8a8_launch_us_M%d" % args.B: {k: dict(us=round(r["us"], 3), GBps=round(r["GBps"], 1))
                                               for k, r in w["launches_decode"].items()},
               "dominant_kernel": dict(name=dom["kernel"], us=round(dom["us"], 3), **dom["config"])}
+    if "grid_us" in w:
+        detail["w8a8_layer_grid"] = {"us": {str(b): {f"k{k}": round(v, 2) for k, v in r.items()} for b, r in w["grid_us"].items()},
+                                     "ratio": {str(b): {f"k{k}": round(v, 3) for k, v in r.items()}
+                                               for b, r in w["grid_ratio"].items()}}
     if not args.no_detail:
         w4 = bench_w4a16(args, K, torch)
         detail["w4a16_verify"] = {k: round(x, 4) for k, x in w4["verify"].items()}
         detail["w4a16_decode"] = {k: round(x, 4) for k, x in w4["decode"].items()}
         detail["w4a16_verify_int32_weights"] = {k: round(x, 4) for k, x in w4["verify_int32"].items()}
+        detail["w4a16_verify_uint8_weights"] = {k: round(x, 4) for k, x in w4["verify_uint8"].items()}
+        detail["w4a16_decode_uint8_weights"] = {k: round(x, 4) for k, x in w4["decode_uint8"].items()}
+        detail["w4a16_layer_grid"] = {"us": {str(b): {f"k{k}": round(v, 2) for k, v in r.items()} for b, r in w4["grid_us"].items()},
+                                      "ratio": {str(b): {f"k{k}": round(v, 3) for k, v in r.items()}
+                                                for b, r in w4["grid_ratio"].items()}}
         detail["w4a16_verify_7_launches"] = {k: round(x, 4) for k, x in w4["verify_7_launches"].items()}
         detail["w4a16_decode_7_launches"] = {k: round(x, 4) for k, x in w4["decode_7_launches"].items()}
         detail["w4a16_verify_over_decode"] = round(w4["verify"]["ms"] / w4["decode"]["ms"], 4)
@@ -747,11 +800,32 @@ def main() -> int:
         detail["w4a8_verify_over_decode"] = round(w48["verify"]["ms"] / w48["decode"]["ms"], 4)
         attn = bench_attention(args, K, torch)
         detail["attention_B8_k8"] = {k: {kk: round(x, 4 if kk.endswith("frac") else 2) for kk, x in r.items()}
-                                     for k, r in attn.items() if isinstance(r, dict) and not k.startswith("kv_append")}
-        detail["event_timing_floor_us"] = round(attn["event_floor_us"], 2)
+                                     for k, r in attn.items() if k.startswith("ctx")}
+        # µs per launch in a graph, B down, k = 0..8 across (config 3), fused and QPP = 1.
+        detail["attention_grid_us"] = {
+            f"ctx{ctx}": {mode: {str(Bx): [round(g[(Bx, kk, (kk + 1) if mode == "fused" else 1)]["us"], 1)
+                                           for kk in range(9)]
+                                 for Bx in sorted({b for b, _, _ in g})}
+                          for mode in ("fused", "qpp1")}
+            for ctx, g in attn["grid"].items()}
+        detail["attention_grid_hbm_frac_fused"] = {
+            f"ctx{ctx}": {str(Bx): [round(g[(Bx, kk, kk + 1)]["frac"], 3) for kk in range(9)]
+                          for Bx in sorted({b for b, _, _ in g})}
+            for ctx, g in attn["grid"].items()}
         detail["kv_append_k8"] = {k: {kk: round(x, 2) for kk, x in r.items()}
                                   for k, r in attn.items() if k.startswith("kv_append")}
         detail["plan_graph_4layer"] = {k: round(x, 4) for k, x in bench_plan_graph(args, K, torch).items()}
+
+    if args.write_grids and not args.no_detail:
+        from specq import grids
+        os.makedirs(args.write_grids, exist_ok=True)
+        cmd = "python bench.py " + " ".join(sys.argv[1:])
+        for name, us, ratio in (("w8a8", w["grid_us"], w["grid_ratio"]), ("w4a16", w4["grid_us"], w4["grid_ratio"])):
+            with open(os.path.join(args.write_grids, f"{name}_layer_grid.md"), "w") as fh:
+                fh.write(f"Command: `{cmd}`\n\n{grids.ratio_grid_md(us, ratio, name.upper())}\n")
+        for ctx, g in attn["grid"].items():
+            with open(os.path.join(args.write_grids, f"attention_grid_ctx{ctx}.md"), "w") as fh:
+                fh.write(f"Command: `{cmd}`\n\n{grids.attention_grid_md(g, ctx)}\n")
 
     cpu = None
     if not args.no_cpu:

@@ -168,6 +168,7 @@ extern "C" int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   p.counters = need ? (int32_t*)workspace : nullptr;
   p.part = need ? (float*)((char*)workspace + kCounterBytes) : nullptr;
+  diag_timeline(&p.tl, &p.tl_cap);
   void* args[] = {&p};
   hipError_t e = hipLaunchKernel(fn, dim3((unsigned)wgs), dim3(kAttnThreads), args, 0, (hipStream_t)stream);
   if (e != hipSuccess) {

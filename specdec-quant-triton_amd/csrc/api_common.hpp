@@ -55,4 +55,8 @@ int ensure_lds(const void* fn, size_t lds);
 // Number of CUs of the current device (cached per device).
 int device_cus();
 
+// Timestamp buffer the kernels of the diagnostics build write (specq_diag_set_timeline);
+// null, and never set, in the product build.
+void diag_timeline(uint64_t** tl, int* cap);
+
 }  // namespace specq

@@ -632,6 +632,7 @@ int run_w8a8(int layout, const int8_t* a, int64_t lda, const W8A8Group& grp, con
   p.counters = need ? reinterpret_cast<int32_t*>(workspace) : nullptr;
   p.partials = need ? reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + kCounterBytes) : nullptr;
   p.vec_store = vec_store(grp.c[0], grp.ldc[0], grp.sw[0]);
+  diag_timeline(&p.tl, &p.tl_cap);
   p.n_grp = grp.n;
   int tile_end = 0;
   for (int g = 0; g < grp.n; ++g) {

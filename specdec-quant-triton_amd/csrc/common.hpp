@@ -222,6 +222,29 @@ __device__ __forceinline__ void wg_barrier_lds() {
   wg_barrier();
 }
 
+// Per-workgroup timestamps, compiled only into the diagnostics build of the library
+// (-DSPECQ_DIAG, libspecq_diag.so): thread 0 of workgroup b stores s_memrealtime (a 100 MHz
+// clock) at tl[b * kTlMarks + i] with an ordinary vector store.  In the product build the
+// kernels' tl pointer stays null and this compiles to nothing.
+constexpr int kTlMarks = 16;
+__device__ __forceinline__ void tl_mark(uint64_t* tl, int cap, int i) {
+#ifdef SPECQ_DIAG
+  if (tl != nullptr && threadIdx.x == 0 && (int)blockIdx.x < cap)
+    tl[(int64_t)blockIdx.x * kTlMarks + i] = __builtin_amdgcn_s_memrealtime();
+#else
+  (void)tl; (void)cap; (void)i;
+#endif
+}
+// The same from lane 0 of every wave: wave w writes mark i + w (marks 8.. hold per-wave times).
+__device__ __forceinline__ void tl_mark_wave(uint64_t* tl, int cap, int i) {
+#ifdef SPECQ_DIAG
+  if (tl != nullptr && (threadIdx.x & 63) == 0 && (int)blockIdx.x < cap)
+    tl[(int64_t)blockIdx.x * kTlMarks + i + (int)(threadIdx.x >> 6)] = __builtin_amdgcn_s_memrealtime();
+#else
+  (void)tl; (void)cap; (void)i;
+#endif
+}
+
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).
 template <int B, int E, class F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -248,11 +271,24 @@ __device__ __forceinline__ void wait_all_memory() {
   __builtin_amdgcn_s_waitcnt(0);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
+// Diagnostics build: mark i once every memory operation this wave issued has completed
+// (thread 0's wave: in the kernels below that is the wave whose stores finish the tile).
+__device__ __forceinline__ void tl_mark_drained(uint64_t* tl, int cap, int i) {
+#ifdef SPECQ_DIAG
+  wait_all_memory();
+  tl_mark(tl, cap, i);
+#else
+  (void)tl; (void)cap; (void)i;
+#endif
+}
+
 // Called by every thread after the workgroup's publish() calls: returns true in the last
 // workgroup to arrive (of `expected`) at counter `ctr`, which is then reset to zero.
 // The caller reads the published values with collect() only when this returns true.
-__device__ __forceinline__ bool arrive_last(int32_t* ctr, int expected, int* s_flag) {
+__device__ __forceinline__ bool arrive_last(int32_t* ctr, int expected, int* s_flag, uint64_t* tl = nullptr,
+                                            int tl_cap = 0) {
   wait_all_memory();
+  tl_mark(tl, tl_cap, 5);  // diagnostics build: this wave's published values acknowledged
   __syncthreads();
   if (threadIdx.x == 0) {
     const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -261,6 +297,7 @@ __device__ __forceinline__ bool arrive_last(int32_t* ctr, int expected, int* s_f
     *s_flag = last;
   }
   __syncthreads();
+  tl_mark(tl, tl_cap, 6);  // diagnostics build: the arrival count has come back
   const bool last = *s_flag != 0;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   return last;

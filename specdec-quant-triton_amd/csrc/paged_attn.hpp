@@ -70,6 +70,8 @@ struct AttnParams {
   float scale_log2;    // sm_scale * log2(e)
   float* part;         // [progs][n_splits][rows][D] unnormalised O, then [progs][n_splits][rows][2] (m, l)
   int32_t* counters;   // [progs]
+  uint64_t* tl;        // diagnostics build only: per-workgroup timestamps (null otherwise)
+  int tl_cap;          // workgroups tl has room for
 };
 
 
@@ -216,6 +218,7 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
   static_assert(RB >= 1 && RB <= NS && HALF <= SLOT, "merge block halves fit a ring slot");
   static_assert((NS - 1) * NVM <= 63, "vmcnt range");
   static_assert(NS == 4, "four ring variables");
+  tl_mark(p.tl, p.tl_cap, 0);  // diagnostics build: workgroup start
 
   int n_seqs = p.n_seqs, q_len = p.q_len;
   if (p.plan != nullptr) {
@@ -309,6 +312,7 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
   // Page ids and Q fragments arrive together (one memory round trip); Q goes to LDS before any
   // DMA is issued, so no LDS store ever waits behind the ring's DMA.
   wait_vmcnt<0>();
+  tl_mark(p.tl, p.tl_cap, 1);  // diagnostics build: page ids, Q and the length have landed
 #pragma unroll
   for (int i = 0; i < QF; ++i) {
     const int f = threadIdx.x + NT * i;
@@ -572,6 +576,7 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
   if constexpr (PIPE) {
     Staged st[2];
     wait_vmcnt<(NS - 2) * NVM>();  // chunk 0 has landed
+    tl_mark(p.tl, p.tl_cap, 2);    // diagnostics build: first chunk landed
     if (n_it > 0) stage_a(std::integral_constant<int, 1 % NS>{}, st[0]);
     for (int base = 0; base < n_it; base += NS) {
       static_for<0, NS>([&](auto ic) __attribute__((always_inline)) {
@@ -600,6 +605,8 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
   }
   // Every DMA has landed before the ring is reused for the merge.
   wait_vmcnt<0>();
+  tl_mark(p.tl, p.tl_cap, 3);       // diagnostics build: chunk loop done (wave 0)
+  tl_mark_wave(p.tl, p.tl_cap, 8);  // ... and per wave (marks 8..15)
 
   // ---- Merge the eight waves.  Row statistics first; every wave's O is scaled to the
   // workgroup's row max.  Wave pair (v, v + 4) shares a merge region: row block rb in ring
@@ -617,6 +624,7 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
     }
   }
   __syncthreads();
+  tl_mark(p.tl, p.tl_cap, 7);  // diagnostics build: every wave's chunk loop done
   constexpr int QPR = D / 4;  // 4-float granules per row
   float wsc[RB];
 #pragma unroll
@@ -702,6 +710,7 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
               (_Float16)f32_opaque(v.w)};
   };
 
+  tl_mark(p.tl, p.tl_cap, 4);  // diagnostics build: waves merged
   if (n_active == 1) {
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
@@ -712,6 +721,7 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
       const float inv = (l == 0.f) ? 0.f : 1.f / l;
       store_row4(e, o[it] * inv);
     }
+    tl_mark_drained(p.tl, p.tl_cap, 6);  // diagnostics build: output stored
     return;
   }
 
@@ -734,7 +744,11 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
     publish(mlp, mx);
     publish(mlp + 1, l);
   }
-  if (!arrive_last(p.counters + prog, n_active, &s_last)) return;
+  tl_mark(p.tl, p.tl_cap, 5);  // diagnostics build: partials issued
+  if (!arrive_last(p.counters + prog, n_active, &s_last, p.tl, p.tl_cap)) {
+    tl_mark(p.tl, p.tl_cap, 6);  // diagnostics build: hand-off done (not the last split)
+    return;
+  }
   // Row weights of the splits, exp2(m_s - max) / l (l summed in split order), in LDS (the first
   // ring, no longer read).  Up to 16 splits the (m, l) pairs are loaded once, all in flight
   // together; more splits take a second pass.
@@ -802,6 +816,7 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
 #pragma unroll
   for (int it = 0; it < ITEMS; ++it)
     if (ivalid[it]) store_row4(threadIdx.x + NT * it, o[it]);
+  tl_mark_drained(p.tl, p.tl_cap, 6);  // diagnostics build: splits merged and stored
 }
 
 // The ring slots are separate LDS variables (see the schedule notes); Q fragments are staged

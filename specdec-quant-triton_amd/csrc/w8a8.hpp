@@ -53,6 +53,8 @@ struct W8A8Params {
   int64_t grp_ldc[3];
   int grp_N[3];
   int grp_vec_store[3];
+  uint64_t* tl;        // diagnostics build only: per-workgroup timestamps (null otherwise)
+  int tl_cap;          // workgroups tl has room for
 };
 constexpr int kW8A8MaxGroup = 4;
 
@@ -218,7 +220,7 @@ __device__ __forceinline__ void w8a8_publish_quad(rsrc_t prs, int split, int ml,
 template <int BM, int BN, int NT>
 __device__ __forceinline__ void w8a8_splitk_finish(const W8A8Params& p, rsrc_t prs, int cidx, int m0, int nbase,
                                                    int M, int* s_last) {
-  if (!arrive_last(p.counters + cidx, p.splits, s_last)) return;
+  if (!arrive_last(p.counters + cidx, p.splits, s_last, p.tl, p.tl_cap)) return;
   constexpr int QUADS = BM * BN / 4;
   constexpr int QPT = (QUADS + NT - 1) / NT;                   // quads per thread
   // Up to 8 quads per thread are summed in one round of loads (up to 32 loads in flight);
@@ -259,6 +261,7 @@ __device__ __forceinline__ void w8a8_splitk_finish(const W8A8Params& p, rsrc_t p
 #pragma unroll
         for (int u = 0; u < SB; ++u) s[i] += t[i][u];
     }
+    if (g0 == 0) tl_mark(p.tl, p.tl_cap, 7);  // diagnostics build: first group of partials summed
 #pragma unroll
     for (int i = 0; i < QG; ++i)
       if (ok[i]) w8a8_store4s(p, m0 + ml[i], nbase + nl[i], s[i], a[i], w[i]);

@@ -56,6 +56,7 @@ __device__ __forceinline__ void w8a8_rk_body(W8A8Params p) {
   using C = W8A8RkCfg<MT, RW, KW, NW>;
   constexpr int CW = C::CW, BM = C::BM, BNW = C::BNW, BN = C::BN, NS = C::NS, D = C::D, PER = C::PER;
   extern __shared__ __attribute__((aligned(16))) int32_t smem_rk[];
+  tl_mark(p.tl, p.tl_cap, 0);  // diagnostics build: workgroup start
 
   int mc, unit;
   if (!chunked_unit(p.m_chunks, p.n_tiles * p.splits, mc, unit)) return;
@@ -156,6 +157,9 @@ __device__ __forceinline__ void w8a8_rk_body(W8A8Params p) {
       issue(it * NS + t + D, wring[tn], aring[tn]);
       __builtin_amdgcn_sched_barrier(0);
       wait_vmcnt<D * PER>();
+      if constexpr (t == 0) {
+        if (it == 0) tl_mark(p.tl, p.tl_cap, 1);  // diagnostics build: first step landed
+      }
 #pragma unroll
       for (int a = 0; a < RW; ++a) {
         const v4i wf = w8a8_wop(wring[t][a]);
@@ -166,6 +170,7 @@ __device__ __forceinline__ void w8a8_rk_body(W8A8Params p) {
     });
   }
   wait_vmcnt<0>();
+  tl_mark(p.tl, p.tl_cap, 2);  // diagnostics build: main loop done
   if constexpr (LAYOUT == 2) w8a8_unscale16(acc);
 
   // Reduce the KW waves of each channel group through LDS in one round: each non-owner wave
@@ -202,6 +207,8 @@ __device__ __forceinline__ void w8a8_rk_body(W8A8Params p) {
           if (m < M && n < p.N) w8a8_store4s(p, m, n, acc[a][j], es.a[j], es.w[a]);
         }
     }
+    tl_mark(p.tl, p.tl_cap, 3);          // diagnostics build: stores issued
+    tl_mark_drained(p.tl, p.tl_cap, 4);  // ... and completed
     return;
   }
   const rsrc_t prs = w8a8_partials_rsrc<BM, BN>(p, cidx);
@@ -212,8 +219,10 @@ __device__ __forceinline__ void w8a8_rk_body(W8A8Params p) {
       for (int j = 0; j < MT; ++j)
         w8a8_publish_quad<BM, BN>(prs, split, j * 16 + r, cw * BNW + a * 16 + 4 * g, acc[a][j]);
   }
+  tl_mark(p.tl, p.tl_cap, 3);  // diagnostics build: partials issued
   __shared__ int s_last_rk;
   w8a8_splitk_finish<BM, BN, NW * 64>(p, prs, cidx, m0, ltile * BN, M, &s_last_rk);
+  tl_mark_drained(p.tl, p.tl_cap, 4);  // diagnostics build: hand-off (and, if last, the sum) done
 }
 
 template <int MT, int RW, int KW, int NW, int LAYOUT>

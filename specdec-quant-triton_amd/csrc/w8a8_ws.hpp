@@ -64,6 +64,7 @@ __device__ __forceinline__ void w8a8_ws_body(W8A8Params p, SlotPtr slot_ptr) {
   static_assert(C::OK, "unsupported W8A8 weight-stream tile");
   constexpr int CW = C::CW, BM = C::BM, BNW = C::BNW, BN = C::BN, KC = C::KC, A_L = C::A_L;
   constexpr int NS = C::NS, D = C::D, P = C::P, SLOT = C::SLOT;
+  tl_mark(p.tl, p.tl_cap, 0);  // diagnostics build: workgroup start
 
   int mc, unit;
   if (!chunked_unit(p.m_chunks, p.n_tiles * p.splits, mc, unit)) return;
@@ -193,6 +194,9 @@ __device__ __forceinline__ void w8a8_ws_body(W8A8Params p, SlotPtr slot_ptr) {
       const int c = c0 + cl;
       wait_vmcnt<P * S * RW + (P - 1) * A_L>();  // this wave's DMA of chunk c has landed
       wg_barrier_lds();  // ... every wave's has, and nobody reads slot (c + P) % NSLOT any more
+      if constexpr (cl == 0) {
+        if (c0 == 0) tl_mark(p.tl, p.tl_cap, 1);  // diagnostics build: first chunk landed
+      }
       dma_chunk(c + P, slot_ptr(std::integral_constant<int, (cl + P) % NSLOT>{}));
       __builtin_amdgcn_sched_barrier(0);
       const uint8_t* aslot = slot_ptr(cc_);
@@ -226,6 +230,7 @@ __device__ __forceinline__ void w8a8_ws_body(W8A8Params p, SlotPtr slot_ptr) {
   }
   wait_vmcnt<0>();
   wg_barrier_lds();  // every wave is done with the activation slots
+  tl_mark(p.tl, p.tl_cap, 2);  // diagnostics build: main loop done
   if constexpr (WL == 2) w8a8_unscale16(acc);
 
   // Reduce the KW waves of each channel group through LDS: every non-owner wave writes its
@@ -304,6 +309,8 @@ __device__ __forceinline__ void w8a8_ws_body(W8A8Params p, SlotPtr slot_ptr) {
         }
       }
     }
+    tl_mark(p.tl, p.tl_cap, 3);          // diagnostics build: stores issued
+    tl_mark_drained(p.tl, p.tl_cap, 4);  // ... and completed
     return;
   }
   const rsrc_t prs = w8a8_partials_rsrc<BM, BN>(p, cidx);
@@ -314,8 +321,10 @@ __device__ __forceinline__ void w8a8_ws_body(W8A8Params p, SlotPtr slot_ptr) {
       for (int u = 0; u < MT; ++u)
         w8a8_publish_quad<BM, BN>(prs, split, u * 16 + r, cw * BNW + a * 16 + 4 * g, acc[a][u]);
   }
+  tl_mark(p.tl, p.tl_cap, 3);  // diagnostics build: partials issued
   __shared__ int s_last_ws;
   w8a8_splitk_finish<BM, BN, NW * 64>(p, prs, cidx, m0, ltile * BN, M, &s_last_ws);
+  tl_mark_drained(p.tl, p.tl_cap, 4);  // diagnostics build: hand-off (and, if last, the sum) done
 }
 
 template <int MT, int RW, int KW, int S, int NSLOT, int NW, int WL>

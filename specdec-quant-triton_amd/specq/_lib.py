@@ -95,6 +95,25 @@ _lib = None
 _lock = threading.Lock()
 
 
+DIAG_LIB_PATH = os.path.join(PKG_DIR, "libspecq_diag.so")
+# Entry points only the measurement build (libspecq_diag.so) exports.
+DIAG_SIGNATURES = {
+    "specq_diag_set_timeline": (_c_int, [_c_vp, _c_int]),
+    "specq_diag_stream_read": (_c_int, [_c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp, _c_vp]),
+}
+
+
+def use_diag() -> None:
+    """Load the measurement build (libspecq_diag.so: the same kernels, plus per-workgroup
+    timestamps and a streaming-read kernel) instead of libspecq.so.  For specq/profiling.py
+    only; must run before the first call into the library."""
+    global LIB_PATH
+    with _lock:
+        if _lib is not None and LIB_PATH != DIAG_LIB_PATH:
+            raise RuntimeError("use_diag(): libspecq.so is already loaded in this process")
+        LIB_PATH = DIAG_LIB_PATH
+
+
 def lib() -> ctypes.CDLL:
     """Load libspecq.so once; raise if it has not been built."""
     global _lib
@@ -106,7 +125,8 @@ def lib() -> ctypes.CDLL:
                         f"{LIB_PATH} is missing: build the HIP kernels first "
                         f"(python {os.path.join(PKG_DIR, 'build.py')})")
                 h = ctypes.CDLL(LIB_PATH)
-                for name, (res, args) in SIGNATURES.items():
+                sigs = dict(SIGNATURES, **(DIAG_SIGNATURES if LIB_PATH == DIAG_LIB_PATH else {}))
+                for name, (res, args) in sigs.items():
                     fn = getattr(h, name)
                     fn.restype = res
                     fn.argtypes = args

@@ -8,6 +8,8 @@ Subcommands (run from the repository root):
               w8a8:M    the fused gate_up W8A8 GEMM (N=28672, K=4096, packed weights)
               w8a8g:M   gate and up (14336 x 4096 each) as one grouped launch over separate
                         packed weights (the headline's dominant launch)
+              w8l:L:M   launch L of a config-1 layer as bench.py runs it (qkv, o, gate_up,
+                        down; q|k|v and gate|up grouped over separate packed weights)
               w4a16:M   the same shape in W4A16 (load-time packed INT4, group 128)
               attn:B:k:ctx  INT8 paged verification attention (32/8 heads, D=128, fp32
                         scales, fused QPP=k+1)
@@ -25,6 +27,14 @@ Subcommands (run from the repository root):
             median per dispatch of each counter, instructions per wave (SQ_INSTS_* / SQ_WAVES),
             and the share of wave cycles spent issuing each instruction class
             (SQ_ACTIVE_INST_* / SQ_WAVE_CYCLES, both counted per wave in the same units).
+  timeline  per-workgroup phase times of one launch of each kind (start skew, time to first
+            operand data, main loop, stores), from the diagnostics build (libspecq_diag.so),
+            whose W8A8 and attention kernels write s_memrealtime marks into a buffer.
+  floors    streaming-read floors of the config-1 weight sizes (diagnostics build's plain
+            read kernel, best over grid / waves / loads in flight) and an empty launch's cost.
+  launches  one derived table per kernel instance over several `--pmc` runs of the same
+            kinds: HBM bytes against the algorithmic bytes, wave-cycle shares, MFMA busy, mean
+            L1->L2 read latency, L2 hit rate, TA / TD busy.
   mfma      reads a `--pmc SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_INSTS_VALU_MFMA_MOPS_F16` run: the
             MFMA ops issued (512 per MOPS unit) against the algorithmic 2*M*N*K, and achieved
             TOP/s from an unprofiled probe's timing (`--map`) against the dense peak.
@@ -55,6 +65,25 @@ def _short(name: str) -> str:
     return name[5:] if name.startswith("void ") else name
 
 
+def _key(name: str, grid) -> str:
+    """Kernel instance key of the maps and tables: short name and grid (the same template runs
+    several launches, told apart by their workgroup counts)."""
+    return f"{_short(name)} [{grid}]" if grid else _short(name)
+
+
+def _row_grid(r):
+    """Workgroups of a rocprofv3 csv row (kernel trace: per-axis columns; counters: totals)."""
+    if "Grid_Size_X" in r:
+        wgs = 1
+        for ax in "XYZ":
+            wgs *= int(r.get(f"Grid_Size_{ax}", 1) or 1) // max(1, int(r.get(f"Workgroup_Size_{ax}", 1) or 1))
+        return wgs
+    try:
+        return int(r["Grid_Size"]) // max(1, int(r["Workgroup_Size"]))
+    except (KeyError, ValueError):
+        return None
+
+
 def _graph_us(fn, launches: int, reps: int = 10) -> float:
     """Mean µs per launch of fn() (which issues `launches` launches) replayed as one graph."""
     import torch
@@ -80,6 +109,133 @@ def _graph_us(fn, launches: int, reps: int = 10) -> float:
     return e0.elapsed_time(e1) * 1e3 / (reps * launches)
 
 
+def _apply_options(args) -> None:
+    """Library options given as --set name=value (specq_set_option)."""
+    from specq import _lib
+    for kv in getattr(args, "set", []) or []:
+        name, val = kv.split("=", 1)
+        _lib.set_option(name, int(val))
+
+
+def _make_kind(kind: str, args, K, gen, g, torch):
+    """Inputs and a run() for one probe kind (see the module docstring): dict(run, launches,
+    ck, workload, bytes, ops), or None for the copy kind, which runs at once."""
+    N, Kd = 28672, 4096
+    f = kind.split(":")
+    if f[0] == "w8a8":
+        M = int(f[1])
+        layers = []
+        for _ in range(args.layers):
+            w = torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=g)
+            layers.append((K.pack_weight_int8(w), torch.rand((N,), device="cuda", generator=g) * 0.009 + 0.001))
+            del w
+        a = torch.randint(-127, 128, (M, Kd), dtype=torch.int8, device="cuda", generator=g)
+        sa = torch.rand((M,), device="cuda", generator=g) * 0.015 + 0.005
+        out = torch.empty((M, N), dtype=torch.float16, device="cuda")
+
+        def run(layers=layers, a=a, sa=sa, out=out):
+            for w, sw in layers:
+                K.w8a8_matmul(a, sa, w, sw, out=out, BLOCK_M=None)
+        _, ck = K.w8a8_matmul(a, sa, *layers[0], out=out, BLOCK_M=None)
+        bytes_, ops = N * Kd + M * Kd + 4 * M + 4 * N + 2 * M * N, 2 * M * N * Kd
+        wl = f"W8A8 N={N} K={Kd} M={M}"
+    elif f[0] == "w8a8g":
+        # The headline's dominant launch: gate and up (14336 x 4096 each, separate packed
+        # weights) as one grouped launch.
+        M, Ng = int(f[1]), 14336
+        layers = []
+        for _ in range(args.layers):
+            pair = []
+            for _ in range(2):
+                w = torch.randint(-127, 128, (Ng, Kd), dtype=torch.int8, device="cuda", generator=g)
+                pair.append((K.pack_weight_int8(w), torch.rand((Ng,), device="cuda", generator=g) * 0.009 + 0.001))
+                del w
+            layers.append(pair)
+        a = torch.randint(-127, 128, (M, Kd), dtype=torch.int8, device="cuda", generator=g)
+        sa = torch.rand((M,), device="cuda", generator=g) * 0.015 + 0.005
+        outs = [torch.empty((M, Ng), dtype=torch.float16, device="cuda") for _ in range(2)]
+
+        def run(layers=layers, a=a, sa=sa, outs=outs):
+            for pair in layers:
+                K.w8a8_matmul_grouped(a, sa, pair, outs=outs, BLOCK_M=None)
+        _, ck = K.w8a8_matmul_grouped(a, sa, layers[0], outs=outs, BLOCK_M=None)
+        bytes_ = 2 * (Ng * Kd + 4 * Ng + 2 * M * Ng) + M * Kd + 4 * M
+        ops = 2 * 2 * M * Ng * Kd
+        wl = f"W8A8 grouped gate|up 2x{Ng}x{Kd} M={M}"
+    elif f[0] == "w8l":
+        # One of the four launches of a config-1 layer (bench.py's step): qkv and gate_up
+        # grouped over their separate packed weights, o and down alone.
+        lname, M = f[1], int(f[2])
+        shapes = {"qkv": [(4096, 4096), (1024, 4096), (1024, 4096)], "o": [(4096, 4096)],
+                  "gate_up": [(14336, 4096), (14336, 4096)], "down": [(4096, 14336)]}[lname]
+        Kl = shapes[0][1]
+        layers = []
+        for _ in range(args.layers):
+            mem = []
+            for Ng, _k in shapes:
+                w = torch.randint(-127, 128, (Ng, Kl), dtype=torch.int8, device="cuda", generator=g)
+                mem.append((K.pack_weight_int8(w), torch.rand((Ng,), device="cuda", generator=g) * 0.009 + 0.001))
+                del w
+            layers.append(mem)
+        a = torch.randint(-127, 128, (M, Kl), dtype=torch.int8, device="cuda", generator=g)
+        sa = torch.rand((M,), device="cuda", generator=g) * 0.015 + 0.005
+        outs = [torch.empty((M, Ng), dtype=torch.float16, device="cuda") for Ng, _k in shapes]
+
+        def run(layers=layers, a=a, sa=sa, outs=outs):
+            for mem in layers:
+                K.w8a8_matmul_grouped(a, sa, mem, outs=outs, BLOCK_M=None)
+        _, ck = K.w8a8_matmul_grouped(a, sa, layers[0], outs=outs, BLOCK_M=None)
+        bytes_ = sum(Ng * Kl + 4 * Ng + 2 * M * Ng for Ng, _k in shapes) + M * Kl + 4 * M
+        ops = sum(2 * M * Ng * Kl for Ng, _k in shapes)
+        wl = f"W8A8 {lname} ({'+'.join(f'{Ng}x{Kl}' for Ng, _k in shapes)}) M={M}"
+    elif f[0] == "w4a16":
+        M = int(f[1])
+        layers = []
+        for _ in range(args.layers):
+            wp = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, Kd // 8), dtype=torch.int32, device="cuda", generator=g)
+            sc = (torch.rand((N, Kd // 128), device="cuda", generator=g) * 0.018 + 0.002).half()
+            layers.append((K.pack_weight_int4(wp), sc))
+            del wp
+        x = torch.randn((M, Kd), device="cuda", generator=g).half()
+        out = torch.empty((M, N), dtype=torch.float16, device="cuda")
+
+        def run(layers=layers, x=x, out=out):
+            for wp, sc in layers:
+                K.w4a16_matmul(x, wp, sc, out=out, BLOCK_M=None)
+        _, ck = K.w4a16_matmul(x, *layers[0], out=out, BLOCK_M=None)
+        bytes_ = N * Kd // 2 + 2 * N * (Kd // 128) + 2 * M * Kd + 2 * M * N
+        ops = 2 * M * N * Kd
+        wl = f"W4A16 N={N} K={Kd} M={M} group 128"
+    elif f[0] == "attn":
+        B, k, ctx = int(f[1]), int(f[2]), int(f[3])
+        ql, H, H_KV, D = k + 1, 32, 8, 128
+        L = ctx + ql
+        caches = [[t.cuda() for t in gen.paged_kv(B, [L] * B, H_KV, D, seed=50 + i)] for i in range(args.layers)]
+        q = gen.queries(B, ql, H, D, seed=6).cuda()
+        out = torch.zeros_like(q)
+
+        def run(caches=caches, q=q, out=out, ql=ql):
+            for kc, vc, ks, vs, bt, cl in caches:
+                K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=ql, out=out)
+        _, ck = K.paged_attention(q, *caches[0], ql, QPP=ql, out=out)
+        pages = (L + 15) // 16
+        bytes_ = B * L * H_KV * (2 * D + 8) + 4 * B * ql * H * D + 4 * B * pages + 4 * B
+        ops = 4 * B * H * D * ql * L
+        wl = f"attention B={B} k={k} ctx={ctx} fused"
+    elif f[0] == "copy":
+        n = (args.copy_mib << 20) // 4
+        src = torch.randint(-2 ** 30, 2 ** 30, (n,), dtype=torch.int32, device="cuda", generator=g)
+        dst = torch.empty_like(src)
+        for _ in range(args.reps):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        print(f"[probe] copy {args.copy_mib} MiB x {args.reps}", flush=True)
+        return None
+    else:
+        raise SystemExit(f"unknown probe kind {kind}")
+    launches = len(layers) if f[0] != "attn" else len(caches)
+    return dict(run=run, launches=launches, ck=ck, workload=wl, bytes=bytes_, ops=ops)
+
 def probe(args) -> int:
     import torch
 
@@ -89,108 +245,177 @@ def probe(args) -> int:
     from specq import gen
 
     torch.cuda.set_device(0)
+    _apply_options(args)
     g = torch.Generator(device="cuda").manual_seed(1)
-    N, Kd = 28672, 4096
     info = {}
     for kind in args.kinds.split(","):
-        f = kind.split(":")
-        if f[0] == "w8a8":
-            M = int(f[1])
-            layers = []
-            for _ in range(args.layers):
-                w = torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=g)
-                layers.append((K.pack_weight_int8(w), torch.rand((N,), device="cuda", generator=g) * 0.009 + 0.001))
-                del w
-            a = torch.randint(-127, 128, (M, Kd), dtype=torch.int8, device="cuda", generator=g)
-            sa = torch.rand((M,), device="cuda", generator=g) * 0.015 + 0.005
-            out = torch.empty((M, N), dtype=torch.float16, device="cuda")
-
-            def run(layers=layers, a=a, sa=sa, out=out):
-                for w, sw in layers:
-                    K.w8a8_matmul(a, sa, w, sw, out=out, BLOCK_M=None)
-            _, ck = K.w8a8_matmul(a, sa, *layers[0], out=out, BLOCK_M=None)
-            bytes_, ops = N * Kd + M * Kd + 4 * M + 4 * N + 2 * M * N, 2 * M * N * Kd
-            wl = f"W8A8 N={N} K={Kd} M={M}"
-        elif f[0] == "w8a8g":
-            # The headline's dominant launch: gate and up (14336 x 4096 each, separate packed
-            # weights) as one grouped launch.
-            M, Ng = int(f[1]), 14336
-            layers = []
-            for _ in range(args.layers):
-                pair = []
-                for _ in range(2):
-                    w = torch.randint(-127, 128, (Ng, Kd), dtype=torch.int8, device="cuda", generator=g)
-                    pair.append((K.pack_weight_int8(w), torch.rand((Ng,), device="cuda", generator=g) * 0.009 + 0.001))
-                    del w
-                layers.append(pair)
-            a = torch.randint(-127, 128, (M, Kd), dtype=torch.int8, device="cuda", generator=g)
-            sa = torch.rand((M,), device="cuda", generator=g) * 0.015 + 0.005
-            outs = [torch.empty((M, Ng), dtype=torch.float16, device="cuda") for _ in range(2)]
-
-            def run(layers=layers, a=a, sa=sa, outs=outs):
-                for pair in layers:
-                    K.w8a8_matmul_grouped(a, sa, pair, outs=outs, BLOCK_M=None)
-            _, ck = K.w8a8_matmul_grouped(a, sa, layers[0], outs=outs, BLOCK_M=None)
-            bytes_ = 2 * (Ng * Kd + 4 * Ng + 2 * M * Ng) + M * Kd + 4 * M
-            ops = 2 * 2 * M * Ng * Kd
-            wl = f"W8A8 grouped gate|up 2x{Ng}x{Kd} M={M}"
-        elif f[0] == "w4a16":
-            M = int(f[1])
-            layers = []
-            for _ in range(args.layers):
-                wp = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, Kd // 8), dtype=torch.int32, device="cuda", generator=g)
-                sc = (torch.rand((N, Kd // 128), device="cuda", generator=g) * 0.018 + 0.002).half()
-                layers.append((K.pack_weight_int4(wp), sc))
-                del wp
-            x = torch.randn((M, Kd), device="cuda", generator=g).half()
-            out = torch.empty((M, N), dtype=torch.float16, device="cuda")
-
-            def run(layers=layers, x=x, out=out):
-                for wp, sc in layers:
-                    K.w4a16_matmul(x, wp, sc, out=out, BLOCK_M=None)
-            _, ck = K.w4a16_matmul(x, *layers[0], out=out, BLOCK_M=None)
-            bytes_ = N * Kd // 2 + 2 * N * (Kd // 128) + 2 * M * Kd + 2 * M * N
-            ops = 2 * M * N * Kd
-            wl = f"W4A16 N={N} K={Kd} M={M} group 128"
-        elif f[0] == "attn":
-            B, k, ctx = int(f[1]), int(f[2]), int(f[3])
-            ql, H, H_KV, D = k + 1, 32, 8, 128
-            L = ctx + ql
-            caches = [[t.cuda() for t in gen.paged_kv(B, [L] * B, H_KV, D, seed=50 + i)] for i in range(args.layers)]
-            q = gen.queries(B, ql, H, D, seed=6).cuda()
-            out = torch.zeros_like(q)
-
-            def run(caches=caches, q=q, out=out, ql=ql):
-                for kc, vc, ks, vs, bt, cl in caches:
-                    K.paged_attention(q, kc, vc, ks, vs, bt, cl, ql, QPP=ql, out=out)
-            _, ck = K.paged_attention(q, *caches[0], ql, QPP=ql, out=out)
-            pages = (L + 15) // 16
-            bytes_ = B * L * H_KV * (2 * D + 8) + 4 * B * ql * H * D + 4 * B * pages + 4 * B
-            ops = 4 * B * H * D * ql * L
-            wl = f"attention B={B} k={k} ctx={ctx} fused"
-        elif f[0] == "copy":
-            n = (args.copy_mib << 20) // 4
-            src = torch.randint(-2 ** 30, 2 ** 30, (n,), dtype=torch.int32, device="cuda", generator=g)
-            dst = torch.empty_like(src)
-            for _ in range(args.reps):
-                torch.neg(src, out=dst)
-            torch.cuda.synchronize()
-            print(f"[probe] copy {args.copy_mib} MiB x {args.reps}", flush=True)
+        kd = _make_kind(kind, args, K, gen, g, torch)
+        if kd is None:
             continue
-        else:
-            raise SystemExit(f"unknown probe kind {kind}")
-        us = _graph_us(run, len(layers) if f[0] != "attn" else len(caches))
+        run, ck, wl, bytes_, ops = kd["run"], kd["ck"], kd["workload"], kd["bytes"], kd["ops"]
+        us = _graph_us(run, kd["launches"])
         for _ in range(args.reps):
             run()
         torch.cuda.synchronize()
-        info[ck.name] = dict(workload=wl, us=round(us, 3), algorithmic_bytes=bytes_, ops=ops,
+        info[_key(ck.name, ck.config.get("grid"))] = dict(workload=wl, us=round(us, 3), algorithmic_bytes=bytes_, ops=ops,
                              GBps=round(bytes_ / (us * 1e-6) / 1e9, 1), TOPs=round(ops / (us * 1e-6) / 1e12, 2))
         print(f"[probe] {wl}: {ck.name} {us:.2f} us/launch", flush=True)
-        del run
+        del run, kd
         torch.cuda.empty_cache()
     if args.map:
         with open(args.map, "w") as fh:
             json.dump(info, fh, indent=1)
+    return 0
+
+
+# Timestamp marks the diagnostics build writes (csrc/common.hpp tl_mark), per kernel family.
+_TL_PHASES = {
+    "gemm": [("start skew", None, 0), ("to first data", 0, 1), ("main loop", 1, 2), ("stores issued", 2, 3),
+             ("stores done", 3, 4), ("split-K: partials acknowledged", 3, 5), ("split-K: arrival count back", 5, 6),
+             ("split-K (last): partials read and summed", 6, 7), ("split-K (last): outputs stored", 7, 4),
+             ("whole workgroup", 0, 4)],
+    "attn": [("start skew", None, 0), ("page ids + Q", 0, 1), ("to first chunk", 1, 2), ("chunk loop (wave 0)", 2, 3),
+             ("wait for the other waves", 3, 7), ("wave merge", 7, 4), ("hand-off / store", 4, 6),
+             ("split: partials acknowledged", 4, 5), ("whole workgroup", 0, 6)],
+}
+
+
+def _pcts(x):
+    import numpy as np
+
+    return [float(np.percentile(x, q)) for q in (10, 50, 90)] + [float(np.max(x))]
+
+
+def timeline(args) -> int:
+    """Per-workgroup phases of one launch of each probe kind, from the diagnostics build's
+    s_memrealtime marks (100 MHz): the kind's graph of back-to-back launches over distinct
+    weights / caches is replayed and the marks of its last launch are read."""
+    import numpy as np
+    import torch
+
+    if PKG not in sys.path:
+        sys.path.insert(0, PKG)
+    from specq import _lib
+    _lib.use_diag()
+    import kernels as K
+    from specq import gen
+
+    torch.cuda.set_device(0)
+    _apply_options(args)
+    g = torch.Generator(device="cuda").manual_seed(1)
+    cap = 1 << 16
+    marks = 16  # kTlMarks of csrc/common.hpp
+    tl = torch.zeros(cap * marks, dtype=torch.int64, device="cuda")
+    _lib.call("specq_diag_set_timeline", tl.data_ptr(), cap)
+    out = [f"Per-workgroup timelines (diagnostics build, s_memrealtime at 100 MHz); µs, p10 / p50 / p90 / max "
+           f"over the workgroups of the last launch of a graph of back-to-back launches."]
+    for kind in args.kinds.split(","):
+        kd = _make_kind(kind, args, K, gen, g, torch)
+        if kd is None:
+            continue
+        us = _graph_us(kd["run"], kd["launches"])
+        tl.zero_()
+        torch.cuda.synchronize()
+        # One more replay of the same graph shape: the marks left are those of its last launch.
+        kd["run"]()
+        torch.cuda.synchronize()
+        t = tl.view(cap, marks).cpu().numpy().astype(np.int64)
+        ck = kd["ck"]
+        grid = int(ck.config.get("grid") or 0)
+        fam = "attn" if kind.startswith("attn") else "gemm"
+        rows = t[: grid if grid else cap]
+        rows = rows[rows[:, 0] != 0]
+        # A mark some workgroup index wrote in an earlier launch of the sequence and not in the
+        # last one (e.g. the split-K finish of a tile whose last arrival was another split)
+        # predates that launch's start mark: drop it.
+        rows[:, 1:] = np.where(rows[:, 1:] >= rows[:, :1], rows[:, 1:], 0)
+        if not len(rows):
+            out.append(f"\n### {kd['workload']}: no marks (kernel without timestamps)")
+            continue
+        t0 = rows[:, 0].min()
+        last = 6 if fam == "attn" else 4
+        worked = rows[rows[:, last] != 0]
+        span = (worked[:, last].max() - t0) / 100.0 if len(worked) else float("nan")
+        out.append(f"\n### {kd['workload']}: `{_key(ck.name, grid)}`\n")
+        out.append(f"{len(rows)} workgroups started, {len(worked)} ran to the end; first start to last end "
+                   f"{span:.2f} µs; graph launch {us:.2f} µs\n")
+        out.append("| phase | p10 | p50 | p90 | max |")
+        out.append("|---|---|---|---|---|")
+        for name, a, b in _TL_PHASES[fam]:
+            sel = worked if b != 0 else rows
+            if a is None:
+                d = (sel[:, b] - t0) / 100.0
+            else:
+                ok = (sel[:, a] != 0) & (sel[:, b] != 0)
+                d = (sel[ok, b] - sel[ok, a]) / 100.0
+            if len(d):
+                out.append(f"| {name} | " + " | ".join(f"{v:.2f}" for v in _pcts(d)) + " |")
+        if fam == "attn":
+            # Spread of the eight waves' loop ends within a workgroup (marks 8..15).
+            wl = worked[:, 8:16]
+            ok = (wl != 0).all(axis=1)
+            if ok.any():
+                spread = (wl[ok].max(axis=1) - wl[ok].min(axis=1)) / 100.0
+                first = (wl[ok].min(axis=1) - worked[ok, 2]) / 100.0
+                out.append("| loop end, last wave - first wave | " + " | ".join(f"{v:.2f}" for v in _pcts(spread)) + " |")
+                out.append("| first chunk to the first wave's loop end | " + " | ".join(f"{v:.2f}" for v in _pcts(first)) + " |")
+        del kd
+        torch.cuda.empty_cache()
+    _lib.call("specq_diag_set_timeline", None, 0)
+    text = "\n".join(out)
+    print(text)
+    if args.out:
+        with open(args.out, "w") as fh:
+            fh.write(text + "\n")
+    return 0
+
+
+def floors(args) -> int:
+    """Streaming-read floors (diagnostics build): a plain read of N bytes (16-byte loads,
+    XOR-reduced) timed as a graph of back-to-back launches over distinct buffers (>= 512 MiB in
+    all, so every launch reads HBM), best over workgroup count x waves x loads in flight; and
+    the cost of an empty launch in the same graph form."""
+    import torch
+
+    if PKG not in sys.path:
+        sys.path.insert(0, PKG)
+    from specq import _lib
+    _lib.use_diag()
+    torch.cuda.set_device(0)
+    sink = torch.zeros(65536, dtype=torch.int32, device="cuda")
+    stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    out = ["| bytes | what | best µs | TB/s | workgroups | waves | 1 KB loads in flight per wave |",
+           "|---|---|---|---|---|---|---|"]
+    tiny = torch.zeros(4, dtype=torch.int32, device="cuda")
+    us = _graph_us(lambda: [_lib.call("specq_diag_stream_read", tiny.data_ptr(), 16, 1, 4, 2, sink.data_ptr(),
+                                      stream()) for _ in range(64)], 64, reps=20)
+    out.append(f"| 16 | empty launch (one workgroup) | {us:.2f} | | 1 | 4 | |")
+    for spec in args.sizes.split(","):
+        name, nb = spec.split(":")
+        nb = int(nb)
+        nbuf = max(2, -(-(512 << 20) // nb) + 1)
+        bufs = [torch.empty(nb, dtype=torch.int8, device="cuda").random_(-128, 127) for _ in range(nbuf)]
+        best = None
+        for wgs in (256, 512, 1024, 2048):
+            for waves in (4, 8):
+                for unroll in (2, 4, 8, 16):
+                    def run(wgs=wgs, waves=waves, unroll=unroll):
+                        for b in bufs:
+                            _lib.call("specq_diag_stream_read", b.data_ptr(), nb, wgs, waves, unroll,
+                                      sink.data_ptr(), stream())
+                    t = _graph_us(run, nbuf, reps=5)
+                    if best is None or t < best[0]:
+                        best = (t, wgs, waves, unroll)
+        t, wgs, waves, unroll = best
+        out.append(f"| {nb} | {name} | {t:.2f} | {nb / (t * 1e-6) / 1e12:.2f} | {wgs} | {waves} | {unroll} |")
+        print(out[-1], flush=True)
+        del bufs
+        torch.cuda.empty_cache()
+    text = "\n".join(out)
+    print(text)
+    if args.out:
+        with open(args.out, "w") as fh:
+            fh.write(text + "\n")
     return 0
 
 
@@ -228,7 +453,7 @@ def _counter(dirname: str, counter: str):
                     continue
                 name, v = r["Kernel_Name"], float(r["Counter_Value"])
                 if "specq::" in name:
-                    vals[_short(name)].append(v)
+                    vals[_key(name, _row_grid(r))].append(v)
                 elif COPY_TAG in name and "neg" in name.lower():
                     copy.append(v)
     return vals, copy
@@ -277,7 +502,7 @@ def _all_counters(dirname: str):
         with open(f) as fh:
             for r in csv.DictReader(fh):
                 if "specq::" in r["Kernel_Name"]:
-                    vals[_short(r["Kernel_Name"])][r["Counter_Name"]].append(float(r["Counter_Value"]))
+                    vals[_key(r["Kernel_Name"], _row_grid(r))][r["Counter_Name"]].append(float(r["Counter_Value"]))
     return vals
 
 
@@ -303,6 +528,99 @@ def sq(args) -> int:
             shares = [(c[len("SQ_ACTIVE_INST_"):], cs[c] / wc) for c in sorted(cs) if c.startswith("SQ_ACTIVE_INST_")]
             shares += [(c[len("SQ_"):], cs[c] / wc) for c in ("SQ_WAIT_ANY", "SQ_WAIT_INST_ANY") if c in cs]
             print("\nshare of wave cycles: " + ", ".join(f"{k} {100 * v:.1f} %" for k, v in shares))
+    return 0
+
+
+def launches(args) -> int:
+    """One derived table over several --pmc runs of the same probe kinds (and the probe's map):
+    per kernel instance its launch time, HBM bytes (FETCH_SIZE / WRITE_SIZE scaled by the copy
+    kernel) against the algorithmic bytes, where its waves spend their cycles, the mean L1->L2
+    read latency and the TA / TD / L2 figures.  Counter units: SQ_* cycle counters are wave
+    quad-cycles summed over waves; GRBM_GUI_ACTIVE is summed over the 8 XCDs, so one XCD's
+    cycles are GRBM_GUI_ACTIVE / 8; TA_*, TD_*, TCP_* sum over the 256 CUs."""
+    merged = collections.defaultdict(dict)
+    copy = {}
+    for d in args.dirs:
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        per = collections.defaultdict(lambda: collections.defaultdict(list))
+        for f in files:
+            with open(f) as fh:
+                for r in csv.DictReader(fh):
+                    name, c, v = r["Kernel_Name"], r["Counter_Name"], float(r["Counter_Value"])
+                    if "specq::" in name:
+                        per[_key(name, _row_grid(r))][c].append(v)
+                    elif COPY_TAG in name and "neg" in name.lower():
+                        copy.setdefault(c, []).append(v)
+        for k, cs in per.items():
+            for c, v in cs.items():
+                merged[k][c] = statistics.median(v)
+    wmap = json.load(open(args.map)) if args.map else {}
+    half = (args.copy_mib << 20)  # the copy reads and writes this many bytes
+    scale = {c: half / (statistics.median(v) * 1024) for c, v in copy.items() if c in ("FETCH_SIZE", "WRITE_SIZE")}
+
+    def g(cs, c):
+        return cs.get(c)
+
+    rows = []
+    for k in sorted(merged, key=lambda x: wmap.get(x, {}).get("workload", x)):
+        cs, w = merged[k], wmap.get(k, {})
+        grbm = g(cs, "GRBM_GUI_ACTIVE")
+        wc = g(cs, "SQ_WAVE_CYCLES")
+        r = dict(key=k, workload=w.get("workload", ""), us=w.get("us"), alg=w.get("algorithmic_bytes"))
+        if "FETCH_SIZE" in cs and "FETCH_SIZE" in scale:
+            r["fetch"] = cs["FETCH_SIZE"] * 1024 * scale["FETCH_SIZE"]
+        if "WRITE_SIZE" in cs and "WRITE_SIZE" in scale:
+            r["write"] = cs["WRITE_SIZE"] * 1024 * scale["WRITE_SIZE"]
+        if wc:
+            for c in ("SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_VMEM", "SQ_ACTIVE_INST_LDS", "SQ_ACTIVE_INST_SCA",
+                      "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY"):
+                if c in cs:
+                    r[c] = cs[c] / wc
+        if g(cs, "TCP_TCC_READ_REQ_sum"):
+            r["l2_lat"] = cs.get("TCP_TCC_READ_REQ_LATENCY_sum", 0) / cs["TCP_TCC_READ_REQ_sum"]
+            r["l2_req"] = cs["TCP_TCC_READ_REQ_sum"]
+        if grbm:
+            xcd = grbm / 8
+            for c in ("TA_TA_BUSY_sum", "TA_DATA_STALLED_BY_TC_CYCLES_sum", "TD_TD_BUSY_sum", "TD_TC_STALL_sum",
+                      "TCP_PENDING_STALL_CYCLES_sum", "TCP_TCP_TA_DATA_STALL_CYCLES_sum"):
+                if c in cs:
+                    r[c] = cs[c] / (256 * xcd)
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in cs:
+                r["mfma_busy"] = cs["SQ_VALU_MFMA_BUSY_CYCLES"] / (1024 * xcd)
+            if "SQ_LDS_BANK_CONFLICT" in cs:
+                r["lds_conflict"] = cs["SQ_LDS_BANK_CONFLICT"] / (256 * xcd)
+        if "TCC_HIT_sum" in cs and "TCC_MISS_sum" in cs:
+            r["l2_hit"] = cs["TCC_HIT_sum"] / max(1.0, cs["TCC_HIT_sum"] + cs["TCC_MISS_sum"])
+        if "SQ_WAVES" in cs:
+            for c in ("SQ_INSTS_VMEM_RD", "SQ_INSTS_LDS", "SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_SALU"):
+                if c in cs:
+                    r["per_wave_" + c[len("SQ_INSTS_"):]] = cs[c] / cs["SQ_WAVES"]
+        rows.append(r)
+
+    def pct(x):
+        return "" if x is None else f"{100 * x:.1f}"
+
+    def num(x, f="{:.0f}"):
+        return "" if x is None else f.format(x)
+    print("| kernel [grid] | workload | µs | alg MB | fetch MB | write MB | VALU % | VMEM % | LDS % | WAIT_ANY % "
+          "| WAIT_INST % | MFMA busy % | L2 read lat (clk) | L2 hit % | TA busy % | TA stall by TC % "
+          "| TD busy % | TCP pending % |")
+    print("|---" * 18 + "|")
+    for r in rows:
+        print(f"| `{r['key']}` | {r['workload']} | {num(r['us'], '{:.2f}')} | {num(r['alg'] and r['alg'] / 1e6, '{:.2f}')} "
+              f"| {num(r.get('fetch') and r['fetch'] / 1e6, '{:.2f}')} | {num(r.get('write') and r['write'] / 1e6, '{:.2f}')} "
+              f"| {pct(r.get('SQ_ACTIVE_INST_VALU'))} | {pct(r.get('SQ_ACTIVE_INST_VMEM'))} | {pct(r.get('SQ_ACTIVE_INST_LDS'))} "
+              f"| {pct(r.get('SQ_WAIT_ANY'))} | {pct(r.get('SQ_WAIT_INST_ANY'))} | {pct(r.get('mfma_busy'))} "
+              f"| {num(r.get('l2_lat'))} | {pct(r.get('l2_hit'))} | {pct(r.get('TA_TA_BUSY_sum'))} "
+              f"| {pct(r.get('TA_DATA_STALLED_BY_TC_CYCLES_sum'))} | {pct(r.get('TD_TD_BUSY_sum'))} "
+              f"| {pct(r.get('TCP_PENDING_STALL_CYCLES_sum'))} |")
+    extra = [c for c in ("per_wave_VMEM_RD", "per_wave_LDS", "per_wave_VALU", "per_wave_MFMA", "per_wave_SALU")
+             if any(c in r for r in rows)]
+    if extra:
+        print("\n| kernel [grid] | " + " | ".join(c.replace("per_wave_", "") + " / wave" for c in extra) + " |")
+        print("|---" * (len(extra) + 1) + "|")
+        for r in rows:
+            print(f"| `{r['key']}` | " + " | ".join(num(r.get(c), "{:.1f}") for c in extra) + " |")
     return 0
 
 
@@ -400,6 +718,7 @@ def main() -> int:
     p.add_argument("dirs", nargs="+")
     p.add_argument("--map", default=None)
     p = sub.add_parser("probe")
+    p.add_argument("--set", action="append", default=[], help="library option name=value (repeatable)")
     p.add_argument("--kinds", default="w8a8:72,copy")
     p.add_argument("--layers", type=int, default=16)
     p.add_argument("--reps", type=int, default=2)
@@ -417,6 +736,20 @@ def main() -> int:
     t.add_argument("--map")
     t.add_argument("--merge", help="existing traffic json whose entries are kept")
     t.add_argument("--out")
+    tp = sub.add_parser("timeline")
+    tp.add_argument("--set", action="append", default=[], help="library option name=value (repeatable)")
+    tp.add_argument("--kinds", required=True)
+    tp.add_argument("--layers", type=int, default=8)
+    tp.add_argument("--reps", type=int, default=1)
+    tp.add_argument("--copy-mib", type=int, default=1024)
+    tp.add_argument("--out")
+    fp = sub.add_parser("floors")
+    fp.add_argument("--sizes", default="o:16777216,qkv:25165824,down:58720256,gate_up:117440512")
+    fp.add_argument("--out")
+    lp = sub.add_parser("launches")
+    lp.add_argument("dirs", nargs="+")
+    lp.add_argument("--map", default=None)
+    lp.add_argument("--copy-mib", type=int, default=1024)
     m = sub.add_parser("mfma")
     m.add_argument("dir")
     m.add_argument("--map", required=True)
@@ -427,7 +760,8 @@ def main() -> int:
     c.add_argument("--kind", choices=("w8a8", "w4a16"), default="w8a8")
     args = ap.parse_args()
     return {"probe": probe, "stats": stats, "traffic": traffic, "mfma": mfma, "staircase": staircase,
-            "staircase-md": staircase_md, "sq": sq}[args.cmd](args)
+            "staircase-md": staircase_md, "sq": sq, "launches": launches, "timeline": timeline,
+            "floors": floors}[args.cmd](args)
 
 
 if __name__ == "__main__":

@@ -216,3 +216,4 @@ def test_w8a8_deterministic_and_strided_out():
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(big[:, 200:1224], o1)
     assert bool((big[:, :200] == 7.0).all()) and bool((big[:, 1224:] == 7.0).all())
+

@@ -246,3 +246,39 @@ def test_gpu_entry_points_refuse_cpu_tensors():
     a = torch.zeros(4, 64, dtype=torch.int8)
     with pytest.raises(RuntimeError, match="GPU"):
         K.w8a8_matmul(a, torch.ones(4), torch.zeros(8, 64, dtype=torch.int8), torch.ones(8))
+
+
+def test_diag_library_is_separate(built_lib):
+    """The measurement build exports its timeline and streaming-read entry points; the product
+    library does not (its kernels never write timestamps)."""
+    from specq import _lib
+    diag = os.path.join(os.path.dirname(built_lib), "libspecq_diag.so")
+    if not os.path.exists(diag):
+        pytest.skip("libspecq_diag.so not built (build.py --no-diag)")
+    d = ctypes.CDLL(diag)
+    p = ctypes.CDLL(built_lib)
+    for name in _lib.DIAG_SIGNATURES:
+        assert hasattr(d, name), name
+        assert not hasattr(p, name), name
+    for name in header_symbols():
+        assert hasattr(d, name), name
+
+
+def test_bench_int4_layout_converter_matches_reference_packing():
+    """bench.py's int32 -> uint8 INT4 conversion gives the reference's packing (kernels.py:143-145)."""
+    import bench
+    from specq import gen
+    qu, _ = gen.int4_weights(40, 512, 128, seed=3)
+    got = bench.i32_to_u8_reference(gen.pack_i32(qu))
+    assert torch.equal(got, gen.pack_u8_reference(qu))
+
+
+def test_grid_markdown_tables():
+    from specq import grids
+    us = {1: {0: 10.0, 8: 12.5}, 8: {0: 11.0, 8: 16.5}}
+    ratio = {B: {k: us[B][k] / us[B][0] for k in us[B]} for B in us}
+    md = grids.ratio_grid_md(us, ratio, "W8A8")
+    assert "| 8 | 11.0 (1.00x) | 16.5 (1.50x) |" in md
+    res = {(B, k, q): dict(us=float(B + k + q), frac=0.5) for B in (1, 2) for k in (0, 1) for q in ({k + 1, 1})}
+    md = grids.attention_grid_md(res, 1024)
+    assert "| 2 | 3.0 | 5.0 / 4.0 |" in md and "50.0 %" in md
