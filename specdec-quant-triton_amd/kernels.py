@@ -70,7 +70,7 @@ __all__ = [
     "silu_mul", "quantize_act_int8_gpu", "silu_mul_quant_int8", "paged_kv_append",
     "pack_int4_i32", "KernelInfo", "PackedWeightInt8", "pack_weight_int8", "PackedWeightInt4", "pack_weight_int4",
     "w4a8_matmul", "quantize_weight_int4_channel", "PackedWeightW4A8", "pack_weight_w4a8",
-    "w8a8_matmul_grouped", "w4a16_matmul_grouped",
+    "w8a8_matmul_grouped", "w4a16_matmul_grouped", "set_weight_pack_cache", "clear_weight_pack_cache",
 ]
 
 
@@ -239,6 +239,92 @@ def pack_weight_int8(w_q):
     return PackedWeightInt8(w_q)
 
 
+class _WeightPackCache:
+    """Row-major int8 weights packed once, for callers that pass the reference's w_q layout.
+
+    w8a8_matmul and w8a8_matmul_grouped given a row-major int8 weight (as the reference's
+    scripts pass it, bench_graphs.py:55-64, correctness.py:36) look it up here and run the
+    packed-fragment kernels on its PackedWeightInt8: the results are bit-identical (the INT32
+    sums do not depend on the weight layout), and the packed layout streams each weight as 1 KB
+    contiguous fragments where the row-major one reads half cache lines.  An entry is keyed on
+    the weight's storage, offset, shape and strides and remembers the storage's version counter,
+    so an in-place update of the weight (through it or any view of it) repacks it on the next
+    call; the entry holds the source storage, so its memory cannot be reused under the key while
+    cached.  A miss inside graph capture does not pack (that would allocate): the call runs the
+    row-major kernel, with the same results.  Entries beyond the byte budget are evicted least
+    recently used first.  Controls: set_weight_pack_cache(enabled, budget_bytes),
+    clear_weight_pack_cache(); the environment variable SPECQ_PACK_CACHE=0 starts it disabled.
+    """
+
+    def __init__(self):
+        import collections
+        import threading
+        self.enabled = os.environ.get("SPECQ_PACK_CACHE", "1") != "0"
+        self.budget = 64 << 30
+        self.bytes = 0
+        self._d = collections.OrderedDict()
+        self._lock = threading.Lock()
+
+    @staticmethod
+    def _key(w: torch.Tensor):
+        return (w.device.index, w.untyped_storage().data_ptr(), w.storage_offset(), tuple(w.shape), tuple(w.stride()))
+
+    def lookup(self, w: torch.Tensor):
+        """The PackedWeightInt8 of w (packing it now on a miss), or None (disabled, or a miss
+        during graph capture)."""
+        if not self.enabled or w.dtype != torch.int8 or w.dim() != 2 or w.stride(-1) != 1:
+            return None
+        key = self._key(w)
+        with self._lock:
+            e = self._d.get(key)
+            if e is not None:
+                if e[1] == w._version:
+                    self._d.move_to_end(key)
+                    return e[0]
+                del self._d[key]
+                self.bytes -= e[0].data.numel()
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        packed = PackedWeightInt8(w)
+        with self._lock:
+            old = self._d.pop(key, None)
+            if old is not None:
+                self.bytes -= old[0].data.numel()
+            self._d[key] = (packed, w._version, w.untyped_storage())
+            self.bytes += packed.data.numel()
+            while self.bytes > self.budget and len(self._d) > 1:
+                _, (pw, _, _) = self._d.popitem(last=False)
+                self.bytes -= pw.data.numel()
+        return packed
+
+    def clear(self):
+        with self._lock:
+            self._d.clear()
+            self.bytes = 0
+
+
+_pack_cache = _WeightPackCache()
+
+
+def set_weight_pack_cache(enabled: bool = True, budget_bytes: int | None = None) -> None:
+    """Turn the transparent packing of row-major W8A8 weights on or off, and set its byte budget."""
+    _pack_cache.enabled = bool(enabled)
+    if budget_bytes is not None:
+        _pack_cache.budget = int(budget_bytes)
+    if not enabled:
+        _pack_cache.clear()
+
+
+def clear_weight_pack_cache() -> None:
+    """Drop every packed copy the transparent cache holds (their memory returns to torch)."""
+    _pack_cache.clear()
+
+
+def _aligned16(a_q: torch.Tensor, K: int) -> bool:
+    """The packed-fragment kernels read 16-byte pieces of the activation rows."""
+    return a_q.data_ptr() % 16 == 0 and (a_q.stride(0) % 16 == 0 or a_q.shape[0] <= 1) and K % 16 == 0
+
+
 def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK_K=128,
                 num_warps=4, num_stages=3, plan=None, grid_m_max=None, split_k=0, workspace=None,
                 plan_tiles=None):
@@ -265,6 +351,10 @@ def w8a8_matmul(a_q, sa, w_q, sw, out=None, BLOCK_M=16, BLOCK_N=None, BLOCK_K=12
     a_q = _rowmajor(a_q)
     if not packed:
         w_q = _rowmajor(w_q)
+        if _aligned16(a_q, K):
+            pw = _pack_cache.lookup(w_q)
+            if pw is not None:
+                w_q, packed = pw, True
     sa = sa.float().contiguous()
     sw = sw.float().contiguous()
     if sa.numel() < M or sw.numel() != N:
@@ -339,6 +429,10 @@ def w8a8_matmul_grouped(a_q, sa, weights, outs=None, BLOCK_M=16, BLOCK_N=None, n
         if (w.shape[1] if layout == 0 else w.K) != K:
             raise RuntimeError(f"w8a8_matmul_grouped: K mismatch {tuple(a_q.shape)} vs {tuple(w.shape)}")
     a_q = _rowmajor(a_q)
+    if layout == 0 and _aligned16(a_q, K):
+        pws = [_pack_cache.lookup(w) for w in ws_]
+        if all(pw is not None for pw in pws):
+            ws_, layout = pws, 1
     sa = sa.float().contiguous()
     sws = [sw.float().contiguous() for _, sw in weights]
     for sw, N in zip(sws, Ns):

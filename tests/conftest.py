@@ -36,3 +36,14 @@ def built_lib():
 
         build.build(quiet=True)
     return _lib.LIB_PATH
+
+
+@pytest.fixture(autouse=True)
+def _row_major_weights_run_row_major_kernels():
+    """Tests pass row-major int8 weights to exercise the row-major kernels, so the transparent
+    packing of such weights (kernels._WeightPackCache) is off unless a test turns it on."""
+    import kernels as K
+
+    K.set_weight_pack_cache(False)
+    yield
+    K.set_weight_pack_cache(False)
