@@ -170,7 +170,11 @@ int specq_w4a8_packed(const int8_t* a, int64_t lda, const void* w_packed,
  * register-stream kernel for token tiles of up to 32 rows, 2 = LDS-staged activations.  Both sum in the
  * same fp32 order, so results do not change either.  "attn_target_wgs": the workgroup count
  * the paged attention's split length aims at (0 = the device's CU count); results depend on
- * the split length, so calls compared bit for bit must use the same value. */
+ * the split length, so calls compared bit for bit must use the same value.  "tuned_tiles":
+ * 1 (default) = eager GEMM calls with automatic tiles on the Llama-3-8B launch shapes run the
+ * tile measured fastest for their 16-row step of M (a table built on a 256-CU MI355X), 0 = the
+ * cost models only; W8A8 results do not change, W4A16 results do not change within a weight
+ * layout's K order. */
 int specq_set_option(const char* name, int value);
 
 /* ---------------------------------------------------------------------------------------
@@ -225,6 +229,10 @@ int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t ldq, int wq_
  *   Other arguments as specq_w4a16, all members with the same wq_layout. */
 size_t specq_w4a16_grouped_workspace_size(int m_grid, int n_members, const int* N, int K, int block_m,
                                           int block_n, int num_warps, int split_k);
+/* The split count a grouped launch of these members runs (the same for every member), or 0
+ * when their counts differ and they run as one launch each; the tiles a grouped call picks
+ * are those specq_kernel_attrs_query reports for the members' total N with this split_k. */
+int specq_w4a16_grouped_split(int n_members, const int* N, int K, int split_k);
 int specq_w4a16_grouped(const void* a, int64_t lda, int n_members, const void* const* wq, const int64_t* ldq,
                         int wq_layout, const void* const* sc, const int64_t* ld_sc, void* const* c,
                         const int64_t* ldc, const int* N, int M, int K, int group, int grid_m_max,

@@ -1,12 +1,33 @@
 // Shared host-side pieces of the C ABI: thread-local error text, launch wrapper, device info,
 // and the kernel-attribute query that dispatches to each kernel family.
+#include <atomic>
 #include <mutex>
 #include <set>
 #include <vector>
 
 #include "api_common.hpp"
+#include "tuned_tiles.hpp"
 
 namespace specq {
+
+// Measured table on (1) or off (0, the cost models only), through specq_set_option("tuned_tiles", v).
+std::atomic<int> g_tuned_tiles{1};
+
+bool tuned_tile(int kind, int N, int K, int M, int* block_m, int* block_n, int* split_k) {
+  if (g_tuned_tiles.load() == 0 || device_cus() != 256 || M > 300) return false;
+  // Steps of the table: 0 = M 1..8, 1 = M 9..16, r >= 2 = the 16 rows up to 16 r.
+  const int step = M <= 8 ? 0 : (M + 15) / 16;
+  for (int i = 0; i < kTunedTileCount; ++i) {
+    const TunedTile& t = kTunedTiles[i];
+    if (t.kind == kind && t.N == N && t.K == K && t.step == step) {
+      *block_m = t.block_m;
+      *block_n = t.block_n;
+      *split_k = t.split_k;
+      return true;
+    }
+  }
+  return false;
+}
 
 static thread_local char g_err[512] = "";
 

@@ -55,6 +55,10 @@ int ensure_lds(const void* fn, size_t lds);
 // Number of CUs of the current device (cached per device).
 int device_cus();
 
+// The measured tile of a launch shape (tuned_tiles.hpp) for M rows: kind 0 = W8A8, 1 = W4A16;
+// N is the launch's total width.  Only on a device of the CU count the table was measured on.
+bool tuned_tile(int kind, int N, int K, int M, int* block_m, int* block_n, int* split_k);
+
 // Timestamp buffer the kernels of the diagnostics build write (specq_diag_set_timeline);
 // null, and never set, in the product build.
 void diag_timeline(uint64_t** tl, int* cap);

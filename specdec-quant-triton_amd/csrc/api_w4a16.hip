@@ -237,7 +237,12 @@ int w4_config(int layout, int m_grid, int N, int K, int block_m, int block_n, in
   } else if (ceil_div(N, 64) > device_cus()) {
     rw = 2;  // 128-channel blocks keep wide N (the fused gate_up) to one workgroup per CU
   }
-  if (block_m <= 0 && !plan_mode && rows16 > 1) {
+  int t_bm = 0, t_bn = 0, t_sk = 0;
+  if (block_m <= 0 && block_n <= 0 && !plan_mode && tuned_tile(1, N, K, std::max(m_grid, 1), &t_bm, &t_bn, &t_sk)) {
+    // A launch shape of the measured table: its tile (the split count still follows N and K).
+    mt = t_bm / 16;
+    rw = t_bn / 64;
+  } else if (block_m <= 0 && !plan_mode && rows16 > 1) {
     const int nb = K / 128;
     const int s_auto = std::min(split_k > 0 ? split_k : w4_auto_splits(N, nb), nb);
     const int s_eff = ceil_div(nb, ceil_div(nb, s_auto));
@@ -426,6 +431,13 @@ extern "C" int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t l
     return launch(cfg.fn, cfg.grid, kW4WsThreads, 0, (hipStream_t)stream, &pp);
   }
   return launch(cfg.fn, cfg.grid, cfg.family == kW4Rk ? 256 : kW4WsThreads, 0, (hipStream_t)stream, &p);
+}
+
+extern "C" int specq_w4a16_grouped_split(int n_members, const int* N, int K, int split_k) {
+  if (n_members < 1 || n_members > kW4MaxGroup || N == nullptr || K <= 0 || K % 128 != 0) return 0;
+  for (int g = 0; g < n_members; ++g)
+    if (N[g] <= 0) return 0;
+  return w4_group_splits(n_members, N, K, split_k);
 }
 
 extern "C" size_t specq_w4a16_grouped_workspace_size(int m_grid, int n_members, const int* N, int K, int block_m,

@@ -133,6 +133,7 @@ static int noalloc_scratch(void** out) {
 std::atomic<int> g_w8a8_path{0};
 extern std::atomic<int> g_w4a16_path;  // api_w4a16.hip
 extern std::atomic<int> g_attn_target;  // api_attn.hip
+extern std::atomic<int> g_tuned_tiles;  // api_common.hip
 
 namespace {
 
@@ -302,12 +303,20 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
     cfg->family = kPlan; cfg->layout = layout; cfg->vec = vec; cfg->nw = 4; cfg->rw = 1;
     return SPECQ_OK;
   }
-  // Eager calls with an automatic BLOCK_M on the streaming kernels choose the token-tile depth,
-  // channel block and split count together.
-  const bool joint = block_m <= 0 && !plan_mode && vec == 16 && path == 0 && rows16 > 1;
+  // Eager calls with automatic tiles on a launch shape of the measured table run its tile;
+  // other eager calls with an automatic BLOCK_M on the streaming kernels choose the token-tile
+  // depth, channel block and split count together from the cost model.
+  int t_bm = 0, t_bn = 0, t_sk = 0;
+  const bool tuned = block_m <= 0 && block_n <= 0 && split_k <= 0 && !plan_mode && vec == 16 && path == 0 &&
+                     layout != 2 && tuned_tile(0, N, K, std::max(m_grid, 1), &t_bm, &t_bn, &t_sk);
+  const bool joint = !tuned && block_m <= 0 && !plan_mode && vec == 16 && path == 0 && rows16 > 1;
   int joint_sel = -1, joint_splits = 1;
   int mt;
-  if (joint) {
+  if (tuned) {
+    mt = t_bm / 16;
+    joint_sel = t_bn == 16 ? 0 : (t_bn == 32 ? 1 : (t_bn == 64 ? 2 : 3));
+    joint_splits = t_sk;
+  } else if (joint) {
     w8a8_auto_tiles(m_grid, N, K, layout == 2 ? 0.5 : 1.0, want, split_k, &mt, &joint_sel, &joint_splits);
   } else if (block_m > 0) {
     SPECQ_REQUIRE(block_m % 16 == 0 && block_m <= 16 * kW8A8MaxMt, SPECQ_ENOTSUP,
@@ -332,7 +341,7 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   int nw = 4, rw = 1, bnsel = 2, ws_splits = 1;
   const void* fn = nullptr;
   if (family == kRk || family == kWs) {
-    if (joint) {
+    if (joint || tuned) {
       bnsel = joint_sel;
       ws_splits = joint_splits;
     } else if (family == kWs) {
@@ -392,6 +401,8 @@ int w8a8_config(int layout, int m_grid, int N, int K, int block_m, int block_n, 
   int splits;
   if (split_k > 0) {
     splits = split_k;
+  } else if (tuned) {
+    splits = t_sk;
   } else if (family == kLegacy) {
     const int target = 2 * device_cus();
     const int base = cfg->n_tiles * cfg->m_chunks;
@@ -855,6 +866,11 @@ extern "C" int specq_set_option(const char* name, int value) {
   if (strcmp(name, "w8a8_path") == 0) {
     SPECQ_REQUIRE(value >= 0 && value <= 3, SPECQ_EINVAL, "set_option: w8a8_path must be 0..3");
     g_w8a8_path.store(value);
+    return SPECQ_OK;
+  }
+  if (strcmp(name, "tuned_tiles") == 0) {
+    SPECQ_REQUIRE(value >= 0 && value <= 1, SPECQ_EINVAL, "set_option: tuned_tiles must be 0 or 1");
+    g_tuned_tiles.store(value);
     return SPECQ_OK;
   }
   if (strcmp(name, "w4a16_path") == 0) {

@@ -683,7 +683,17 @@ def w4a16_matmul_grouped(a, weights, group=128, outs=None, BLOCK_M=None, BLOCK_N
               arr(ctypes.c_int64, [o.stride(0) for o in outs]), n_arr, M, K, int(group), int(grid_m_max or 0),
               _plan_ptr(plan), bm, bn, 4, split_k, wptr, wbytes, _stream_ptr(a))
     _w4a16_kernel._note(a.device.index or 0, (bm, bn, "grouped", layout))
-    return outs, KernelInfo(1, layout | (16 if plan is not None else 0), m_grid, sum(Ns), K, bm, bn, 4, split_k)
+    # The launch runs the members' common split count: report the tiles of that launch.
+    sk = w4a16_group_split(Ns, K, split_k) if n > 1 else split_k
+    return outs, KernelInfo(1, layout | (16 if plan is not None else 0), m_grid, sum(Ns), K, bm, bn, 4,
+                            sk if sk > 0 else split_k)
+
+
+def w4a16_group_split(Ns, K: int, split_k: int = 0) -> int:
+    """The split count a grouped W4A16 launch of members of widths Ns runs, or 0 when their
+    counts differ (the members then run as one launch each)."""
+    arr = (ctypes.c_int * len(Ns))(*[int(n) for n in Ns])
+    return int(_lib.lib().specq_w4a16_grouped_split(len(Ns), arr, int(K), int(split_k)))
 
 
 # ----------------------------------------------------------------------------------------

@@ -66,6 +66,7 @@ SIGNATURES = {
                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_vp,
                              _c_int, _c_int, _c_int, _c_int, _c_vp, _c_size, _c_vp]),
     "specq_w4a16_grouped_workspace_size": (_c_size, [_c_int, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "specq_w4a16_grouped_split": (_c_int, [_c_int, _c_vp, _c_int, _c_int]),
     "specq_w4a16_grouped": (_c_int, [_c_vp, _c_i64, _c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                      _c_int, _c_int, _c_int, _c_int, _c_vp, _c_int, _c_int, _c_int, _c_int, _c_vp,
                                      _c_size, _c_vp]),

@@ -43,6 +43,9 @@ Subcommands (run from the repository root):
             boundaries, on the four config-1 shapes, each point the mean launch of a graph
             cycling over enough weight copies to stream from HBM.
   staircase-md  the markdown view of a staircase json.
+  tune      the measured tile table: every 16-row step of M on the config-1 launch shapes,
+            the automatic tiling against the reference's BLOCK_M and the other channel blocks.
+  tune-emit the C++ table (csrc/tuned_tiles.hpp) of a tune json; tune-md its markdown view.
 """
 from __future__ import annotations
 
@@ -692,22 +695,200 @@ def staircase(args) -> int:
             a = torch.randint(-127, 128, (300, Kd), dtype=torch.int8, device="cuda", generator=g)
         sa = torch.rand((300,), device="cuda", generator=g) * 0.015 + 0.005
         out = torch.empty((300, N), dtype=torch.float16, device="cuda")
+        timed = {}
         row = {}
+        kid = 1 if w4 else 0
         for bm in (None, 16, 32, 64, 128):
             for M in (range(1, 301) if bm is None else bounds):
+                # A fixed BLOCK_M that resolves to the same tiling as the automatic choice is the
+                # same launch: it reuses that timing instead of a second, noisy one.
+                cfg = K.KernelInfo(kid, 2 if w4 else 1, M, N, Kd, bm or 0, 0, 4, 0).config
+                key = (M, cfg["block_m"], cfg["block_n"], cfg["split_k"])
+                if key in timed:
+                    row.setdefault(str(bm or "auto"), {})[M] = timed[key]
+                    continue
+
                 def run(M=M, bm=bm):
                     for w in ws:
                         if w4:
                             K.w4a16_matmul(a[:M], w, sw, out=out[:M], BLOCK_M=bm)
                         else:
                             K.w8a8_matmul(a[:M], sa[:M], w, sw, out=out[:M], BLOCK_M=bm)
-                row.setdefault(str(bm or "auto"), {})[M] = round(_graph_us(run, copies, reps=3), 2)
+                t = round(min(_graph_us(run, copies, reps=3) for _ in range(2 if bm is None and M not in bounds else 3)), 2)
+                timed[key] = t
+                row.setdefault(str(bm or "auto"), {})[M] = t
         res[f"{N}x{Kd}"] = row
         print(f"[staircase] {'w4a16' if w4 else 'w8a8'} {N}x{Kd} done", flush=True)
         del ws
         torch.cuda.empty_cache()
     with open(args.out, "w") as fh:
         json.dump(res, fh)
+    return 0
+
+
+# The config-1 launch shapes the measured tile table covers: the four N x K of one GEMM and
+# the two grouped launches (q|k|v, gate|up) by their members.
+TUNE_SHAPES = {"4096x4096": [(4096, 4096)], "1024x4096": [(1024, 4096)], "14336x4096": [(14336, 4096)],
+               "4096x14336": [(4096, 14336)], "6144x4096": [(4096, 4096), (1024, 4096), (1024, 4096)],
+               "28672x4096": [(14336, 4096), (14336, 4096)]}
+
+
+def tune(args) -> int:
+    """Measured tile table: for each config-1 launch shape and each step of M (M = 1..8, 9..16,
+    then 16 rows at a time up to 300; timed at the step's first and last M, the mean of the
+    two), the mean launch of every candidate
+    tiling -- the automatic one, the reference's four BLOCK_M with the library's channel block
+    and split for that depth, and the automatic depth with every channel block -- each as a graph
+    cycling over enough weight copies to stream from HBM.  Writes {kind: {shape: {rows16:
+    dict(best=[BLOCK_M, BLOCK_N, split_k], us, auto=[...], auto_us)}}} for `tune-emit`."""
+    import torch
+
+    if PKG not in sys.path:
+        sys.path.insert(0, PKG)
+    import kernels as K
+    from specq import _lib
+
+    torch.cuda.set_device(0)
+    # "auto" below is the cost model's own choice, with any existing table switched off.
+    _lib.set_option("tuned_tiles", 0)
+    g = torch.Generator(device="cuda").manual_seed(17)
+    res = {}
+    for kind in args.kinds.split(","):
+        w4 = kind == "w4a16"
+        res[kind] = {}
+        for sname, members in TUNE_SHAPES.items():
+            Kd = members[0][1]
+            N_total = sum(N for N, _ in members)
+            wbytes = sum(N * Kd for N, _ in members) // (2 if w4 else 1)
+            copies = max(4, -(-600 * (1 << 20) // wbytes))
+            weights = []
+            for _ in range(copies):
+                mem = []
+                for N, _k in members:
+                    if w4:
+                        wp = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, Kd // 8), dtype=torch.int32, device="cuda",
+                                           generator=g)
+                        sc = (torch.rand((N, Kd // 128), device="cuda", generator=g) * 0.018 + 0.002).half()
+                        mem.append((K.pack_weight_int4(wp), sc))
+                    else:
+                        w = torch.randint(-127, 128, (N, Kd), dtype=torch.int8, device="cuda", generator=g)
+                        mem.append((K.pack_weight_int8(w), torch.rand((N,), device="cuda", generator=g) * 0.009 + 0.001))
+                weights.append(mem)
+            if w4:
+                a = torch.randn((300, Kd), device="cuda", generator=g).half()
+            else:
+                a = torch.randint(-127, 128, (300, Kd), dtype=torch.int8, device="cuda", generator=g)
+            sa = torch.rand((300,), device="cuda", generator=g) * 0.015 + 0.005
+            outs = [torch.empty((300, N), dtype=torch.float16, device="cuda") for N, _ in members]
+            kid = 1 if w4 else 0
+            bns = (64, 128) if w4 else (16, 32, 64, 128)
+            # A grouped W4A16 launch runs its members' common split count: resolve tiles with it.
+            gsk = K.w4a16_group_split([N for N, _ in members], Kd) if w4 else 0
+            table = {}
+            for r in range(0, 20):
+                # Step 0 is M = 1..8, step 1 M = 9..16, step r >= 2 the 16 rows up to 16 r.  Every
+                # M of a step runs its tile: time the candidates at both ends of the step and rank
+                # them by the mean.
+                lo, M = (1, 8) if r == 0 else ((9, 16) if r == 1 else (16 * (r - 1) + 1, min(16 * r, 300)))
+                Ms = sorted({lo, M})
+                auto = K.KernelInfo(kid, 2 if w4 else 1, M, N_total, Kd, 0, 0, 4, gsk).config
+                reqs = [(None, None)] + [(bm, None) for bm in (16, 32, 64, 128)] + [(auto["block_m"], bn) for bn in bns]
+                cands = []
+                for bm, bn in reqs:
+                    c = K.KernelInfo(kid, 2 if w4 else 1, M, N_total, Kd, bm or 0, bn or 0, 4, gsk).config
+                    t = (c["block_m"], c["block_n"], c["split_k"])
+                    if t not in cands:
+                        cands.append(t)
+                times, per_m = {}, {}
+                for bm, bn, sk in cands:
+                    tot = 0.0
+                    per_m[(bm, bn, sk)] = {}
+                    for Mx in Ms:
+                        def run(bm=bm, bn=bn, sk=sk, M=Mx):
+                            for mem in weights:
+                                o = [x[:M] for x in outs]
+                                if w4:
+                                    K.w4a16_matmul_grouped(a[:M], mem, outs=o, BLOCK_M=bm, BLOCK_N=bn,
+                                                           split_k=sk if len(members) == 1 else 0)
+                                else:
+                                    K.w8a8_matmul_grouped(a[:M], sa[:M], mem, outs=o, BLOCK_M=bm, BLOCK_N=bn,
+                                                          split_k=sk)
+                        t = min(_graph_us(run, copies, reps=4), _graph_us(run, copies, reps=4))
+                        per_m[(bm, bn, sk)][Mx] = t
+                        tot += t
+                    times[(bm, bn, sk)] = tot / len(Ms)
+                at = (auto["block_m"], auto["block_n"], auto["split_k"])
+                # The tile whose worst ratio to the fastest at each measured M of the step is
+                # smallest; the automatic tile unless that worst ratio is measurably better (2 %).
+                fastest = {Mx: min(per_m[c][Mx] for c in cands) for Mx in Ms}
+                regret = {c: max(per_m[c][Mx] / fastest[Mx] for Mx in Ms) for c in cands}
+                best = min(cands, key=lambda c: (regret[c], times[c]))
+                if regret[best] > regret[at] - 0.02:
+                    best = at
+                table[r] = dict(best=list(best), us=round(times[best], 3), auto=list(at), auto_us=round(times[at], 3),
+                                regret=round(regret[best], 4), auto_regret=round(regret[at], 4),
+                                candidates={f"{b}x{n}s{k}": {str(m): round(t, 3) for m, t in per_m[(b, n, k)].items()}
+                                            for (b, n, k) in cands})
+            res[kind][sname] = table
+            print(f"[tune] {kind} {sname}: " + ", ".join(f"{r}:{table[r]['best']}" for r in table), flush=True)
+            del weights
+            torch.cuda.empty_cache()
+    with open(args.out, "w") as fh:
+        json.dump(res, fh, indent=1)
+    return 0
+
+
+def tune_emit(args) -> int:
+    """The C++ table (csrc/tuned_tiles.hpp) of a `tune` json: one entry per kind, launch shape
+    and rows16 whose measured best differs from the cost model's choice or not, so the library
+    runs the measured tile for every step of M on these shapes."""
+    res = json.load(open(args.json))
+    lines = ["// Measured tile choices for the Llama-3-8B launch shapes on MI355X (256 CUs).",
+             "// Generated by `specq/profiling.py tune-emit` from a `specq/profiling.py tune` run (every",
+             "// step of M on each shape -- step 0 is M = 1..8, step 1 M = 9..16, step r >= 2 the 16 rows up",
+             "// to 16 r (M <= 300) -- the automatic tiling, the reference's four BLOCK_M and every channel",
+             "// block at the automatic depth, each timed at the step's first and last M as graphs of",
+             "// back-to-back launches streaming their weights from HBM); the fastest on average, or the",
+             "// model's own choice within 2 %.",
+             "// kind 0 = W8A8 (BLOCK_M, BLOCK_N, split_k), kind 1 = W4A16 (BLOCK_M, BLOCK_N; its split",
+             "// count follows from N and K).  N is the launch's total width (grouped launches: the sum).",
+             "#pragma once", "", "namespace specq {", "",
+             "struct TunedTile {", "  int kind, N, K, step, block_m, block_n, split_k;", "};", "",
+             "constexpr TunedTile kTunedTiles[] = {"]
+    n = 0
+    for kind, shapes in res.items():
+        kid = 1 if kind == "w4a16" else 0
+        for sname, table in shapes.items():
+            N, Kd = (int(x) for x in sname.split("x"))
+            for r in sorted(table, key=int):
+                bm, bn, sk = table[r]["best"]
+                lines.append(f"    {{{kid}, {N}, {Kd}, {int(r)}, {bm}, {bn}, {sk}}},")
+                n += 1
+    lines += ["};", f"constexpr int kTunedTileCount = {n};", "", "}  // namespace specq", ""]
+    with open(args.out, "w") as fh:
+        fh.write("\n".join(lines))
+    print(f"{n} entries -> {args.out}")
+    return 0
+
+
+def tune_md(args) -> int:
+    """Markdown view of a `tune` json: per shape and rows16 the model's tile, the measured best
+    and the gain."""
+    res = json.load(open(args.json))
+    for kind, shapes in res.items():
+        for sname, table in shapes.items():
+            print(f"\n### {kind} {sname}\n")
+            print("| step (M range) | model tile (BM x BN, split) | µs | measured best | µs | model / best "
+                  "| worst ratio to the fastest: model / chosen |")
+            print("|---|---|---|---|---|---|---|")
+            for r in sorted(table, key=int):
+                e = table[r]
+                fmt = lambda t: f"{t[0]} x {t[1]}, {t[2]}"  # noqa: E731
+                ri = int(r)
+                rng = "1-8" if ri == 0 else ("9-16" if ri == 1 else f"{16 * ri - 15}-{min(16 * ri, 300)}")
+                print(f"| {r} ({rng}) | {fmt(e['auto'])} | {e['auto_us']:.2f} | {fmt(e['best'])} | "
+                      f"{e['us']:.2f} | {e['auto_us'] / e['us']:.3f} | {e.get('auto_regret', 0):.3f} / "
+                      f"{e.get('regret', 0):.3f} |")
     return 0
 
 
@@ -755,13 +936,21 @@ def main() -> int:
     m.add_argument("--map", required=True)
     sm = sub.add_parser("staircase-md")
     sm.add_argument("json")
+    tu = sub.add_parser("tune")
+    tu.add_argument("--kinds", default="w8a8,w4a16")
+    tu.add_argument("--out", required=True)
+    te = sub.add_parser("tune-emit")
+    te.add_argument("json")
+    te.add_argument("--out", required=True)
+    tm = sub.add_parser("tune-md")
+    tm.add_argument("json")
     c = sub.add_parser("staircase")
     c.add_argument("--out", required=True)
     c.add_argument("--kind", choices=("w8a8", "w4a16"), default="w8a8")
     args = ap.parse_args()
     return {"probe": probe, "stats": stats, "traffic": traffic, "mfma": mfma, "staircase": staircase,
             "staircase-md": staircase_md, "sq": sq, "launches": launches, "timeline": timeline,
-            "floors": floors}[args.cmd](args)
+            "floors": floors, "tune": tune, "tune-emit": tune_emit, "tune-md": tune_md}[args.cmd](args)
 
 
 if __name__ == "__main__":
