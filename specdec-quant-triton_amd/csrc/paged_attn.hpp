@@ -197,6 +197,7 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
                                                 uint8_t (&ring2)[kAttnWaves][AttnSlot<D>::value],
                                                 uint8_t (&ring3)[kAttnWaves][AttnSlot<D>::value],
                                                 float (&ml_lds)[kAttnWaves][2][RBL * 16],
+                                                float (&row_lds)[2][RBL * 16],
                                                 v8h (&q_lds)[RBL][D / 32][64], int& s_last) {
   static_assert(RB <= RBL, "LDS arrays hold the row blocks");
   constexpr int NU = D / 32;              // MFMA K-steps over the head dimension
@@ -626,14 +627,28 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
   __syncthreads();
   tl_mark(p.tl, p.tl_cap, 7);  // diagnostics build: every wave's chunk loop done
   constexpr int QPR = D / 4;  // 4-float granules per row
+  // Each row's workgroup statistics, once: the row max over the waves and, in wave 0, the sum
+  // l = sum_w exp2(m_w - max) l_w in wave order, kept in LDS for the stores and the split
+  // hand-off below (visible after the merge's next barrier).
   float wsc[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int row = rb * 16 + r;
-    float mx = ml_lds[0][0][row];
+    float mv[kAttnWaves];
 #pragma unroll
-    for (int ww = 1; ww < kAttnWaves; ++ww) mx = fmaxf(mx, ml_lds[ww][0][row]);
-    wsc[rb] = fast_exp2(m_run[rb] - ((mx == -INFINITY) ? 0.f : mx));
+    for (int ww = 0; ww < kAttnWaves; ++ww) mv[ww] = ml_lds[ww][0][row];
+    float mx = mv[0];
+#pragma unroll
+    for (int ww = 1; ww < kAttnWaves; ++ww) mx = fmaxf(mx, mv[ww]);
+    const float ms = (mx == -INFINITY) ? 0.f : mx;
+    wsc[rb] = fast_exp2(m_run[rb] - ms);
+    if (w == 0 && g == 0) {
+      float l = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < kAttnWaves; ++ww) l += fast_exp2(mv[ww] - ms) * ml_lds[ww][1][row];
+      row_lds[0][row] = mx;
+      row_lds[1][row] = l;
+    }
   }
   const int pr = w & 3;  // the wave pair
   // O^T rows 4g + e of block db hold d = ND (4g + e) + db: granule (ND / 4)(4g + e) + cc.
@@ -674,11 +689,8 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
     return *reinterpret_cast<const v4f*>(reinterpret_cast<const float*>(base) + (n & 7) * D + 4 * (c ^ n));
   };
   auto row_stats = [&](int row, float& mx, float& l) {
-    mx = ml_lds[0][0][row];
-    for (int ww = 1; ww < kAttnWaves; ++ww) mx = fmaxf(mx, ml_lds[ww][0][row]);
-    const float ms = (mx == -INFINITY) ? 0.f : mx;
-    l = 0.f;
-    for (int ww = 0; ww < kAttnWaves; ++ww) l += fast_exp2(ml_lds[ww][0][row] - ms) * ml_lds[ww][1][row];
+    mx = row_lds[0][row];
+    l = row_lds[1][row];
   };
   constexpr int ITEMS = (ROWS * QPR + NT - 1) / NT;
   v4f o[ITEMS];
@@ -827,13 +839,14 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
   __shared__ __attribute__((aligned(16))) uint8_t ring2[kAttnWaves][AttnSlot<D>::value]; \
   __shared__ __attribute__((aligned(16))) uint8_t ring3[kAttnWaves][AttnSlot<D>::value]; \
   __shared__ float ml_lds[kAttnWaves][2][(RBL) * 16];                                 \
+  __shared__ float row_lds[2][(RBL) * 16];                                            \
   __shared__ __attribute__((aligned(16))) v8h q_lds[RBL][D / 32][64];                 \
   __shared__ int s_last
 
 template <int D, int RB, typename ST>
 __global__ __launch_bounds__(kAttnThreads) void paged_attn_kernel(AttnParams p) {
   SPECQ_ATTN_LDS(RB);
-  paged_attn_body<D, RB, ST, RB>(p, ring0, ring1, ring2, ring3, ml_lds, q_lds, s_last);
+  paged_attn_body<D, RB, ST, RB>(p, ring0, ring1, ring2, ring3, ml_lds, row_lds, q_lds, s_last);
 }
 
 // Plan-mode launch captured for programs of up to RBMAX row blocks: the active q_len (plan[1])
@@ -845,13 +858,13 @@ __global__ __launch_bounds__(kAttnThreads) void paged_attn_plan_kernel(AttnParam
   const int q_len = min(max(p.plan[1], 0), p.ql_grid);
   const int rb = uniform(min(max((min(q_len, p.QPP) * p.G + 15) / 16, 1), RBMAX));
   if (rb == 1) {
-    paged_attn_body<D, 1, ST, RBMAX>(p, ring0, ring1, ring2, ring3, ml_lds, q_lds, s_last);
+    paged_attn_body<D, 1, ST, RBMAX>(p, ring0, ring1, ring2, ring3, ml_lds, row_lds, q_lds, s_last);
   } else if (rb == 2) {
-    if constexpr (RBMAX >= 2) paged_attn_body<D, 2, ST, RBMAX>(p, ring0, ring1, ring2, ring3, ml_lds, q_lds, s_last);
+    if constexpr (RBMAX >= 2) paged_attn_body<D, 2, ST, RBMAX>(p, ring0, ring1, ring2, ring3, ml_lds, row_lds, q_lds, s_last);
   } else if (rb == 3) {
-    if constexpr (RBMAX >= 3) paged_attn_body<D, 3, ST, RBMAX>(p, ring0, ring1, ring2, ring3, ml_lds, q_lds, s_last);
+    if constexpr (RBMAX >= 3) paged_attn_body<D, 3, ST, RBMAX>(p, ring0, ring1, ring2, ring3, ml_lds, row_lds, q_lds, s_last);
   } else {
-    if constexpr (RBMAX >= 4) paged_attn_body<D, 4, ST, RBMAX>(p, ring0, ring1, ring2, ring3, ml_lds, q_lds, s_last);
+    if constexpr (RBMAX >= 4) paged_attn_body<D, 4, ST, RBMAX>(p, ring0, ring1, ring2, ring3, ml_lds, row_lds, q_lds, s_last);
   }
 }
 #undef SPECQ_ATTN_LDS

@@ -10,7 +10,9 @@ import os
 import threading
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG_DIR, "libspecq.so")
+# SPECQ_LIB_PATH names another build of the same library (for example one compiled with
+# different tuning); there is no fallback: a missing file raises like a missing libspecq.so.
+LIB_PATH = os.environ.get("SPECQ_LIB_PATH") or os.path.join(PKG_DIR, "libspecq.so")
 
 _c_int, _c_i64, _c_size, _c_vp, _c_float = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_float
 
