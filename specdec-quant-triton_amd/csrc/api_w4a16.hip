@@ -424,6 +424,7 @@ extern "C" int specq_w4a16(const void* a, int64_t lda, const void* wq, int64_t l
   p.partials = need ? (float*)((char*)workspace + kCounterBytes) : nullptr;
   p.vec_store = ((uintptr_t)c % 8 == 0) && (ldc % 4 == 0);
   p.n_grp = 1;
+  diag_timeline(&p.tl, &p.tl_cap);
   if (cfg.family == kW4Plan) {
     W4PlanParams pp;
     pp.p = p;
@@ -518,6 +519,7 @@ extern "C" int specq_w4a16_grouped(const void* a, int64_t lda, int n_members, co
   p.partials = need ? (float*)((char*)workspace + kCounterBytes) : nullptr;
   p.vec_store = vec_ok(0);
   p.n_grp = n_members;
+  diag_timeline(&p.tl, &p.tl_cap);
   for (int g = 1; g < kW4MaxGroup; ++g) {
     const bool on = g < n_members;
     p.grp_tile_end[g - 1] = on ? tile_end[g - 1] : 0;

@@ -266,6 +266,33 @@ __device__ __forceinline__ bool chunked_unit(int m_chunks, int units, int& mc, i
 }
 __host__ __device__ inline int chunked_grid(int units, int m_chunks) { return units * m_chunks; }
 
+// Channel tile and split-K index of chunk-local unit `unit` (n_tiles tiles x splits).  The
+// splits of a tile are placed 8 units apart, in blocks of 8 tiles x splits units (the tiles of a
+// trailing partial block run their splits back to back), so the workgroups of one tile share
+// blockIdx.x mod 8 -- the XCD the dispatcher deals them to -- and the workgroups running next to
+// each other in dispatch order cover different tiles.  Measured on the split-K launches of the
+// Llama-3-8B linears: the device-coherent stores of the partial tiles complete in 0.4-0.6 us
+// instead of 0.9-1.4 us when neighbouring workgroups are the splits of one tile (W4A16 q|k|v at
+// M = 72: 19.3 -> 16.3 us per launch).  The result does not depend on the order.
+__device__ __forceinline__ void split_decode(int unit, int n_tiles, int splits, int& tile, int& split) {
+  if (splits == 1) {
+    tile = unit;
+    split = 0;
+    return;
+  }
+  constexpr int X = 8;
+  const int full = (n_tiles / X) * X;
+  if (unit < full * splits) {
+    const int blk = unit / (X * splits), r = unit - blk * (X * splits);
+    tile = blk * X + r % X;
+    split = r / X;
+    return;
+  }
+  const int r = unit - full * splits;
+  tile = full + r / splits;
+  split = r % splits;
+}
+
 __device__ __forceinline__ void wait_all_memory() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);

@@ -233,13 +233,15 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
   // round trip before the first K/V DMA.
   const int cap = p.max_pages * p.PAGE;
   const int split_tokens = kAttnUnit * attn_split_units(cap, n_seqs * p.H_KV, p.target_wgs);
-  // The grid is one-dimensional: workgroup id = program * splits + split, with the split count
-  // of the active sequences, so the workgroups that have work are the first ones dispatched and
-  // a plan-mode grid (sized for the worst active count) carries few idle workgroups.
+  // The grid is one-dimensional: the first (active programs) x (splits of the active count)
+  // workgroups have work, in blocks of 8 programs whose splits sit 8 workgroups apart
+  // (split_decode), so the workgroups that have work are the first ones dispatched and a
+  // plan-mode grid (sized for the worst active count) carries few idle workgroups.
   const int ns_act = (cap + split_tokens - 1) / split_tokens;
-  const int prog = (int)blockIdx.x / ns_act;
-  const int split = (int)blockIdx.x - prog * ns_act;
-  if (prog >= n_seqs * p.H_KV * p.n_qc) return;
+  const int n_prog = n_seqs * p.H_KV * p.n_qc;
+  if ((int)blockIdx.x >= n_prog * ns_act) return;
+  int prog, split;
+  split_decode((int)blockIdx.x, n_prog, ns_act, prog, split);
   const int qc = prog % p.n_qc, kvh = (prog / p.n_qc) % p.H_KV, b = prog / (p.n_qc * p.H_KV);
   if (qc * p.QPP >= q_len) return;
   const int s0 = split * split_tokens;

@@ -63,6 +63,8 @@ struct W4A16Params {
   _Float16* grp_C[kW4MaxGroup - 1];
   int64_t grp_ldc[kW4MaxGroup - 1];
   int grp_N[kW4MaxGroup - 1], grp_ntiles16[kW4MaxGroup - 1], grp_vec_store[kW4MaxGroup - 1];
+  uint64_t* tl;  // diagnostics build only: per-workgroup timestamps (null otherwise)
+  int tl_cap;    // workgroups tl has room for
 };
 
 // Points the weight, scale and output fields of p at the GEMM of a grouped launch that owns
@@ -241,8 +243,7 @@ __device__ __forceinline__ void w4_store4(const W4A16Params& p, int m, int n, v4
 __device__ __forceinline__ bool w4_decode_id(const W4A16Params& p, int& mc, int& tile, int& split) {
   int unit;
   if (!chunked_unit(p.m_chunks, p.units, mc, unit)) return false;
-  split = unit % p.splits;
-  tile = unit / p.splits;
+  split_decode(unit, p.n_tiles, p.splits, tile, split);
   return true;
 }
 
@@ -255,28 +256,49 @@ template <int BM, int BN>
 __device__ __forceinline__ void w4_publish_quad(rsrc_t prs, int split, int ml, int nl, v4f v) {
   publish16(prs, (uint32_t)(((split * BM + ml) * BN + nl) * 4), __builtin_bit_cast(v4i, v));
 }
-// The last workgroup of the tile to arrive adds the splits in split order (0, 1, 2, ...),
-// with four splits' loads in flight at a time.
-template <int BM, int BN>
+// The last workgroup of the tile to arrive adds the splits in split order (0, 1, 2, ...).
+// Thread t owns quads t, t + NT, ...; the partials of up to QG quads x SB splits are loaded
+// together, so the sum costs one memory round trip per group of quads.
+template <int BM, int BN, int NT>
 __device__ __forceinline__ void w4_splitk_finish(const W4A16Params& p, rsrc_t prs, int cidx, int m0, int nbase,
                                                  int M, int* s_last) {
-  if (!arrive_last(p.counters + cidx, p.splits, s_last)) return;
+  if (!arrive_last(p.counters + cidx, p.splits, s_last, p.tl, p.tl_cap)) return;
   constexpr int QUADS = BM * BN / 4;
-  for (int q = threadIdx.x; q < QUADS; q += blockDim.x) {
-    const int ml = q / (BN / 4), nl = (q % (BN / 4)) * 4;
-    const int m = m0 + ml, n = nbase + nl;
-    if (m >= M || n >= p.N) continue;
-    v4f s = __builtin_bit_cast(v4f, collect16(prs, (uint32_t)((ml * BN + nl) * 4)));
-    for (int sp0 = 1; sp0 < p.splits; sp0 += 4) {
-      v4i t[4];
+  constexpr int QPT = (QUADS + NT - 1) / NT;  // quads per thread
+  constexpr int QG = QPT <= 4 ? QPT : 4;      // quads summed together
+  constexpr int SB = 16 / QG > 8 ? 8 : 16 / QG;  // splits loaded together
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        t[u] = collect16(prs, oob_unless(sp0 + u < p.splits, (uint32_t)((((sp0 + u) * BM + ml) * BN + nl) * 4)));
+  for (int g0 = 0; g0 < QPT; g0 += QG) {
+    int ml[QG], nl[QG];
+    bool ok[QG];
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (sp0 + u < p.splits) s += __builtin_bit_cast(v4f, t[u]);
+    for (int i = 0; i < QG; ++i) {
+      const int q = (int)threadIdx.x + (g0 + i) * NT;
+      ml[i] = q / (BN / 4);
+      nl[i] = (q % (BN / 4)) * 4;
+      ok[i] = (g0 + i < QPT) & (q < QUADS) & (m0 + ml[i] < M) & (nbase + nl[i] < p.N);
     }
-    w4_store4(p, m, n, s);
+    v4f s[QG];
+    for (int sp0 = 0; sp0 < p.splits; sp0 += SB) {
+      v4i t[QG][SB];
+#pragma unroll
+      for (int i = 0; i < QG; ++i)
+#pragma unroll
+        for (int u = 0; u < SB; ++u)
+          t[i][u] = collect16(prs, oob_unless(ok[i] & (sp0 + u < p.splits),
+                                              (uint32_t)((((sp0 + u) * BM + ml[i]) * BN + nl[i]) * 4)));
+#pragma unroll
+      for (int i = 0; i < QG; ++i)
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          const v4f v = __builtin_bit_cast(v4f, t[i][u]);
+          if (sp0 + u == 0) s[i] = v;
+          else if (sp0 + u < p.splits) s[i] += v;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < QG; ++i)
+      if (ok[i]) w4_store4(p, m0 + ml[i], nbase + nl[i], s[i]);
   }
 }
 
@@ -295,6 +317,8 @@ __device__ __forceinline__ void w4_epilogue(const W4A16Params& p, const v4f (&ac
         const int m = m0 + 16 * j + r, n = n0_wave + 16 * i + 4 * g;
         if (m < M && n < p.N) w4_store4(p, m, n, acc[i][j]);
       }
+    tl_mark(p.tl, p.tl_cap, 3);          // diagnostics build: stores issued
+    tl_mark_drained(p.tl, p.tl_cap, 4);  // ... and completed
     return;
   }
   const int cidx = mc * p.n_tiles + tile;
@@ -303,7 +327,9 @@ __device__ __forceinline__ void w4_epilogue(const W4A16Params& p, const v4f (&ac
   for (int i = 0; i < RW; ++i)
 #pragma unroll
     for (int j = 0; j < MT; ++j) w4_publish_quad<BM, BN>(prs, split, 16 * j + r, nl_wave + 16 * i + 4 * g, acc[i][j]);
-  w4_splitk_finish<BM, BN>(p, prs, cidx, m0, n0_wave - nl_wave, M, s_last);
+  tl_mark(p.tl, p.tl_cap, 3);  // diagnostics build: partials issued
+  w4_splitk_finish<BM, BN, 256>(p, prs, cidx, m0, n0_wave - nl_wave, M, s_last);
+  tl_mark_drained(p.tl, p.tl_cap, 4);  // diagnostics build: hand-off (and, if last, the sum) done
 }
 
 }  // namespace specq

@@ -40,6 +40,7 @@ __global__ __launch_bounds__(256) void w4a16_rk_kernel(W4A16Params p) {
   using C = W4RkCfg<MT, RW, LAYOUT>;
   static_assert(C::OK, "W4A16 register-stream tile does not fit the load counter");
   constexpr int BM = C::BM, BNW = C::BNW, BN = C::BN, NS = C::NS, D = C::D, PER = C::PER, NSC = C::NSC;
+  tl_mark(p.tl, p.tl_cap, 0);  // diagnostics build: workgroup start
 
   int mc, tile, split;
   if (!w4_decode_id(p, mc, tile, split)) return;
@@ -123,6 +124,7 @@ __global__ __launch_bounds__(256) void w4a16_rk_kernel(W4A16Params p) {
     });
   }
   wait_vmcnt<0>();
+  tl_mark(p.tl, p.tl_cap, 2);  // diagnostics build: main loop done
   v4f sum[RW][MT];
 #pragma unroll
   for (int i = 0; i < RW; ++i)

@@ -63,6 +63,7 @@ __device__ __forceinline__ void w4a16_ws_body(W4A16Params p, SlotPtr slot_ptr) {
   static_assert(C::OK, "unsupported W4A16 weight-stream tile");
   constexpr int BM = C::BM, BNW = C::BNW, BN = C::BN, A_L = C::A_L, NS = C::NS, D = C::D, P = C::P;
   constexpr int WPER = C::WPER, NSC = C::NSC;
+  tl_mark(p.tl, p.tl_cap, 0);  // diagnostics build: workgroup start
 
   int mc, tile, split;
   if (!w4_decode_id(p, mc, tile, split)) return;
@@ -167,6 +168,9 @@ __device__ __forceinline__ void w4a16_ws_body(W4A16Params p, SlotPtr slot_ptr) {
       const int c = c0 + cb;
       wait_vmcnt<P * S * WPER + (P - 1) * A_L>();  // this wave's DMA of chunk c has landed
       wg_barrier_lds();  // ... every wave's has, and nobody reads slot (c + P) % NSLOT any more
+      if constexpr (cb == 0) {
+        if (c0 == 0) tl_mark(p.tl, p.tl_cap, 1);  // diagnostics build: first chunk landed
+      }
       dma_chunk(c + P, slot_ptr(std::integral_constant<int, (cl + P) % NSLOT>{}, h));
       __builtin_amdgcn_sched_barrier(0);
       const uint8_t* aslot = slot_ptr(std::integral_constant<int, cl>{}, h);
@@ -202,6 +206,7 @@ __device__ __forceinline__ void w4a16_ws_body(W4A16Params p, SlotPtr slot_ptr) {
     });
   }
   wait_vmcnt<0>();
+  tl_mark(p.tl, p.tl_cap, 2);  // diagnostics build: main loop done
 
   // Hand-over: stream 1's tiles into the streams' first slots (every wave is past its last
   // read of the rings), stream 0 adds them: even + odd.
@@ -232,6 +237,8 @@ __device__ __forceinline__ void w4a16_ws_body(W4A16Params p, SlotPtr slot_ptr) {
           if (m < M && n < p.N) w4_store4(p, m, n, acc[i][j]);
         }
     }
+    tl_mark(p.tl, p.tl_cap, 3);          // diagnostics build: stores issued
+    tl_mark_drained(p.tl, p.tl_cap, 4);  // ... and completed
     return;
   }
   const int cidx = mc * p.n_tiles + tile;
@@ -242,11 +249,13 @@ __device__ __forceinline__ void w4a16_ws_body(W4A16Params p, SlotPtr slot_ptr) {
 #pragma unroll
       for (int j = 0; j < MT; ++j) w4_publish_quad<BM, BN>(prs, split, 16 * j + r, w * BNW + 16 * i + 4 * g, acc[i][j]);
   }
+  tl_mark(p.tl, p.tl_cap, 3);  // diagnostics build: partials issued
   // Every thread of the workgroup takes part in the arrival and the last one's finish.
-  w4_splitk_finish<BM, BN>(p, prs, cidx, m0, ltile * BN, M, &s_last_ws4);
+  w4_splitk_finish<BM, BN, 512>(p, prs, cidx, m0, ltile * BN, M, &s_last_ws4);
+  tl_mark_drained(p.tl, p.tl_cap, 4);  // diagnostics build: hand-off (and, if last, the sum) done
 }
 
-constexpr int kW4WsThreads = 512;
+constexpr int kW4WsThreads = 512;  // the split-K finish above is instantiated for 512 threads
 
 template <int MT, int RW, int S, int NSLOT, int NSW, int LAYOUT>
 __global__ __launch_bounds__(kW4WsThreads) void w4a16_ws_kernel(W4A16Params p) {

@@ -214,24 +214,23 @@ __device__ __forceinline__ void w8a8_publish_quad(rsrc_t prs, int split, int ml,
   publish16(prs, (uint32_t)(((split * BM + ml) * BN + nl) * 4), v);
 }
 // Called by every thread after its publishes: the last workgroup of the tile to arrive sums
-// the splits and applies the epilogue.  Thread t owns quads t, t + NT, ...; the scales and
-// the partials of up to QG quads x SB splits are loaded together, so the sum costs one
-// memory round trip per group instead of one per quad (INT32 sums are order independent).
+// the splits and applies the epilogue.  Thread t owns quads t, t + NT, ...; the partials of up
+// to QG quads x SB splits are loaded together, so the sum costs one memory round trip per
+// group instead of one per quad (INT32 sums are order independent).  The first group's scales
+// are loaded before the arrival, in flight with the stores of the partial tiles.
 template <int BM, int BN, int NT>
 __device__ __forceinline__ void w8a8_splitk_finish(const W8A8Params& p, rsrc_t prs, int cidx, int m0, int nbase,
                                                    int M, int* s_last) {
-  if (!arrive_last(p.counters + cidx, p.splits, s_last, p.tl, p.tl_cap)) return;
   constexpr int QUADS = BM * BN / 4;
   constexpr int QPT = (QUADS + NT - 1) / NT;                   // quads per thread
   // Up to 8 quads per thread are summed in one round of loads (up to 32 loads in flight);
   // the deepest tiles, whose main loops need every register, take 4 quads per round.
   constexpr int QG = QPT <= 8 ? QPT : 4;                       // quads summed together
   constexpr int SB = (QPT <= 8 ? 32 : 16) / QG > 8 ? 8 : (QPT <= 8 ? 32 : 16) / QG;  // splits loaded together
-#pragma unroll
-  for (int g0 = 0; g0 < QPT; g0 += QG) {
-    int ml[QG], nl[QG];
-    bool ok[QG];
-    float a[QG], w[QG][4];
+  int ml[QG], nl[QG];
+  bool ok[QG];
+  float a[QG], w[QG][4];
+  auto prepare = [&](int g0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < QG; ++i) {
       const int q = (int)threadIdx.x + (g0 + i) * NT;
@@ -245,6 +244,12 @@ __device__ __forceinline__ void w8a8_splitk_finish(const W8A8Params& p, rsrc_t p
 #pragma unroll
       for (int c = 0; c < 4; ++c) w[i][c] = p.sw[min(ok[i] ? n + c : nbase, p.N - 1)];
     }
+  };
+  prepare(0);
+  if (!arrive_last(p.counters + cidx, p.splits, s_last, p.tl, p.tl_cap)) return;
+#pragma unroll
+  for (int g0 = 0; g0 < QPT; g0 += QG) {
+    if (g0 > 0) prepare(g0);
     v4i s[QG];
 #pragma unroll
     for (int i = 0; i < QG; ++i) s[i] = v4i{0, 0, 0, 0};

@@ -68,8 +68,8 @@ __device__ __forceinline__ void w8a8_ws_body(W8A8Params p, SlotPtr slot_ptr) {
 
   int mc, unit;
   if (!chunked_unit(p.m_chunks, p.n_tiles * p.splits, mc, unit)) return;
-  const int split = unit % p.splits;
-  const int tile = unit / p.splits;          // launch-wide tile (counters, partials)
+  int split, tile;  // tile: launch-wide (counters, partials)
+  split_decode(unit, p.n_tiles, p.splits, tile, split);
   const int ltile = w8a8_select_member(p, tile);  // tile within its GEMM (weights, outputs)
 
   int M = p.M;

@@ -11,6 +11,7 @@ Subcommands (run from the repository root):
               w8l:L:M   launch L of a config-1 layer as bench.py runs it (qkv, o, gate_up,
                         down; q|k|v and gate|up grouped over separate packed weights)
               w4a16:M   the same shape in W4A16 (load-time packed INT4, group 128)
+              w4l:L:M   launch L of a config-2 layer as bench.py's W4A16 step runs it
               attn:B:k:ctx  INT8 paged verification attention (32/8 heads, D=128, fp32
                         scales, fused QPP=k+1)
               copy      torch.neg over 1 GiB of int32 (reads and writes 1 GiB): the
@@ -191,6 +192,32 @@ def _make_kind(kind: str, args, K, gen, g, torch):
         bytes_ = sum(Ng * Kl + 4 * Ng + 2 * M * Ng for Ng, _k in shapes) + M * Kl + 4 * M
         ops = sum(2 * M * Ng * Kl for Ng, _k in shapes)
         wl = f"W8A8 {lname} ({'+'.join(f'{Ng}x{Kl}' for Ng, _k in shapes)}) M={M}"
+    elif f[0] == "w4l":
+        # One of the four launches of a config-2 layer (bench.py's W4A16 step): qkv and gate_up
+        # grouped over their separate packed INT4 weights, o and down alone.
+        lname, M = f[1], int(f[2])
+        shapes = {"qkv": [(4096, 4096), (1024, 4096), (1024, 4096)], "o": [(4096, 4096)],
+                  "gate_up": [(14336, 4096), (14336, 4096)], "down": [(4096, 14336)]}[lname]
+        Kl = shapes[0][1]
+        layers = []
+        for _ in range(args.layers):
+            mem = []
+            for Ng, _k in shapes:
+                wp = torch.randint(-2 ** 31, 2 ** 31 - 1, (Ng, Kl // 8), dtype=torch.int32, device="cuda", generator=g)
+                sc = (torch.rand((Ng, Kl // 128), device="cuda", generator=g) * 0.018 + 0.002).half()
+                mem.append((K.pack_weight_int4(wp), sc))
+                del wp
+            layers.append(mem)
+        x = torch.randn((M, Kl), device="cuda", generator=g).half()
+        outs = [torch.empty((M, Ng), dtype=torch.float16, device="cuda") for Ng, _k in shapes]
+
+        def run(layers=layers, x=x, outs=outs):
+            for mem in layers:
+                K.w4a16_matmul_grouped(x, mem, outs=outs)
+        _, ck = K.w4a16_matmul_grouped(x, layers[0], outs=outs)
+        bytes_ = sum(Ng * Kl // 2 + 2 * Ng * (Kl // 128) + 2 * M * Ng for Ng, _k in shapes) + 2 * M * Kl
+        ops = sum(2 * M * Ng * Kl for Ng, _k in shapes)
+        wl = f"W4A16 {lname} ({'+'.join(f'{Ng}x{Kl}' for Ng, _k in shapes)}) M={M}"
     elif f[0] == "w4a16":
         M = int(f[1])
         layers = []
