@@ -13,7 +13,7 @@
 //    program reads each K/V byte once for all (k+1) * G rows.
 //  * Split length follows the work on the device: a split is a whole number of 128-token
 //    units, as many as make (active sequences) x (KV heads) x (splits) reach the CU count for
-//    a sequence filling the block table, at most 4096 tokens and at most 64 splits, and at
+//    a sequence filling the block table, at most 8192 tokens and at most 64 splits, and at
 //    least 256 tokens (384 once the block table holds 4096 tokens or more), the units spread
 //    evenly over the splits (attn_split_units).  It depends only on the block table's
 //    capacity and the number of active sequences, so a QPP=1 and a fused program, and an eager and a plan-mode call, cut
@@ -80,14 +80,17 @@ constexpr int kAttnWaves = 8;                       // two per SIMD
 constexpr int kAttnThreads = kAttnWaves * 64;
 constexpr int kAttnUnit = kAttnChunk * kAttnWaves;  // 128 tokens: one chunk of every wave
 constexpr int kAttnMinUnits = 2;                    // shortest split: 256 tokens (384 from 4096 tokens)
-constexpr int kAttnMaxUnits = 32;                   // longest split: 4096 tokens (32 page ids per wave)
+// Longest split: 8192 tokens, 64 chunks per wave, whose page ids the wave's 64 lanes hold.  At
+// 32 sequences x 8 KV heads and 4096 tokens the programs alone fill the CUs: one split each runs
+// one round of 256 workgroups, where 4096-token splits ran two rounds of 256 (91.6 us).
+constexpr int kAttnMaxUnits = 64;
 constexpr int kAttnMergeMax = 64;                   // most splits one program merges
 constexpr int kAttnRing = 4;                        // LDS chunk slots per wave
 // Largest unnormalised probability p = exp2(s - m) the lazy running max lets through (2^6):
 // p * vs stays at most 64 * 65504 / 127 < 65504, inside fp16, for the V scale of any fp16 row
 // quantised to int8 (vs <= 65504 / 127).
 constexpr float kAttnLazyP = 64.f;
-constexpr int64_t kAttnMaxTokens = (int64_t)kAttnUnit * kAttnMaxUnits * kAttnMergeMax;  // 262144
+constexpr int64_t kAttnMaxTokens = (int64_t)kAttnUnit * kAttnMaxUnits * kAttnMergeMax;  // 524288
 
 // 128-token units per split for a sequence of L tokens when `pairs` (sequence, KV head) pairs
 // are active and the device has `target` CUs.
@@ -233,15 +236,16 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
   // round trip before the first K/V DMA.
   const int cap = p.max_pages * p.PAGE;
   const int split_tokens = kAttnUnit * attn_split_units(cap, n_seqs * p.H_KV, p.target_wgs);
-  // The grid is one-dimensional: the first (active programs) x (splits of the active count)
-  // workgroups have work, in blocks of 8 programs whose splits sit 8 workgroups apart
-  // (split_decode), so the workgroups that have work are the first ones dispatched and a
-  // plan-mode grid (sized for the worst active count) carries few idle workgroups.
+  // The grid is one-dimensional: workgroup id = program * splits + split, with the split count
+  // of the active sequences, so the workgroups that have work are the first ones dispatched and
+  // a plan-mode grid (sized for the worst active count) carries few idle workgroups.  (The
+  // GEMMs' interleaved split order does not pay here: it puts each KV head's workgroups on one
+  // XCD, and every XCD then fetches the 128-byte lines that hold the scales of all the heads --
+  // 90.1 instead of 79.2 MB per launch at B = 8, k = 8, context 4096, for no time gained.)
   const int ns_act = (cap + split_tokens - 1) / split_tokens;
-  const int n_prog = n_seqs * p.H_KV * p.n_qc;
-  if ((int)blockIdx.x >= n_prog * ns_act) return;
-  int prog, split;
-  split_decode((int)blockIdx.x, n_prog, ns_act, prog, split);
+  const int prog = (int)blockIdx.x / ns_act;
+  const int split = (int)blockIdx.x - prog * ns_act;
+  if (prog >= n_seqs * p.H_KV * p.n_qc) return;
   const int qc = prog % p.n_qc, kvh = (prog / p.n_qc) % p.H_KV, b = prog / (p.n_qc * p.H_KV);
   if (qc * p.QPP >= q_len) return;
   const int s0 = split * split_tokens;
@@ -271,7 +275,7 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
   // page sub-tile.
   auto chunk_t0 = [&](int it) { return s0 + kAttnChunk * (w + kAttnWaves * it); };
   const int32_t* bt_row = p.bt + (int64_t)b * p.s_bt;
-  // Page of the wave's chunk `lane` within the split and the block table (at most 32 chunks);
+  // Page of the wave's chunk `lane` within the split and the block table (at most 64 chunks);
   // chunks at or past kv_end never use theirs.
   int page_v;
   {

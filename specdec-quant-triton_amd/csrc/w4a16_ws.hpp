@@ -226,7 +226,10 @@ __device__ __forceinline__ void w4a16_ws_body(W4A16Params p, SlotPtr slot_ptr) {
       for (int j = 0; j < MT; ++j) acc[i][j] = acc[i][j] + *reinterpret_cast<const v4f*>(xch + ((i * MT + j) * 64 + lane) * 4);
   }
 
-  __shared__ int s_last_ws4;
+  // The split-K arrival flag lives in stream 0's slot 1, free once the main loop is done (the
+  // hand-over above uses the streams' slot 0), so the workgroup's LDS is exactly its rings:
+  // two 80-row workgroups (4 x 20 KB each) then fit one CU.
+  int* s_last_ws4 = reinterpret_cast<int*>(slot_ptr(std::integral_constant<int, 1>{}, 0));
   if (p.splits == 1) {
     if (h == 0) {
 #pragma unroll
@@ -251,7 +254,7 @@ __device__ __forceinline__ void w4a16_ws_body(W4A16Params p, SlotPtr slot_ptr) {
   }
   tl_mark(p.tl, p.tl_cap, 3);  // diagnostics build: partials issued
   // Every thread of the workgroup takes part in the arrival and the last one's finish.
-  w4_splitk_finish<BM, BN, 512>(p, prs, cidx, m0, ltile * BN, M, &s_last_ws4);
+  w4_splitk_finish<BM, BN, 512>(p, prs, cidx, m0, ltile * BN, M, s_last_ws4);
   tl_mark_drained(p.tl, p.tl_cap, 4);  // diagnostics build: hand-off (and, if last, the sum) done
 }
 

@@ -507,10 +507,13 @@ def traffic(args) -> int:
         # the steady state of a launch whose operands come from HBM.
         fb = statistics.median(fv) * 1024 * f_scale
         wb = statistics.median(wv) * 1024 * w_scale
-        w = wmap.get(name, {})
+        # Counter rows carry the grid (" [N]"); probe maps may key a kernel without it.
+        base, _, grid = name.partition(" [")
+        w = wmap.get(name) or wmap.get(base, {})
         tag = w.get("workload", f"M={args.M}")
-        out[f"{name}@{tag}"] = dict(fetch_bytes=round(fb), write_bytes=round(wb), bytes_per_launch=round(fb + wb),
-                                   launches=len(fv), algorithmic_bytes=w.get("algorithmic_bytes"))
+        out[f"{base}@{tag}"] = dict(fetch_bytes=round(fb), write_bytes=round(wb), bytes_per_launch=round(fb + wb),
+                                   launches=len(fv), algorithmic_bytes=w.get("algorithmic_bytes"),
+                                   grid=int(grid.rstrip("]")) if grid else None)
     meta = dict(copy_mib=args.copy_mib, fetch_scale=round(f_scale, 4), write_scale=round(w_scale, 4),
                 copy_fetch_kib=statistics.median(cf), copy_write_kib=statistics.median(cw))
     res = {"_calibration": meta, **out}
