@@ -6,7 +6,9 @@
 //    following W8A8 and attention launch writes per-workgroup s_memrealtime marks (kernel
 //    start, first operand data landed, main loop done, stores issued, all memory done);
 //  * specq_diag_stream_read: a plain streaming read of a buffer (16-byte loads, XOR-reduced),
-//    the floor a weight-streaming GEMM launch of the same bytes is measured against.
+//    the floor a weight-streaming GEMM launch of the same bytes is measured against;
+//  * specq_diag_xcc_ids: the XCD (hardware register XCC_ID) each workgroup of a launch ran on,
+//    which shows how the dispatcher deals workgroups to the XCDs.
 #include <atomic>
 
 #include "api_common.hpp"
@@ -46,6 +48,12 @@ __global__ __launch_bounds__(512) void diag_stream_read_kernel(const int8_t* buf
   const int x = acc.x ^ acc.y ^ acc.z ^ acc.w;
   if (x == 0x7e57c0de && lane == 63) sink[blockIdx.x] = x;
 }
+
+__global__ void diag_xcc_kernel(int* out) {
+  int x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(x));
+  if (threadIdx.x == 0) out[blockIdx.x] = x;
+}
 #endif
 
 }  // namespace specq
@@ -79,6 +87,20 @@ extern "C" int specq_diag_stream_read(const void* buf, int64_t bytes, int wgs, i
   void* args[] = {&b, const_cast<int64_t*>(&per_wg), &bytes, &sink};
   hipError_t e = hipLaunchKernel(fn, dim3(wgs), dim3(waves * 64), args, 0, reinterpret_cast<hipStream_t>(stream));
   if (e != hipSuccess) return specq::fail(SPECQ_EIO, "diag_stream_read: launch failed");
+  return SPECQ_OK;
+}
+#endif
+
+#ifdef SPECQ_DIAG
+// out[b] = XCD of workgroup b, for a launch of `wgs` workgroups of `threads` threads.
+extern "C" int specq_diag_xcc_ids(int* out, int wgs, int threads, void* stream) {
+  specq::clear_error();
+  SPECQ_REQUIRE(out && wgs >= 1 && wgs <= (1 << 20) && threads >= 64 && threads <= 1024 && threads % 64 == 0,
+                SPECQ_EINVAL, "diag_xcc_ids: 1..2^20 workgroups of 64..1024 threads");
+  void* args[] = {&out};
+  hipError_t e = hipLaunchKernel((const void*)&specq::diag_xcc_kernel, dim3(wgs), dim3(threads), args, 0,
+                                 reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return specq::fail(SPECQ_EIO, "diag_xcc_ids: launch failed");
   return SPECQ_OK;
 }
 #endif

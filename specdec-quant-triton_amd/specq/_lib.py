@@ -103,6 +103,7 @@ DIAG_LIB_PATH = os.path.join(PKG_DIR, "libspecq_diag.so")
 DIAG_SIGNATURES = {
     "specq_diag_set_timeline": (_c_int, [_c_vp, _c_int]),
     "specq_diag_stream_read": (_c_int, [_c_vp, _c_i64, _c_int, _c_int, _c_int, _c_vp, _c_vp]),
+    "specq_diag_xcc_ids": (_c_int, [_c_vp, _c_int, _c_int, _c_vp]),
 }
 
 

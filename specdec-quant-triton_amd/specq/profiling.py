@@ -28,6 +28,8 @@ Subcommands (run from the repository root):
             median per dispatch of each counter, instructions per wave (SQ_INSTS_* / SQ_WAVES),
             and the share of wave cycles spent issuing each instruction class
             (SQ_ACTIVE_INST_* / SQ_WAVE_CYCLES, both counted per wave in the same units).
+  tiles     graph timing of explicit tilings (auto or BMxBNsS) of the w8l / w4l layer launches
+  xcc       the XCD each workgroup of a launch runs on (diagnostics build), for several grids
   timeline  per-workgroup phase times of one launch of each kind (start skew, time to first
             operand data, main loop, stores), from the diagnostics build (libspecq_diag.so),
             whose W8A8 and attention kernels write s_memrealtime marks into a buffer.
@@ -185,10 +187,12 @@ def _make_kind(kind: str, args, K, gen, g, torch):
         sa = torch.rand((M,), device="cuda", generator=g) * 0.015 + 0.005
         outs = [torch.empty((M, Ng), dtype=torch.float16, device="cuda") for Ng, _k in shapes]
 
+        bm, bn, sk = getattr(args, "tile", None) or (None, None, 0)
+
         def run(layers=layers, a=a, sa=sa, outs=outs):
             for mem in layers:
-                K.w8a8_matmul_grouped(a, sa, mem, outs=outs, BLOCK_M=None)
-        _, ck = K.w8a8_matmul_grouped(a, sa, layers[0], outs=outs, BLOCK_M=None)
+                K.w8a8_matmul_grouped(a, sa, mem, outs=outs, BLOCK_M=bm, BLOCK_N=bn, split_k=sk)
+        _, ck = K.w8a8_matmul_grouped(a, sa, layers[0], outs=outs, BLOCK_M=bm, BLOCK_N=bn, split_k=sk)
         bytes_ = sum(Ng * Kl + 4 * Ng + 2 * M * Ng for Ng, _k in shapes) + M * Kl + 4 * M
         ops = sum(2 * M * Ng * Kl for Ng, _k in shapes)
         wl = f"W8A8 {lname} ({'+'.join(f'{Ng}x{Kl}' for Ng, _k in shapes)}) M={M}"
@@ -211,10 +215,12 @@ def _make_kind(kind: str, args, K, gen, g, torch):
         x = torch.randn((M, Kl), device="cuda", generator=g).half()
         outs = [torch.empty((M, Ng), dtype=torch.float16, device="cuda") for Ng, _k in shapes]
 
+        bm, bn, sk = getattr(args, "tile", None) or (None, None, 0)
+
         def run(layers=layers, x=x, outs=outs):
             for mem in layers:
-                K.w4a16_matmul_grouped(x, mem, outs=outs)
-        _, ck = K.w4a16_matmul_grouped(x, layers[0], outs=outs)
+                K.w4a16_matmul_grouped(x, mem, outs=outs, BLOCK_M=bm, BLOCK_N=bn, split_k=sk)
+        _, ck = K.w4a16_matmul_grouped(x, layers[0], outs=outs, BLOCK_M=bm, BLOCK_N=bn, split_k=sk)
         bytes_ = sum(Ng * Kl // 2 + 2 * Ng * (Kl // 128) + 2 * M * Ng for Ng, _k in shapes) + 2 * M * Kl
         ops = sum(2 * M * Ng * Kl for Ng, _k in shapes)
         wl = f"W4A16 {lname} ({'+'.join(f'{Ng}x{Kl}' for Ng, _k in shapes)}) M={M}"
@@ -314,6 +320,79 @@ def _pcts(x):
     import numpy as np
 
     return [float(np.percentile(x, q)) for q in (10, 50, 90)] + [float(np.max(x))]
+
+
+def tiles(args) -> int:
+    """Graph timing of explicit tilings of config-1/2 layer launches (kinds w8l:L:M, w4l:L:M):
+    each --tiles entry is "auto" or BMxBNsS (BLOCK_M x BLOCK_N, split_k S), every entry timed
+    twice (the faster kept) over the kind's distinct weight copies."""
+    import torch
+
+    if PKG not in sys.path:
+        sys.path.insert(0, PKG)
+    import kernels as K
+    from specq import gen
+
+    torch.cuda.set_device(0)
+    _apply_options(args)
+    g = torch.Generator(device="cuda").manual_seed(1)
+    out = ["| launch | tile (BLOCK_M x BLOCK_N, split) | kernel [grid] | µs per launch |", "|---|---|---|---|"]
+    for kind in args.kinds.split(","):
+        for t in args.tiles.split(","):
+            if t == "auto":
+                args.tile = None
+            else:
+                bmbn, sk = t.split("s")
+                bm, bn = bmbn.split("x")
+                args.tile = (int(bm), int(bn), int(sk))
+            kd = _make_kind(kind, args, K, gen, g, torch)
+            us = min(_graph_us(kd["run"], kd["launches"]) for _ in range(2))
+            ck = kd["ck"]
+            cfg = ck.config
+            tile = f"{cfg.get('block_m')} x {cfg.get('block_n')}, {cfg.get('split_k')}" + (" (auto)" if t == "auto" else "")
+            out.append(f"| {kd['workload']} | {tile} | `{_key(ck.name, cfg.get('grid'))}` | {us:.2f} |")
+            print(out[-1], flush=True)
+            del kd
+            torch.cuda.empty_cache()
+    text = "\n".join(out)
+    if args.out:
+        with open(args.out, "w") as fh:
+            fh.write(text + "\n")
+    return 0
+
+
+def xcc(args) -> int:
+    """Which XCD each workgroup of a launch runs on (diagnostics build, hardware register
+    XCC_ID), against the round-robin deal blockIdx.x mod (number of XCDs), for several grids."""
+    import torch
+
+    if PKG not in sys.path:
+        sys.path.insert(0, PKG)
+    from specq import _lib
+    _lib.use_diag()
+    torch.cuda.set_device(0)
+    grids = [int(x) for x in args.grids.split(",")]
+    buf = torch.zeros(max(grids), dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    out = ["| workgroups x threads | launches | XCDs seen | workgroups per XCD | workgroups not on XCD blockIdx mod XCDs |",
+           "|---|---|---|---|---|"]
+    for n in grids:
+        for threads in (256, 512):
+            counts, bad, nx = torch.zeros(16, dtype=torch.int64), 0, 0
+            for _ in range(args.reps):
+                buf.fill_(-1)
+                _lib.call("specq_diag_xcc_ids", buf.data_ptr(), n, threads, stream)
+                ids = buf[:n].cpu().to(torch.int64)
+                nx = max(nx, int(ids.max()) + 1)
+                counts += torch.bincount(ids, minlength=16)[:16]
+                bad += int((ids != torch.arange(n) % nx).sum())
+            out.append(f"| {n} x {threads} | {args.reps} | {nx} | {' / '.join(str(int(v)) for v in counts[:nx])} | {bad} |")
+            print(out[-1], flush=True)
+    text = "\n".join(out)
+    if args.out:
+        with open(args.out, "w") as fh:
+            fh.write(text + "\n")
+    return 0
 
 
 def timeline(args) -> int:
@@ -947,6 +1026,17 @@ def main() -> int:
     t.add_argument("--map")
     t.add_argument("--merge", help="existing traffic json whose entries are kept")
     t.add_argument("--out")
+    xp = sub.add_parser("xcc")
+    xp.add_argument("--grids", default="8,64,192,224,256,384,448,1000,4096,8192")
+    xp.add_argument("--reps", type=int, default=5)
+    xp.add_argument("--out")
+    tl = sub.add_parser("tiles")
+    tl.add_argument("--set", action="append", default=[], help="library option name=value (repeatable)")
+    tl.add_argument("--kinds", required=True)
+    tl.add_argument("--tiles", required=True, help="comma list of auto or BMxBNsS")
+    tl.add_argument("--layers", type=int, default=8)
+    tl.add_argument("--copy-mib", type=int, default=1024)
+    tl.add_argument("--out")
     tp = sub.add_parser("timeline")
     tp.add_argument("--set", action="append", default=[], help="library option name=value (repeatable)")
     tp.add_argument("--kinds", required=True)
@@ -979,7 +1069,7 @@ def main() -> int:
     c.add_argument("--kind", choices=("w8a8", "w4a16"), default="w8a8")
     args = ap.parse_args()
     return {"probe": probe, "stats": stats, "traffic": traffic, "mfma": mfma, "staircase": staircase,
-            "staircase-md": staircase_md, "sq": sq, "launches": launches, "timeline": timeline,
+            "staircase-md": staircase_md, "sq": sq, "launches": launches, "timeline": timeline, "tiles": tiles, "xcc": xcc,
             "floors": floors, "tune": tune, "tune-emit": tune_emit, "tune-md": tune_md}[args.cmd](args)
 
 
