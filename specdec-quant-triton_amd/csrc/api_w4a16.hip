@@ -2,8 +2,8 @@
 // launch, and the load-time weight packing.
 //
 // Kernel families (identical fp32 summation order, so every choice is bit-identical):
-//   WS  LDS-staged activations (w4a16_ws.hpp) for token tiles up to 144 rows (default; a
-//       deeper BLOCK_M runs as equal chunks of at most 144 rows).
+//   WS  LDS-staged activations (w4a16_ws.hpp) for token tiles up to 160 rows (default; a
+//       deeper BLOCK_M runs as equal chunks of at most 160 rows).
 //   RK  register-stream kernel (w4a16_rk.hpp) for 16- and 32-row token tiles (w4a16_path 1).
 #include <algorithm>
 #include <atomic>
@@ -114,8 +114,8 @@ void w4_auto_tiles(int M, int N, int K, int splits, int rw_fixed, int* mt_out, i
   const int rows16 = ceil_div(std::max(M, 1), 16);
   double best_t = 0;
   int best_mt = -1, best_rw = 1, last_mt = -1;
-  // No measured best tile was deeper than 144 rows (9 x 16), where the model is least accurate.
-  constexpr int kMaxAutoMt = 9;
+  // At most the deepest compiled tile (160 rows), so M up to 320 runs as at most two chunks.
+  constexpr int kMaxAutoMt = kW4MaxMt;
   const int max_c = std::max(6, ceil_div(rows16, kMaxAutoMt));
   for (int c = 1; c <= max_c; ++c) {
     const int mt = ceil_div(rows16, c);

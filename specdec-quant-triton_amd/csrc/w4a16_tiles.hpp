@@ -1,6 +1,6 @@
 // Tile table of the W4A16 kernels, shared by the instantiation units and the C-ABI dispatcher.
 //   rk (w4a16_rk.hpp): token tiles of 1-2 x 16 rows, activations loaded into registers.
-//   ws (w4a16_ws.hpp): token tiles of 1-9 x 16 rows, 8 waves in two K streams, each stream's
+//   ws (w4a16_ws.hpp): token tiles of 1-10 x 16 rows, 8 waves in two K streams, each stream's
 //      activations staged in an LDS ring of NSLOT chunks of S 128-wide K blocks (4 KB per
 //      block per 16 token rows), weights in a register ring NSW blocks deep (W4WsPick).
 // RW = 1 or 2 16-channel fragments per wave, i.e. BLOCK_N = 64 or 128 per workgroup.
@@ -10,7 +10,7 @@
 
 namespace specq {
 
-constexpr int kW4MaxMt = 9;     // deepest token tile (144 rows: two streams x two LDS slots)
+constexpr int kW4MaxMt = 10;    // deepest token tile (160 rows: two streams x two 40 KB LDS slots = 160 KB)
 constexpr int kW4RkMaxMt = 2;
 
 // LDS ring and weight-ring depth per tile (measured on the Llama-3-8B linears, 8-wave

@@ -46,7 +46,7 @@ struct W4WsCfg {
   // Two streams, each with its NSLOT slots; stream 1's tiles are handed over in the two
   // streams' first slots.
   static constexpr bool OK = S >= 1 && NSLOT >= 2 && NSLOT <= 4 && NS % (S * NSLOT) == 0 && NS <= 16 &&
-                             wait_w(0) <= 63 && P * S * WPER + P * A_L <= 63 && 2 * NSLOT * SLOT <= 160 * 1024 - 256 &&
+                             wait_w(0) <= 63 && P * S * WPER + P * A_L <= 63 && 2 * NSLOT * SLOT <= 160 * 1024 &&
                              4 * RW * MT * 1024 <= 2 * SLOT;
 };
 

@@ -1,5 +1,5 @@
 // Instantiations of the LDS-staged-activation W4A16 kernel for the packed fragment layout:
-// token tiles of 1 .. 9 x 16 rows, BLOCK_N = 64 (RW 1) and 128 (RW 2).
+// token tiles of 1 .. 10 x 16 rows, BLOCK_N = 64 (RW 1) and 128 (RW 2).
 #include "w4a16_tiles.hpp"
 
 namespace specq {
@@ -24,6 +24,8 @@ const void* w4a16_ws_fn_l2(int mt, int rw) {
     case 34: return w4a16_ws_pick<8, 2, 2>();
     case 37: return w4a16_ws_pick<9, 1, 2>();
     case 38: return w4a16_ws_pick<9, 2, 2>();
+    case 41: return w4a16_ws_pick<10, 1, 2>();
+    case 42: return w4a16_ws_pick<10, 2, 2>();
     default: return nullptr;
   }
 }

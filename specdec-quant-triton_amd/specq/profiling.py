@@ -902,6 +902,8 @@ def tune(args) -> int:
                 Ms = sorted({lo, M})
                 auto = K.KernelInfo(kid, 2 if w4 else 1, M, N_total, Kd, 0, 0, 4, gsk).config
                 reqs = [(None, None)] + [(bm, None) for bm in (16, 32, 64, 128)] + [(auto["block_m"], bn) for bn in bns]
+                if w4 and M > 144:
+                    reqs.append((160, None))  # the deepest W4A16 tile: M up to 320 in two chunks
                 cands = []
                 for bm, bn in reqs:
                     c = K.KernelInfo(kid, 2 if w4 else 1, M, N_total, Kd, bm or 0, bn or 0, 4, gsk).config
@@ -934,6 +936,7 @@ def tune(args) -> int:
                 best = min(cands, key=lambda c: (regret[c], times[c]))
                 if regret[best] > regret[at] - 0.02:
                     best = at
+                print(f"[tune] {kind} {sname} step {r}: {list(best)}", flush=True)
                 table[r] = dict(best=list(best), us=round(times[best], 3), auto=list(at), auto_us=round(times[at], 3),
                                 regret=round(regret[best], 4), auto_regret=round(regret[at], 4),
                                 candidates={f"{b}x{n}s{k}": {str(m): round(t, 3) for m, t in per_m[(b, n, k)].items()}

@@ -12,6 +12,7 @@ written (bench_graphs.py:144-159).  Eager work and host synchronisation run betw
 """
 import random
 
+import numpy as np
 import pytest
 import torch
 
@@ -141,3 +142,48 @@ def test_config4_bucketed_plan_graphs_every_shape_bit_exact():
     gset = PlanGraphSet(stack.step, B_MAX, [k + 1 for k in KS])
     assert len(gset.graphs) == len(gset.buckets) * len(KS)
     replay_and_check(stack, gset.replay, "bucketed")
+
+
+@pytest.mark.parametrize("B,k", [(3, 2), (8, 8)])
+def test_config4_eager_layer_against_oracle(B, k):
+    """One layer of the config-4 stack, eager at (B, k), against the CPU oracle: the qkv (N =
+    6144), o, gate and up GEMMs bit-exact (oracle.w8a8), the fused SiLU*mul quantisation
+    bit-exact against the oracle's row quantisation of the device's SiLU*mul (which
+    test_gpu_elementwise.py pins to one fp16 ulp of the float64 form), down bit-exact on those
+    INT8 activations, and attention at context 1024 within the attention tests' bound."""
+    from oracle import oracle as O
+    ql = k + 1
+    M = B * ql
+    lw = {}
+    for j, (name, N, Kd) in enumerate((("qkv", QKV, HID), ("o", HID, HID), ("gate", FF, HID), ("up", FF, HID),
+                                       ("down", HID, FF))):
+        w, sw = gen.w8a8_weights(N, Kd, seed=800 + j)
+        lw[name] = (w, sw)
+    a, sa = gen.w8a8_acts(M, HID, seed=810)
+    kv = gen.paged_kv(B, [CTX + ql] * B, H_KV, D, seed=811)
+    q = gen.queries(B, ql, H, D, seed=812)
+    note(f"config4 eager layer vs oracle B={B} k={k}")
+    dev = {n: (K.pack_weight_int8(w.to(DEV)), sw.to(DEV)) for n, (w, sw) in lw.items()}
+    ad, sad = a.to(DEV), sa.to(DEV)
+    qkv, _ = K.w8a8_matmul(ad, sad, *dev["qkv"], BLOCK_M=None)
+    o, _ = K.w8a8_matmul(ad, sad, *dev["o"], BLOCK_M=None)
+    (gate, up), _ = K.w8a8_matmul_grouped(ad, sad, [dev["gate"], dev["up"]], BLOCK_M=None)
+    hq, hs = K.silu_mul_quant_int8(gate, up)
+    h = K.silu_mul(gate, up)
+    down, _ = K.w8a8_matmul(hq, hs, *dev["down"], BLOCK_M=None)
+    kvd = [t.to(DEV) for t in kv]
+    att, _ = K.paged_attention(q.to(DEV), *kvd, ql, QPP=ql)
+    torch.cuda.synchronize()
+    an, san = a.numpy(), sa.numpy()
+    for name, got in (("qkv", qkv), ("o", o), ("gate", gate), ("up", up)):
+        w, sw = lw[name]
+        ref = O.w8a8(an, san, w.numpy(), sw.numpy())
+        assert np.array_equal(got.cpu().numpy().view(np.uint16), ref.view(np.uint16)), f"{name} differs from the oracle"
+    rq, rs = O.quantize_rows_int8(h.cpu().numpy())
+    assert np.array_equal(hq.cpu().numpy(), rq) and np.array_equal(hs.cpu().numpy(), rs), "SiLU*mul quantisation"
+    w, sw = lw["down"]
+    ref = O.w8a8(hq.cpu().numpy(), hs.cpu().numpy(), w.numpy(), sw.numpy())
+    assert np.array_equal(down.cpu().numpy().view(np.uint16), ref.view(np.uint16)), "down differs from the oracle"
+    ref = O.paged_attention(q.numpy(), *[t.numpy() for t in kv], ql)
+    err = np.abs(att.float().cpu().numpy().astype(np.float64) - ref)
+    assert (err <= 4e-3 + 2.0 ** -9 * np.abs(ref)).all(), f"attention: max err {err.max():.3e}"

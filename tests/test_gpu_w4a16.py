@@ -152,7 +152,7 @@ def test_w4a16_layouts_families_tiles_bit_identical(shape):
             for path in (0, 1, 2):
                 _lib.set_option("w4a16_path", path)
                 for wname, (order, wp) in weights.items():
-                    for bm in (None, 16, 32, 80, 256):
+                    for bm in (None, 16, 32, 80, 160, 256):
                         for bn in (None, 128):
                             out, ck = K.w4a16_matmul(a[:M], wp, sc, BLOCK_M=bm, BLOCK_N=bn)
                             torch.cuda.synchronize()
