@@ -257,6 +257,9 @@ int specq_w4a16_pack_weight(const void* wq, int64_t ldq, int wq_layout, int N, i
  *   kc, vc   int8 [pages, PAGE, H_KV, D]    strides s_kp, s_ko, s_kh (shared by kc and vc)
  *   ks, vs   fp16 or fp32 (scale_fp32 = 0/1) [pages, PAGE, H_KV], strides s_sp, s_so, s_sh
  *   block_tbl int32 [B_grid, max_pages], row stride s_bt
+ *   n_pages  pages in the K/V pool: a block-table id outside [0, n_pages) masks its page's
+ *            tokens (no load; a row with no visible token left outputs 0).  No reference
+ *            counterpart: the reference loads through any id it is given
  *   ctx_len  int32 [B_grid]; includes the q_len query tokens, which are the last q_len
  *            positions of each sequence (kernels.py:173, 204)
  *   out      fp16 like q, strides s_ob, s_ot, s_oh
@@ -281,7 +284,7 @@ int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64_t s_qh,
                      const int8_t* kc, const int8_t* vc, int64_t s_kp, int64_t s_ko, int64_t s_kh,
                      const void* ks, const void* vs, int64_t s_sp, int64_t s_so, int64_t s_sh,
                      int scale_fp32, const int32_t* block_tbl, int64_t s_bt, int max_pages,
-                     const int32_t* ctx_len, void* out, int64_t s_ob, int64_t s_ot, int64_t s_oh,
+                     int n_pages, const int32_t* ctx_len, void* out, int64_t s_ob, int64_t s_ot, int64_t s_oh,
                      int B_grid, int n_seqs, int q_len, int ql_grid, int H, int H_KV, int D,
                      int PAGE, int QPP, float sm_scale, const int32_t* plan,
                      void* workspace, size_t workspace_bytes, void* stream);

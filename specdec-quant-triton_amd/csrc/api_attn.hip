@@ -92,7 +92,8 @@ extern "C" size_t specq_paged_attn_workspace_size(int B_grid, int H, int H_KV, i
 extern "C" int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64_t s_qh, const int8_t* kc,
                                 const int8_t* vc, int64_t s_kp, int64_t s_ko, int64_t s_kh, const void* ks,
                                 const void* vs, int64_t s_sp, int64_t s_so, int64_t s_sh, int scale_fp32,
-                                const int32_t* block_tbl, int64_t s_bt, int max_pages, const int32_t* ctx_len,
+                                const int32_t* block_tbl, int64_t s_bt, int max_pages, int n_pages,
+                                const int32_t* ctx_len,
                                 void* out, int64_t s_ob, int64_t s_ot, int64_t s_oh, int B_grid, int n_seqs,
                                 int q_len, int ql_grid, int H, int H_KV, int D, int PAGE, int QPP, float sm_scale,
                                 const int32_t* plan, void* workspace, size_t workspace_bytes, void* stream) {
@@ -104,6 +105,7 @@ extern "C" int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64
   SPECQ_REQUIRE(D == 64 || D == 128, SPECQ_ENOTSUP, "paged_attn: head_dim %d (64 or 128 supported)", D);
   SPECQ_REQUIRE(PAGE > 0 && PAGE % 16 == 0, SPECQ_ENOTSUP, "paged_attn: PAGE=%d must be a multiple of 16", PAGE);
   SPECQ_REQUIRE(max_pages > 0, SPECQ_EINVAL, "paged_attn: empty block table");
+  SPECQ_REQUIRE(n_pages > 0, SPECQ_EINVAL, "paged_attn: empty K/V pool (n_pages=%d)", n_pages);
   SPECQ_REQUIRE((int64_t)max_pages * PAGE <= kAttnMaxTokens, SPECQ_ENOTSUP,
                 "paged_attn: block table of %lld tokens exceeds %lld", (long long)max_pages * PAGE,
                 (long long)kAttnMaxTokens);
@@ -160,7 +162,7 @@ extern "C" int specq_paged_attn(const void* q, int64_t s_qb, int64_t s_qt, int64
   p.q = (const _Float16*)q; p.s_qb = s_qb; p.s_qt = s_qt; p.s_qh = s_qh;
   p.kc = kc; p.vc = vc; p.s_kp = s_kp; p.s_ko = s_ko; p.s_kh = s_kh;
   p.ks = ks; p.vs = vs; p.s_sp = s_sp; p.s_so = s_so; p.s_sh = s_sh;
-  p.bt = block_tbl; p.s_bt = s_bt; p.max_pages = max_pages; p.ctx_len = ctx_len;
+  p.bt = block_tbl; p.s_bt = s_bt; p.max_pages = max_pages; p.n_pages = n_pages; p.ctx_len = ctx_len;
   p.out = (_Float16*)out; p.s_ob = s_ob; p.s_ot = s_ot; p.s_oh = s_oh;
   p.plan = plan; p.B_grid = B_grid; p.n_seqs = plan ? B_grid : n_seqs; p.q_len = plan ? ql_grid : q_len;
   p.ql_grid = ql_grid; p.G = G; p.QPP = QPP; p.n_qc = n_qc; p.H_KV = H_KV; p.PAGE = PAGE; p.n_splits = ns;

@@ -6,6 +6,8 @@
 //   p_t = softmax_t(s)                  (online, rows with no visible key give 0)
 //   o   = sum_t fp16(p_t * vs_t) * v_t  (the V scale is folded into P before the PV product)
 // K/V are int8 [pages, PAGE, H_KV, D] reached through a block table; scales are fp16 or fp32.
+// Tokens on a page whose block-table id lies outside [0, pages) are masked (read nothing,
+// contribute nothing); the reference reads whatever address such an id names.
 //
 // MI355X schedule:
 //  * One workgroup = (KV split, KV head, query chunk of QPP tokens, sequence).  The QPP * G
@@ -60,6 +62,7 @@ struct AttnParams {
   const int8_t* kc; const int8_t* vc; int64_t s_kp, s_ko, s_kh;
   const void* ks; const void* vs; int64_t s_sp, s_so, s_sh;
   const int32_t* bt; int64_t s_bt; int max_pages;
+  int n_pages;         // pages in the K/V pool: block-table ids outside [0, n_pages) are masked
   const int32_t* ctx_len;
   _Float16* out; int64_t s_ob, s_ot, s_oh;
   const int32_t* plan;
@@ -343,21 +346,25 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
   // Per-chunk bases, lane c holding the wave's chunk c: the byte offset of the chunk's page
   // sub-tile of this KV head in the K/V cache, and that of its first token's scales.  Chunks
   // at or past the wave's last use page 0 (their DMAs read nothing or a fixed valid address).
+  // Chunks whose page id lies outside the pool read nothing and are masked like tokens past
+  // kv_end (bit c of bad_chunks: the wave's chunk c).
+  const bool page_ok = (uint32_t)page_v < (uint32_t)p.n_pages;
+  const uint64_t bad_chunks = __builtin_amdgcn_ballot_w64(lane < n_it && !page_ok);
   int64_t kv_base_v, sc_base_v;
   {
-    const int pg = lane < n_it ? page_v : 0;
+    const int pg = lane < n_it && page_ok ? page_v : 0;
     const int tk = chunk_t0(lane) % p.PAGE;
     kv_base_v = (int64_t)pg * p.s_kp + (int64_t)tk * p.s_ko + (int64_t)kvh * p.s_kh;
     sc_base_v = ((int64_t)pg * p.s_sp + (int64_t)tk * p.s_so + (int64_t)kvh * p.s_sh) * (int64_t)sizeof(ST);
   }
   // Issue the DMAs of chunk `it` into ring slot SL.  K/V granules of chunks past the wave's
-  // last, and of tokens at or past kv_end, are out of range (zeros); their scales read a fixed
-  // valid address.
+  // last or on a page outside the pool, and of tokens at or past kv_end, are out of range
+  // (zeros); their scales read a fixed valid address.
   auto issue = [&](auto slc, int it) __attribute__((always_inline)) {
     uint8_t* dst = ring_of(slc, w);
-    const bool real = it < n_it;
-    const int t0 = chunk_t0(it);
     const int li = min(it, 63);
+    const bool real = it < n_it && ((bad_chunks >> li) & 1) == 0;
+    const int t0 = chunk_t0(it);
     const int64_t kb = readlane64(kv_base_v, li);
     const int64_t sb = readlane64(sc_base_v, li);
     const v4i rk = attn_rsrc(p.kc + kb), rv = attn_rsrc(p.vc + kb);
@@ -467,15 +474,18 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
   };
   auto stage_b = [&](int it, const Staged& st) __attribute__((always_inline)) {
     const int t0 = chunk_t0(it);
-    // Zero V scale for tokens at or past kv_end (their scale slots hold the dummy address's).
+    // A chunk on a page outside the pool: every token masked (wave-uniform).
+    const bool bad = ((bad_chunks >> (it & 63)) & 1) != 0;
+    // Zero V scale for tokens at or past kv_end and of masked chunks (their scale slots hold
+    // the dummy address's).
     float vsc[4] = {st.vsc[0], st.vsc[1], st.vsc[2], st.vsc[3]};
-    if (t0 + kAttnChunk > kv_end) {
+    if (bad || t0 + kAttnChunk > kv_end) {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (t0 + attn_perm(4 * g + e) >= kv_end) vsc[e] = 0.f;
+        if (bad || t0 + attn_perm(4 * g + e) >= kv_end) vsc[e] = 0.f;
     }
     // Every row of the program sees every token of the chunk: no causal mask needed.
-    const bool full = t0 + kAttnChunk - 1 <= L - q_len + qc * p.QPP;
+    const bool full = !bad && t0 + kAttnChunk - 1 <= L - q_len + qc * p.QPP;
     // Unnormalised probabilities against the row's running max m: p = exp2(s_raw * ksc - m)
     // (one fma; masked tokens 0).  While m = -inf every visible p is +inf.  The row max of p is
     // taken on the bit patterns (p >= 0, so their integer order is the numeric order).
@@ -488,7 +498,7 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
       if (!full) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (t0 + attn_perm(4 * g + e) > qpos[rb]) pr[rb][e] = 0.f;
+          if (bad || t0 + attn_perm(4 * g + e) > qpos[rb]) pr[rb][e] = 0.f;
       }
       const uint32_t b0 = __builtin_bit_cast(uint32_t, pr[rb][0]), b1 = __builtin_bit_cast(uint32_t, pr[rb][1]);
       const uint32_t b2 = __builtin_bit_cast(uint32_t, pr[rb][2]), b3 = __builtin_bit_cast(uint32_t, pr[rb][3]);
@@ -513,7 +523,7 @@ __device__ __forceinline__ void paged_attn_body(const AttnParams& p, uint8_t (&r
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           s[e] = st.cs[rb][e] * st.ksc[e];
-          if (!full && t0 + attn_perm(4 * g + e) > qpos[rb]) s[e] = -INFINITY;
+          if (!full && (bad || t0 + attn_perm(4 * g + e) > qpos[rb])) s[e] = -INFINITY;
         }
         const float rmax = group_max4(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
         if (rowp > __builtin_bit_cast(uint32_t, kAttnLazyP)) {

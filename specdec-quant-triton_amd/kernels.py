@@ -705,7 +705,8 @@ def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len, QPP=None, BLOC
 
     q fp16 [B, QLMAX, H, D]; kc/vc int8 [pages, PAGE, H_KV, D]; ks/vs fp16 or fp32
     [pages, PAGE, H_KV]; block_tbl int32 [B, max_pages]; ctx_len int32 [B] (includes the
-    q_len query tokens).  QPP query tokens per program (default q_len = fused).  With
+    q_len query tokens; block-table ids outside [0, pages) mask their page's tokens).  QPP
+    query tokens per program (default q_len = fused).  With
     `plan`, (n_seqs, q_len) = plan[0:2] on the device and the grid covers (B, QLMAX).
     Returns (out, ck).
     """
@@ -754,7 +755,7 @@ def paged_attention(q, kc, vc, ks, vs, block_tbl, ctx_len, q_len, QPP=None, BLOC
               kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2),
               ks.data_ptr(), vs.data_ptr(), ks.stride(0), ks.stride(1), ks.stride(2),
               1 if ks.dtype == torch.float32 else 0,
-              block_tbl.data_ptr(), block_tbl.stride(0), max_pages, ctx_len.data_ptr(),
+              block_tbl.data_ptr(), block_tbl.stride(0), max_pages, min(kc.shape[0], 2**31 - 1), ctx_len.data_ptr(),
               out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
               B_grid, int(n_seqs), int(q_len), QLMAX, H, H_KV, D, PAGE, int(QPP),
               1.0 / math.sqrt(D), _plan_ptr(plan), wptr, wbytes, _stream_ptr(q))

@@ -76,7 +76,7 @@ SIGNATURES = {
     "specq_paged_attn": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64,
                                   _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
                                   _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
-                                  _c_vp, _c_i64, _c_int, _c_vp,
+                                  _c_vp, _c_i64, _c_int, _c_int, _c_vp,
                                   _c_vp, _c_i64, _c_i64, _c_i64,
                                   _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                   _c_int, _c_int, _c_float, _c_vp, _c_vp, _c_size, _c_vp]),

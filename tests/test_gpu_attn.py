@@ -204,3 +204,52 @@ def test_attention_split_target_option(target):
     check(o1, ref, ql, f"target {target}")
     assert torch.equal(o1, o2), "QPP=1 and fused results differ"
     assert torch.equal(o1, o3), "plan mode differs from eager"
+
+
+def test_attention_out_of_pool_page_ids():
+    """Block-table ids outside [0, pages) mask their page's tokens (n_pages bound, no load):
+    sequence 0 has three scattered bad prefix pages (ids = pages, -1, 2^31 - 1), sequence 1 a
+    run of 90 bad pages that empties whole splits, sequence 2 only bad pages.  Expected:
+    the oracle on the block table with the bad pages removed (context shortened by as many
+    pages; the query tokens' pages stay valid, so causal positions keep their order), and
+    zeros for sequence 2.  QPP=1 equals fused, and plan mode equals eager."""
+    from specq.plan import Plan
+    B, k, PAGE = 3, 4, 16
+    ql = k + 1
+    ctx = [1500, 3000, 200]
+    kc, vc, ks, vs, bt, cl = gen.paged_kv(B, ctx, H_KV, D, PAGE=PAGE, seed=87)
+    q = gen.queries(B, ql, H, D, seed=88)
+    n_pages = kc.shape[0]
+    bad = {0: {2: n_pages, 5: -1, 6: 2**31 - 1}, 1: {j: n_pages + j for j in range(10, 100)}}
+    bt_bad = bt.clone()
+    bt_ok = torch.zeros_like(bt)
+    cl_ok = cl.clone()
+    for b in range(B):
+        used = (ctx[b] + PAGE - 1) // PAGE
+        if b == 2:
+            bt_bad[b, :used] = n_pages + 1000
+            continue
+        keep = [int(bt[b, j]) for j in range(used) if j not in bad[b]]
+        for j, v in bad[b].items():
+            assert (j + 1) * PAGE <= ctx[b] - ql, "bad pages must be whole prefix pages"
+            bt_bad[b, j] = v
+        bt_ok[b, :len(keep)] = torch.tensor(keep, dtype=torch.int32)
+        cl_ok[b] = ctx[b] - PAGE * len(bad[b])
+    ref = O.paged_attention(*cpu(q, kc, vc, ks, vs, bt_ok, cl_ok), ql)
+    ref[2] = 0.0
+    kc, vc, ks, vs, bt_bad, cl, q = (t.to(DEV) for t in (kc, vc, ks, vs, bt_bad, cl, q))
+    note(f"attn out-of-pool page ids ctx={ctx} n_pages={n_pages}")
+    outs = {}
+    for QPP in (1, ql):
+        out, _ = K.paged_attention(q, kc, vc, ks, vs, bt_bad, cl, ql, QPP=QPP)
+        torch.cuda.synchronize()
+        check(out, ref, ql, f"out-of-pool ids QPP={QPP}")
+        outs[QPP] = out
+    assert torch.equal(outs[1], outs[ql]), "QPP=1 and fused results differ"
+    assert bool((outs[ql][2] == 0).all()), "a sequence with only out-of-pool pages must give zeros"
+    plan = Plan(DEV)
+    plan.set(B, ql)
+    o3 = torch.full_like(q, 7.0)
+    K.paged_attention(q, kc, vc, ks, vs, bt_bad, cl, ql, QPP=ql, plan=plan.attn, out=o3)
+    torch.cuda.synchronize()
+    assert torch.equal(o3, outs[ql]), "plan mode differs from eager"

@@ -115,15 +115,18 @@ def test_attn_validation_errors(built_lib):
     from specq import _lib
     f = _lib.lib().specq_paged_attn
     args = [16, 128 * 32 * 9, 128 * 32, 128, 16, 16, 16 * 8 * 128, 8 * 128, 128, 16, 16, 128, 8, 1, 1,
-            16, 64, 64, 16, 16, 128 * 32 * 9, 128 * 32, 128, 2, 2, 9, 9, 32, 8, 128, 16, 9, 0.088, 0, 0, 0, 0]
-    bad_d = list(args); bad_d[29] = 96
+            16, 64, 64, 128, 16, 16, 128 * 32 * 9, 128 * 32, 128, 2, 2, 9, 9, 32, 8, 128, 16, 9, 0.088,
+            0, 0, 0, 0]
+    bad_d = list(args); bad_d[30] = 96
     assert f(*bad_d) == -95
-    bad_page = list(args); bad_page[30] = 8
+    bad_page = list(args); bad_page[31] = 8
     assert f(*bad_page) == -95
-    too_many_rows = list(args); too_many_rows[31] = 17   # 17 * 4 rows > 64
+    too_many_rows = list(args); too_many_rows[32] = 17   # 17 * 4 rows > 64
     assert f(*too_many_rows) == -95
-    bad_heads = list(args); bad_heads[28] = 5
+    bad_heads = list(args); bad_heads[29] = 5
     assert f(*bad_heads) == -22
+    no_pool = list(args); no_pool[18] = 0
+    assert f(*no_pool) == -22
     null_q = list(args); null_q[0] = 0
     assert f(*null_q) == -22
 
