@@ -206,21 +206,23 @@ def test_attention_split_target_option(target):
     assert torch.equal(o1, o3), "plan mode differs from eager"
 
 
-def test_attention_out_of_pool_page_ids():
+@pytest.mark.parametrize("D_, PAGE, sdt", [(128, 16, torch.float32), (64, 32, torch.float16)])
+def test_attention_out_of_pool_page_ids(D_, PAGE, sdt):
     """Block-table ids outside [0, pages) mask their page's tokens (n_pages bound, no load):
     sequence 0 has three scattered bad prefix pages (ids = pages, -1, 2^31 - 1), sequence 1 a
-    run of 90 bad pages that empties whole splits, sequence 2 only bad pages.  Expected:
+    run of bad pages over 1440 tokens that empties whole splits, sequence 2 only bad pages.  Expected:
     the oracle on the block table with the bad pages removed (context shortened by as many
     pages; the query tokens' pages stay valid, so causal positions keep their order), and
     zeros for sequence 2.  QPP=1 equals fused, and plan mode equals eager."""
     from specq.plan import Plan
-    B, k, PAGE = 3, 4, 16
+    B, k = 3, 4
     ql = k + 1
     ctx = [1500, 3000, 200]
-    kc, vc, ks, vs, bt, cl = gen.paged_kv(B, ctx, H_KV, D, PAGE=PAGE, seed=87)
-    q = gen.queries(B, ql, H, D, seed=88)
+    kc, vc, ks, vs, bt, cl = gen.paged_kv(B, ctx, H_KV, D_, PAGE=PAGE, seed=87, scale_dtype=sdt)
+    q = gen.queries(B, ql, H, D_, seed=88)
     n_pages = kc.shape[0]
-    bad = {0: {2: n_pages, 5: -1, 6: 2**31 - 1}, 1: {j: n_pages + j for j in range(10, 100)}}
+    run = 90 * 16 // PAGE  # 1440 tokens of bad pages in sequence 1
+    bad = {0: {2: n_pages, 5: -1, 6: 2**31 - 1}, 1: {j: n_pages + j for j in range(10, 10 + run)}}
     bt_bad = bt.clone()
     bt_ok = torch.zeros_like(bt)
     cl_ok = cl.clone()
@@ -238,7 +240,7 @@ def test_attention_out_of_pool_page_ids():
     ref = O.paged_attention(*cpu(q, kc, vc, ks, vs, bt_ok, cl_ok), ql)
     ref[2] = 0.0
     kc, vc, ks, vs, bt_bad, cl, q = (t.to(DEV) for t in (kc, vc, ks, vs, bt_bad, cl, q))
-    note(f"attn out-of-pool page ids ctx={ctx} n_pages={n_pages}")
+    note(f"attn out-of-pool page ids D={D_} PAGE={PAGE} ctx={ctx} n_pages={n_pages}")
     outs = {}
     for QPP in (1, ql):
         out, _ = K.paged_attention(q, kc, vc, ks, vs, bt_bad, cl, ql, QPP=QPP)
