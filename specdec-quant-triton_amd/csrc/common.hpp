@@ -265,6 +265,25 @@ __device__ __forceinline__ bool chunked_unit(int m_chunks, int units, int& mc, i
   return mc < m_chunks;
 }
 __host__ __device__ inline int chunked_grid(int units, int m_chunks) { return units * m_chunks; }
+// The same grid with the M-chunks of a unit 8 workgroups apart, in blocks of 8 units (a
+// trailing partial block runs its units' chunks back to back): the chunks of one channel tile
+// share blockIdx.x mod 8 -- the XCD the dispatcher deals them to -- and run at the same time, so
+// the weight lines the first chunk reads from memory reach the other chunks from that XCD's L2.
+__device__ __forceinline__ bool interleaved_unit(int m_chunks, int units, int& mc, int& unit) {
+  const int id = blockIdx.x;
+  const int full = (units / 8) * 8;
+  if (id < full * m_chunks) {
+    const int blk = id / (8 * m_chunks), rem = id - blk * (8 * m_chunks);
+    mc = rem / 8;
+    unit = blk * 8 + rem % 8;
+    return true;
+  }
+  const int rem = id - full * m_chunks, tail = units - full;
+  if (tail <= 0 || rem >= tail * m_chunks) return false;
+  mc = rem / tail;
+  unit = full + rem % tail;
+  return true;
+}
 
 // Channel tile and split-K index of chunk-local unit `unit` (n_tiles tiles x splits).  The
 // splits of a tile are placed 8 units apart, in blocks of 8 tiles x splits units (the tiles of a

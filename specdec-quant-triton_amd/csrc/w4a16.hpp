@@ -239,10 +239,17 @@ __device__ __forceinline__ void w4_store4(const W4A16Params& p, int m, int n, v4
   }
 }
 
-// Workgroup -> (M-chunk, channel tile, split); false for padding workgroups (chunked_unit).
+// Workgroup -> (M-chunk, channel tile, split); false for padding workgroups.
 __device__ __forceinline__ bool w4_decode_id(const W4A16Params& p, int& mc, int& tile, int& split) {
   int unit;
-  if (!chunked_unit(p.m_chunks, p.units, mc, unit)) return false;
+  // Eager launches run the M-chunks of a channel tile together on one XCD (W4A16 at M = 288:
+  // q|k|v 43.1 -> 39.0 us, gate|up 92.0 -> 89.6; M = 200 gate|up 69.9 -> 66.4); plan mode keeps
+  // the chunks in order so those past the active M are the last dispatched and exit at once.
+  if (p.plan == nullptr && p.m_chunks > 1) {
+    if (!interleaved_unit(p.m_chunks, p.units, mc, unit)) return false;
+  } else if (!chunked_unit(p.m_chunks, p.units, mc, unit)) {
+    return false;
+  }
   split_decode(unit, p.n_tiles, p.splits, tile, split);
   return true;
 }
