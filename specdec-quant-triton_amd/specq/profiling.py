@@ -826,6 +826,7 @@ def staircase(args) -> int:
                 t = round(min(_graph_us(run, copies, reps=3) for _ in range(2 if bm is None and M not in bounds else 3)), 2)
                 timed[key] = t
                 row.setdefault(str(bm or "auto"), {})[M] = t
+            print(f"[staircase] {N}x{Kd} BLOCK_M={bm or 'auto'} done", flush=True)
         res[f"{N}x{Kd}"] = row
         print(f"[staircase] {'w4a16' if w4 else 'w8a8'} {N}x{Kd} done", flush=True)
         del ws
