@@ -895,7 +895,8 @@ def tune(args) -> int:
             # A grouped W4A16 launch runs its members' common split count: resolve tiles with it.
             gsk = K.w4a16_group_split([N for N, _ in members], Kd) if w4 else 0
             table = {}
-            for r in range(0, 20):
+            lo_step, hi_step = (int(x) for x in getattr(args, "steps", "0-19").split("-"))
+            for r in range(lo_step, hi_step + 1):
                 # Step 0 is M = 1..8, step 1 M = 9..16, step r >= 2 the 16 rows up to 16 r.  Every
                 # M of a step runs its tile: time the candidates at both ends of the step and rank
                 # them by the mean.
@@ -1062,6 +1063,7 @@ def main() -> int:
     sm.add_argument("json")
     tu = sub.add_parser("tune")
     tu.add_argument("--kinds", default="w8a8,w4a16")
+    tu.add_argument("--steps", default="0-19", help="steps of M to tune, lo-hi (step r >= 2: M up to 16 r)")
     tu.add_argument("--out", required=True)
     te = sub.add_parser("tune-emit")
     te.add_argument("json")
